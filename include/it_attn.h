@@ -1,0 +1,142 @@
+/* irontimber-mi355x: C ABI of the attention / Gated-DeltaNet hot path, hand-written HIP for gfx950.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer argument is a device pointer unless its comment says otherwise. The caller owns
+ *     every buffer (inputs, outputs, KV cache, recurrent state, scratch); the library allocates and
+ *     frees nothing. (The reference's Vulkan backend follows the same rule with one caller-owned
+ *     arena: src/vk/mod.rs:2-6, 544-566.)
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Calls only enqueue work; they
+ *     do not synchronise.
+ *   - Return 0 on success. A nonzero return means nothing was enqueued (geometry, alignment or
+ *     scratch validation failed on the host) or a launch failed; it_last_error() then returns a
+ *     thread-local message. This mirrors the reference's Result<(), String> validation before any
+ *     device work (src/vk/mod.rs:179-220).
+ *   - Strides are counted in elements of the pointed-to type.
+ *   - Calls on one stream from one thread, like the reference's !Sync Ctx (src/vk/mod.rs:235-240).
+ */
+#ifndef IT_ATTN_H
+#define IT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Thread-local text of the last error (empty string if none). */
+const char* it_last_error(void);
+
+/* ABI version: bumped whenever a signature or a buffer layout below changes. */
+int it_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------------
+ * Softmax attention over an f16 KV cache (decode, MTP verify, chunked and whole-prompt prefill).
+ * ---------------------------------------------------------------------------------------------- */
+
+/* Append nt new K and V rows (f32, already RMS-normed and roped) to the f16 cache at rows
+ * pos0..pos0+nt-1. Source row t is k[t*src_tok_stride + i], i < kvd. Cache row p is kc[p*kvd + i].
+ * round_mode 0 = round to nearest even (the half crate's f16::from_f32 used by cpu.rs:22),
+ * 1 = round toward zero (packHalf2x16 on the reference's HAWAII GPU, src/vk/r012_parity.rs:14-18).
+ * Replaces the pair of kv_pack dispatches, src/vk/mod.rs:832-838 (kernel kernels/src/lib.rs:743-750). */
+int it_kv_append_f16(const float* k, const float* v, int src_tok_stride, uint16_t* kc, uint16_t* vc,
+                     int pos0, int nt, int kvd, int round_mode, void* stream);
+
+/* Bytes of scratch it_attn_f16 needs for this call geometry (0 if the chosen kernel needs none). */
+size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv);
+
+/* Causal GQA attention with sigmoid output gate, f32 accumulation.
+ *   q    : f32. Token t, q-head h: q[t*q_tok_stride + h*2*hd + d] for d < hd is the (normed, roped)
+ *          query and d in [hd, 2hd) the output gate (the reference's q row, cpu.rs:249-254).
+ *   kc,vc: f16 cache [pos][kvd], kvd = nkv*hd; KV head kh at column kh*hd. Rows 0..pos0+nt-1 must
+ *          be written (append first with it_kv_append_f16).
+ *   Token t attends keys 0..pos0+t (n = pos0+t+1, cpu.rs:260; kernels/src/lib.rs:764); q-head h
+ *   reads KV head h/(nh/nkv) (cpu.rs:265).
+ *   out  : f32 out[t*out_tok_stride + h*hd + d] = softmax(scale*q.K) V * sigmoid(gate).
+ *   scratch: device buffer of at least it_attn_scratch_bytes(...) bytes (may be NULL if that is 0).
+ * Requires hd == 256, nh % nkv == 0, q_tok_stride and out_tok_stride multiples of 4, 16-byte
+ * aligned q/out/kc/vc (the reference asserts the same f16 layout, src/vk/mod.rs:713).
+ * Replaces VkEngine::attention_kv(qo,qts,kco,vco,kvd,pos0,hd,nh,nkv,oo,nt,f16=true),
+ * src/vk/mod.rs:710-729, i.e. the split-K partial dispatch plus attn_comb. One entry point covers
+ * decode (nt=1), MTP verify (nt<=4), chunked prefill (nt=64, pos0>0) and whole-prompt prefill. */
+int it_attn_f16(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,
+                int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
+                void* scratch, size_t scratch_bytes, void* stream);
+
+/* it_attn_f16 with the kernel choice exposed (the reference's BONSAI_PREFILL_ATTN / chunk policy,
+ * src/vk/mod.rs:714-717 and 192-204):
+ *   kernel 0 = automatic (what it_attn_f16 does), 1 = split-K partials + combine,
+ *          2 = flash prefill (one pass, no scratch; needs nt >= 16).
+ *   chunk  = keys per split for kernel 1 (multiple of 64), 0 = automatic.
+ * it_attn_scratch_bytes_ex gives the scratch for the same choice. */
+size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int kernel, int chunk);
+int it_attn_f16_ex(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,
+                   int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
+                   void* scratch, size_t scratch_bytes, int kernel, int chunk, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Gated DeltaNet: short causal conv, q/k L2 norm, gated-delta recurrence.
+ * ---------------------------------------------------------------------------------------------- */
+
+/* Depthwise causal conv (kernel K in 2..4) + SiLU over nt tokens, carrying the rolling (K-1)-token
+ * state (oldest first) across calls.
+ *   x     : f32 x[t*x_tok_stride + ch], ch < cd (the qkv projection output)
+ *   w     : f32 w[ch*K + i]             (ssm_conv1d.weight)
+ *   state : f32 state[i*cd + ch], i < K-1, updated in place to the last K-1 inputs
+ *   out   : f32 out[t*out_tok_stride + ch]  (must not alias x or state)
+ * Replaces the conv dispatch, src/vk/mod.rs:803 (kernel kernels/src/lib.rs:119-140; CPU
+ * cpu.rs:201-212). */
+int it_gdn_conv(const float* x, int x_tok_stride, const float* w, float* state, float* out,
+                int out_tok_stride, int cd, int nt, int K, void* stream);
+
+/* In-place L2 normalisation x / max(||x||, eps) of nheads consecutive rows of length d per token:
+ * row r of token t is x[t*tok_stride + r*d ...]. d must be 128 or 256.
+ * Replaces rmsnorm mode 2 on the 2*nk q/k heads, src/vk/mod.rs:804 (kernels/src/lib.rs:207-229;
+ * cpu.rs:214). */
+int it_l2norm_heads(float* x, int tok_stride, int nheads, int d, int nt, float eps, void* stream);
+
+/* Gated-delta recurrence, token by token, for nt tokens (decode: nt=1).
+ *   co    : f32 normalised conv output, token t at co[t*co_tok_stride]: q heads [0, nk*S),
+ *           k heads [nk*S, 2*nk*S), v heads [2*nk*S, 2*nk*S + nv*S). V head h uses q/k head h % nk.
+ *   beta_raw, alpha_raw: f32 [t*ba_tok_stride + h]; beta = sigmoid(beta_raw),
+ *           g = softplus(alpha_raw + dt[h]) * a[h] (a < 0 is the decay rate), S <- exp(g) S.
+ *   dt, a : f32 [nv]
+ *   state : f32 [nv][S][S], element [h][i][j] = S_h[i][j], i = key index, j = value index
+ *           (the GPU arena layout of shaders/gdn.comp:2), updated in place.
+ *   out   : f32 out[t*out_tok_stride + h*S + j] = (S_h^T q)_j / sqrt(S)
+ * Requires S == 128, nv % nk == 0.
+ * Replaces the gdn / gdn_p dispatches, src/vk/mod.rs:805-806 and the per-token MTP-verify loop
+ * 797-801 (kernels/src/lib.rs:252-331; CPU cpu.rs:216-232). */
+int it_gdn_step(const float* co, int co_tok_stride, const float* beta_raw, const float* alpha_raw,
+                int ba_tok_stride, const float* dt, const float* a, float* state, float* out,
+                int out_tok_stride, int nt, int nv, int nk, int S, void* stream);
+
+/* Same contract and result as it_gdn_step over nt tokens, computed with the chunk-64 WY/UT form of
+ * the gated delta rule on f16 MFMA with f32 state and accumulation (a new algorithm: the reference
+ * runs the recurrence token-sequentially, kernels/src/lib.rs:285-331). Scratch as returned by
+ * it_gdn_chunked_scratch_bytes. */
+size_t it_gdn_chunked_scratch_bytes(int nt, int nv, int S);
+int it_gdn_chunked(const float* co, int co_tok_stride, const float* beta_raw, const float* alpha_raw,
+                   int ba_tok_stride, const float* dt, const float* a, float* state, float* out,
+                   int out_tok_stride, int nt, int nv, int nk, int S, void* scratch,
+                   size_t scratch_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Reference-shaped dispatch policy (pure host functions, no device access).
+ * ---------------------------------------------------------------------------------------------- */
+
+/* 64*heads*max(ctx,260): split-K partial words reserved per layer arena (src/vk/mod.rs:138). */
+size_t it_attention_scratch_words(size_t ctx, size_t heads);
+/* ceil(nt/64)*64*heads*max(ctx,260), nt in 1..=512 (src/vk/mod.rs:148-150); 0 if nt is invalid. */
+size_t it_attention_dispatch_room(size_t ctx, size_t heads, size_t nt);
+/* Keys per split the reference would choose: 64 doubled (at most to 1024) until
+ * nt*nh*ceil((pos0+nt)/C)*260 <= room (src/vk/mod.rs:714-716); -1 if even 1024 does not fit. */
+int it_attention_chunk(uint32_t nt, uint32_t nh, uint32_t pos0, size_t room);
+/* Geometry check of src/vk/mod.rs:207-220 restricted to the attention/GDN fields; 0 = supported. */
+int it_validate_geometry(int ctx_len, int head_dim, int n_head, int n_head_kv, int ssm_state,
+                         int ssm_groups, int ssm_vheads, int ssm_inner, int conv_k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IT_ATTN_H */

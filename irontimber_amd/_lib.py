@@ -1,0 +1,65 @@
+"""ctypes binding of libit_attn.so, the C ABI declared in include/it_attn.h.
+
+The library is the only compute path: if it is missing, loading raises instead of falling back.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_float, c_int, c_size_t, c_uint32, c_void_p, c_char_p
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libit_attn.so")
+
+# name -> (restype, argtypes); pointers travel as c_void_p (device addresses as ints).
+P = c_void_p
+SIGNATURES = {
+    "it_last_error": (c_char_p, []),
+    "it_abi_version": (c_int, []),
+    "it_kv_append_f16": (c_int, [P, P, c_int, P, P, c_int, c_int, c_int, c_int, P]),
+    "it_attn_scratch_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "it_attn_f16": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P, c_size_t, P]),
+    "it_attn_scratch_bytes_ex": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "it_attn_f16_ex": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P, c_size_t,
+                               c_int, c_int, P]),
+    "it_gdn_conv": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "it_l2norm_heads": (c_int, [P, c_int, c_int, c_int, c_int, c_float, P]),
+    "it_gdn_step": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
+    "it_gdn_chunked_scratch_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "it_gdn_chunked": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_size_t, P]),
+    "it_attention_scratch_words": (c_size_t, [c_size_t, c_size_t]),
+    "it_attention_dispatch_room": (c_size_t, [c_size_t, c_size_t, c_size_t]),
+    "it_attention_chunk": (c_int, [c_uint32, c_uint32, c_uint32, c_size_t]),
+    "it_validate_geometry": (c_int, [c_int] * 9),
+}
+
+
+class ItError(RuntimeError):
+    """A nonzero return from the C ABI, carrying it_last_error()."""
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ItError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C irontimber_amd/csrc)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().it_last_error().decode()
+
+
+def call(name: str, *args) -> int:
+    """Call an int-returning entry point; raise ItError with the library's message on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise ItError(f"{name}: {last_error()}")
+    return rc

@@ -1,0 +1,209 @@
+// C ABI of the hot path (declared in include/it_attn.h): host-side validation, dispatch policy and
+// kernel launches. Validation runs before any device work, like the reference's fail-closed
+// checks (src/vk/mod.rs:179-220); runtime errors come back as nonzero codes with a thread-local
+// message instead of the reference's panics.
+#include <string>
+#include <cstdio>
+#include <cstdarg>
+#include "../../include/it_attn.h"
+#include "internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return -1;
+}
+int check(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail("%s: %s", what, hipGetErrorString(e));
+    g_err.clear();
+    return 0;
+}
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+constexpr int HD = 256;
+constexpr size_t PART_WORDS = 260;
+constexpr int KERNEL_AUTO = 0, KERNEL_SPLITK = 1, KERNEL_FLASH = 2;
+constexpr size_t AUTO_SCRATCH_CAP = size_t(256) << 20;   // keep automatic split-K scratch under 256 MiB
+
+// Keys per split for the split-K kernel when the caller leaves it to us.
+int auto_chunk(int pos0, int nt, int nh) {
+    const size_t total = (size_t)pos0 + nt;
+    int c = 64;
+    while (c < (1 << 20) && (size_t)nt * nh * ((total + c - 1) / c) * PART_WORDS * 4 > AUTO_SCRATCH_CAP) c *= 2;
+    return c;
+}
+int auto_kernel(int nt) { (void)nt; return KERNEL_SPLITK; }
+
+size_t splitk_scratch(int pos0, int nt, int nh, int chunk) {
+    const size_t smax = ((size_t)pos0 + nt + chunk - 1) / chunk;
+    return (size_t)nt * nh * smax * PART_WORDS * sizeof(float);
+}
+
+int validate_attn(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
+                  int nkv, int nt, const float* out, int ots) {
+    if (hd != HD) return fail("it_attn_f16: head_dim %d unsupported (the f16 KV path requires 256)", hd);
+    if (nh <= 0 || nkv <= 0 || nh % nkv != 0) return fail("it_attn_f16: n_head %d / n_head_kv %d invalid", nh, nkv);
+    if (kvd != nkv * hd) return fail("it_attn_f16: kvd %d != n_head_kv*head_dim %d", kvd, nkv * hd);
+    if (nt <= 0 || pos0 < 0) return fail("it_attn_f16: nt %d / pos0 %d invalid", nt, pos0);
+    if ((long)pos0 + nt > (1L << 22)) return fail("it_attn_f16: context %ld too long", (long)pos0 + nt);
+    if (!q || !kc || !vc || !out) return fail("it_attn_f16: null buffer");
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out))
+        return fail("it_attn_f16: q/kc/vc/out must be 16-byte aligned");
+    if (qts % 4 != 0 || ots % 4 != 0) return fail("it_attn_f16: token strides must be multiples of 4");
+    if (nt > 1 && (qts < 2 * nh * hd || ots < nh * hd)) return fail("it_attn_f16: token strides overlap rows");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* it_last_error(void) { return g_err.c_str(); }
+int it_abi_version(void) { return 1; }
+
+int it_kv_append_f16(const float* k, const float* v, int src_tok_stride, uint16_t* kc, uint16_t* vc, int pos0, int nt,
+                     int kvd, int round_mode, void* stream) {
+    if (nt < 0 || pos0 < 0 || kvd <= 0 || kvd % 4 != 0) return fail("it_kv_append_f16: bad geometry nt=%d pos0=%d kvd=%d", nt, pos0, kvd);
+    if (round_mode != 0 && round_mode != 1) return fail("it_kv_append_f16: round_mode must be 0 (RNE) or 1 (RTZ)");
+    if (nt > 1 && src_tok_stride < kvd) return fail("it_kv_append_f16: source stride %d < kvd %d", src_tok_stride, kvd);
+    if (src_tok_stride % 4 != 0) return fail("it_kv_append_f16: source stride must be a multiple of 4");
+    if (!k || !v || !kc || !vc || !aligned16(k) || !aligned16(v) || !aligned16(kc) || !aligned16(vc))
+        return fail("it_kv_append_f16: buffers must be non-null and 16-byte aligned");
+    return check(it::launch_kv_append(k, v, src_tok_stride, kc, vc, pos0, nt, kvd, round_mode, (hipStream_t)stream),
+                 "it_kv_append_f16");
+}
+
+size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int kernel, int chunk) {
+    (void)hd; (void)nkv;
+    if (nt <= 0 || pos0 < 0 || nh <= 0) return 0;
+    if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
+    if (kernel == KERNEL_FLASH) return 0;
+    if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh);
+    return splitk_scratch(pos0, nt, nh, chunk);
+}
+size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv) {
+    return it_attn_scratch_bytes_ex(pos0, nt, hd, nh, nkv, KERNEL_AUTO, 0);
+}
+
+int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
+                   int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes, int kernel,
+                   int chunk, void* stream) {
+    if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, out, ots)) return -1;
+    if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
+    hipStream_t st = (hipStream_t)stream;
+    if (kernel == KERNEL_FLASH) {
+        if (nt < 16) return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
+        return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st), "it_attn_f16 (flash)");
+    }
+    if (kernel != KERNEL_SPLITK) return fail("it_attn_f16: unknown kernel %d", kernel);
+    if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh);
+    if (chunk % 64 != 0) return fail("it_attn_f16: chunk %d must be a multiple of 64", chunk);
+    const size_t need = splitk_scratch(pos0, nt, nh, chunk);
+    if (scratch_bytes < need || (need && !scratch))
+        return fail("it_attn_f16: scratch of %zu bytes < %zu required (it_attn_scratch_bytes)", scratch_bytes, need);
+    if (!aligned16(scratch)) return fail("it_attn_f16: scratch must be 16-byte aligned");
+    return check(it::launch_attn_splitk(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, (float*)scratch, chunk, st),
+                 "it_attn_f16 (split-K)");
+}
+
+int it_attn_f16(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
+                int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes, void* stream) {
+    return it_attn_f16_ex(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, ots, scratch, scratch_bytes,
+                          KERNEL_AUTO, 0, stream);
+}
+
+int it_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt, int K,
+                void* stream) {
+    if (K < 2 || K > 4) return fail("it_gdn_conv: kernel size %d unsupported (2..4)", K);
+    if (cd <= 0 || nt < 0) return fail("it_gdn_conv: bad geometry cd=%d nt=%d", cd, nt);
+    if (nt > 1 && (xts < cd || ots < cd)) return fail("it_gdn_conv: token strides smaller than cd");
+    if (!x || !w || !state || !out) return fail("it_gdn_conv: null buffer");
+    if (nt == 0) { g_err.clear(); return 0; }
+    return check(it::launch_gdn_conv(x, xts, w, state, out, ots, cd, nt, K, (hipStream_t)stream), "it_gdn_conv");
+}
+
+int it_l2norm_heads(float* x, int ts, int nheads, int d, int nt, float eps, void* stream) {
+    if (d != 128 && d != 256) return fail("it_l2norm_heads: row length %d unsupported (128 or 256)", d);
+    if (nheads <= 0 || nt < 0) return fail("it_l2norm_heads: bad geometry");
+    if (nt > 1 && ts < nheads * d) return fail("it_l2norm_heads: token stride overlaps rows");
+    if (!x) return fail("it_l2norm_heads: null buffer");
+    if (nt == 0) { g_err.clear(); return 0; }
+    return check(it::launch_l2norm(x, ts, nheads, d, nt, eps, (hipStream_t)stream), "it_l2norm_heads");
+}
+
+static int validate_gdn(const char* who, const float* co, int cts, const float* br, const float* ar, int bts,
+                        const float* dt, const float* a, const float* state, const float* out, int ots, int nt, int nv,
+                        int nk, int S) {
+    if (S != 128) return fail("%s: state size %d unsupported (128)", who, S);
+    if (nv <= 0 || nk <= 0 || nv % nk != 0) return fail("%s: nv %d / nk %d invalid", who, nv, nk);
+    if (nt < 0) return fail("%s: nt %d invalid", who, nt);
+    if (!co || !br || !ar || !dt || !a || !state || !out) return fail("%s: null buffer", who);
+    if (!aligned16(co) || !aligned16(state) || !aligned16(out)) return fail("%s: co/state/out must be 16-byte aligned", who);
+    if (cts % 4 != 0 || ots % 4 != 0) return fail("%s: token strides must be multiples of 4", who);
+    if (nt > 1 && (cts < (2 * nk + nv) * S || ots < nv * S || bts < nv)) return fail("%s: token strides overlap rows", who);
+    return 0;
+}
+
+int it_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt, const float* a,
+                float* state, float* out, int ots, int nt, int nv, int nk, int S, void* stream) {
+    if (validate_gdn("it_gdn_step", co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, S)) return -1;
+    if (nt == 0) { g_err.clear(); return 0; }
+    return check(it::launch_gdn_step(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, (hipStream_t)stream),
+                 "it_gdn_step");
+}
+
+size_t it_gdn_chunked_scratch_bytes(int nt, int nv, int S) {
+    if (nt <= 0 || nv <= 0 || S != 128) return 0;
+    return it::gdn_chunked_scratch_bytes(nt, nv, S);
+}
+
+int it_gdn_chunked(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt, const float* a,
+                   float* state, float* out, int ots, int nt, int nv, int nk, int S, void* scratch, size_t scratch_bytes,
+                   void* stream) {
+    if (validate_gdn("it_gdn_chunked", co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, S)) return -1;
+    if (nt == 0) { g_err.clear(); return 0; }
+    const size_t need = it::gdn_chunked_scratch_bytes(nt, nv, S);
+    if (scratch_bytes < need || (need && !scratch))
+        return fail("it_gdn_chunked: scratch of %zu bytes < %zu required", scratch_bytes, need);
+    if (!aligned16(scratch)) return fail("it_gdn_chunked: scratch must be 16-byte aligned");
+    return check(it::launch_gdn_chunked(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, scratch,
+                                        (hipStream_t)stream),
+                 "it_gdn_chunked");
+}
+
+// ---- reference-shaped policy (src/vk/mod.rs:130-220) -------------------------------------------
+size_t it_attention_scratch_words(size_t ctx, size_t heads) { return 64 * heads * (ctx > 260 ? ctx : 260); }
+
+size_t it_attention_dispatch_room(size_t ctx, size_t heads, size_t nt) {
+    if (nt == 0 || nt > 512) return 0;
+    return (nt + 63) / 64 * 64 * heads * (ctx > 260 ? ctx : 260);
+}
+
+int it_attention_chunk(uint32_t nt, uint32_t nh, uint32_t pos0, size_t room) {
+    const uint64_t total = (uint64_t)pos0 + nt;
+    uint64_t c = 64;
+    while (c < 1024 && (uint64_t)nt * nh * ((total + c - 1) / c) * 260 > room) c *= 2;
+    if ((uint64_t)nt * nh * ((total + c - 1) / c) * 260 > room) return -1;
+    return (int)c;
+}
+
+int it_validate_geometry(int ctx_len, int head_dim, int n_head, int n_head_kv, int ssm_state, int ssm_groups,
+                         int ssm_vheads, int ssm_inner, int conv_k) {
+    if (ctx_len <= 0 || ctx_len > 8192) return fail("supported context capacity is 1..=8192");
+    if (head_dim != 256 || n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0 || ssm_state != 128 ||
+        ssm_groups <= 0 || ssm_vheads <= 0 || ssm_vheads % ssm_groups != 0 || ssm_inner != ssm_vheads * ssm_state ||
+        ssm_inner % 1024 != 0 || conv_k < 2 || conv_k > 4)
+        return fail("unsupported kernel geometry");
+    g_err.clear();
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,50 @@
+// Shared device helpers for the gfx950 kernels of this library.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace it {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// D = A(16x32) * B(32x16) + C on the matrix cores, f16 inputs, f32 accumulate (gfx950).
+// Lane l holds A row (l & 15) and B column (l & 15), each with 8 consecutive k values of the
+// lane's k-group (l >> 4); D element i of lane l is row 4*(l >> 4) + i, column l & 15.
+__device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// D = A(32x16) * B(16x32) + C; lane l holds A row / B column (l & 31) with 8 k values of k-group
+// (l >> 5); D element i of lane l is row 8*(i/4) + 4*(l >> 5) + (i & 3), column l & 31.
+__device__ __forceinline__ f16v mfma32x32x16(h8 a, h8 b, f16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h8 ld_h8(const void* p) { return __builtin_bit_cast(h8, *(const u4*)p); }
+__device__ __forceinline__ f4 ld_f4(const float* p) { return *(const f4*)p; }
+
+// Split 8 f32 values into f16 hi + f16 lo with hi + lo == x to ~2^-22 relative: two MFMAs with
+// the halves reproduce an f32-accurate dot product against exact f16 operands.
+__device__ __forceinline__ void split_hi_lo(f4 x0, f4 x1, h8& hi, h8& lo) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        _Float16 a = (_Float16)x0[j], b = (_Float16)x1[j];
+        hi[j] = a; hi[j + 4] = b;
+        lo[j] = (_Float16)(x0[j] - (float)a); lo[j + 4] = (_Float16)(x1[j] - (float)b);
+    }
+}
+__device__ __forceinline__ h8 to_h8(f4 x0, f4 x1) {
+    h8 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { r[j] = (_Float16)x0[j]; r[j + 4] = (_Float16)x1[j]; }
+    return r;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+
+}  // namespace it

@@ -1,0 +1,166 @@
+// Gated DeltaNet for gfx950: depthwise causal conv + SiLU, per-head L2 norm, and the gated-delta
+// recurrence for decode / short token runs with the state held in registers.
+//
+// Reference behaviour: src/cpu.rs:201-232 (math), kernels/src/lib.rs:119-140 (conv),
+// 207-229 (rmsnorm mode 2), 252-331 (gdn, gdn_p).
+#include "common.h"
+#include "internal.h"
+
+namespace it {
+
+// ------------------------------------------------------------------------------------------------
+// Conv: thread per (channel, run of TT tokens). The K-1 inputs before the run come from x or, for
+// tokens before 0, from the carried state (oldest first). With one run (grid.y == 1) the same
+// thread also writes the new state; otherwise gdn_conv_state_kernel does it after this kernel.
+template <int K>
+__global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__ x, int xts, const float* __restrict__ w,
+                                                       float* __restrict__ state, float* __restrict__ out, int ots,
+                                                       int cd, int nt, int TT) {
+    const int ch = blockIdx.x * 256 + threadIdx.x;
+    if (ch >= cd) return;
+    const int t0 = blockIdx.y * TT, t1 = min(nt, t0 + TT);
+    float wt[K], win[K - 1];
+#pragma unroll
+    for (int i = 0; i < K; ++i) wt[i] = w[(size_t)ch * K + i];
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) {
+        const int tt = t0 - (K - 1) + i;
+        win[i] = tt >= 0 ? x[(size_t)tt * xts + ch] : state[(size_t)(tt + K - 1) * cd + ch];
+    }
+    for (int t = t0; t < t1; ++t) {
+        const float xv = x[(size_t)t * xts + ch];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i) s += win[i] * wt[i];
+        s += xv * wt[K - 1];
+        out[(size_t)t * ots + ch] = siluf_(s);
+#pragma unroll
+        for (int i = 0; i + 1 < K - 1; ++i) win[i] = win[i + 1];
+        win[K - 2] = xv;
+    }
+    if (gridDim.y == 1) {
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i) state[(size_t)i * cd + ch] = win[i];
+    }
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __restrict__ x, int xts, float* __restrict__ state,
+                                                             int cd, int nt) {
+    const int ch = blockIdx.x * 256 + threadIdx.x;
+    if (ch >= cd) return;
+    float nv[K - 1];
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) {
+        const int tt = nt - (K - 1) + i;
+        nv[i] = tt >= 0 ? x[(size_t)tt * xts + ch] : state[(size_t)(tt + K - 1) * cd + ch];
+    }
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) state[(size_t)i * cd + ch] = nv[i];
+}
+
+// ------------------------------------------------------------------------------------------------
+// L2 norm of rows of D floats, one wave per row, in place: x / max(||x||, eps).
+template <int D>
+__global__ __launch_bounds__(256) void l2norm_kernel(float* __restrict__ x, int ts, int nheads, int nt, float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (row >= nheads * nt) return;
+    const int t = row / nheads, r = row % nheads;
+    float* p = x + (size_t)t * ts + (size_t)r * D;
+    constexpr int PER = D / 64;
+    float v[PER];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) { v[i] = p[l + 64 * i]; ss += v[i] * v[i]; }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m);
+    const float sc = 1.0f / fmaxf(sqrtf(ss), eps);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) p[l + 64 * i] = v[i] * sc;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Gated-delta recurrence, S = 128, token-sequential with the state slice in registers.
+// Workgroup = (16-column block cb, V head h); thread = (column quad cg = tid & 3, row pair
+// rp = tid >> 2): it holds S[2rp..2rp+1][16cb+4cg .. +3]. Column sums over the 128 rows reduce
+// across lanes (xor 4..32) and then across the 4 waves through LDS.
+__global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__ co, int cts, const float* __restrict__ br,
+                                                       const float* __restrict__ ar, int bts, const float* __restrict__ dt,
+                                                       const float* __restrict__ A, float* __restrict__ state,
+                                                       float* __restrict__ out, int ots, int nt, int nv, int nk) {
+    constexpr int S = 128;
+    __shared__ f4 red1[4][4], red2[4][4];
+    const int cb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int cg = tid & 3, rp = tid >> 2;
+    const int kh = h % nk, qk = nk * S;
+    const int j0 = cb * 16 + 4 * cg, i0 = 2 * rp;
+    float* sb = state + (size_t)h * S * S;
+    f4 s0 = ld_f4(sb + (size_t)i0 * S + j0), s1 = ld_f4(sb + (size_t)(i0 + 1) * S + j0);
+    const float scale = 1.0f / sqrtf((float)S);
+    const float dth = dt[h], ah = A[h];
+    for (int t = 0; t < nt; ++t) {
+        const float* c = co + (size_t)t * cts;
+        const float q0 = c[kh * S + i0], q1 = c[kh * S + i0 + 1];
+        const float k0 = c[qk + kh * S + i0], k1 = c[qk + kh * S + i0 + 1];
+        const f4 v = ld_f4(c + 2 * qk + h * S + j0);
+        const float beta = sigmoidf_(br[(size_t)t * bts + h]);
+        const float eg = expf(softplusf_(ar[(size_t)t * bts + h] + dth) * ah);
+        s0 *= eg; s1 *= eg;
+        f4 p = s0 * k0 + s1 * k1;
+#pragma unroll
+        for (int m = 4; m < 64; m <<= 1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] += __shfl_xor(p[j], m);
+        if (l < 4) red1[w][l] = p;
+        __syncthreads();
+        const f4 sk = red1[0][cg] + red1[1][cg] + red1[2][cg] + red1[3][cg];
+        const f4 delta = (v - sk) * beta;
+        s0 += k0 * delta; s1 += k1 * delta;
+        f4 o = s0 * q0 + s1 * q1;
+#pragma unroll
+        for (int m = 4; m < 64; m <<= 1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] += __shfl_xor(o[j], m);
+        if (l < 4) red2[w][l] = o;
+        __syncthreads();
+        if (tid < 4) {
+            const f4 ot = (red2[0][cg] + red2[1][cg] + red2[2][cg] + red2[3][cg]) * scale;
+            *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = ot;
+        }
+    }
+    *(f4*)(sb + (size_t)i0 * S + j0) = s0;
+    *(f4*)(sb + (size_t)(i0 + 1) * S + j0) = s1;
+}
+
+// ------------------------------------------------------------------------------------------------
+hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,
+                           int K, hipStream_t st) {
+    const int TT = nt <= 16 ? nt : 16;
+    const dim3 grid((cd + 255) / 256, (nt + TT - 1) / TT);
+#define IT_CONV(KK)                                                                              \
+    gdn_conv_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT);           \
+    if (grid.y > 1) gdn_conv_state_kernel<KK><<<grid.x, 256, 0, st>>>(x, xts, state, cd, nt);
+    switch (K) {
+        case 2: IT_CONV(2) break;
+        case 3: IT_CONV(3) break;
+        default: IT_CONV(4) break;
+    }
+#undef IT_CONV
+    return hipGetLastError();
+}
+
+hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps, hipStream_t st) {
+    const int rows = nheads * nt;
+    const dim3 grid((rows + 3) / 4);
+    if (d == 128) l2norm_kernel<128><<<grid, 256, 0, st>>>(x, ts, nheads, nt, eps);
+    else l2norm_kernel<256><<<grid, 256, 0, st>>>(x, ts, nheads, nt, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+                           const float* a, float* state, float* out, int ots, int nt, int nv, int nk, hipStream_t st) {
+    gdn_step_kernel<<<dim3(8, nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk);
+    return hipGetLastError();
+}
+
+}  // namespace it

@@ -1,0 +1,28 @@
+// Launch functions shared between the kernel files and the C ABI layer (api.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace it {
+
+hipError_t launch_kv_append(const float* k, const float* v, int sts, uint16_t* kc, uint16_t* vc, int pos0, int nt,
+                            int kvd, int rtz, hipStream_t st);
+int attn_partial_rows_per_group(int nt, int G);
+hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
+                              int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
+                              hipStream_t st);
+hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
+                             int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st);
+
+hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,
+                           int K, hipStream_t st);
+hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps, hipStream_t st);
+hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+                           const float* a, float* state, float* out, int ots, int nt, int nv, int nk, hipStream_t st);
+size_t gdn_chunked_scratch_bytes(int nt, int nv, int S);
+hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+                              const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
+                              hipStream_t st);
+
+}  // namespace it

@@ -1,0 +1,116 @@
+"""Torch-tensor front end over the C ABI (device memory and streams come from PyTorch-ROCm).
+
+Each function validates dtypes/devices/contiguity, then calls the matching `it_*` entry point on
+torch's current stream. Buffer layouts and semantics are those of include/it_attn.h.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import call, lib
+
+KERNEL_AUTO, KERNEL_SPLITK, KERNEL_FLASH = 0, 1, 2
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, dtype: torch.dtype, name: str):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def kv_append_f16(k: torch.Tensor, v: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int,
+                  round_mode: int = 0) -> None:
+    """Append k, v [nt, kvd] f32 to the f16 caches kc, vc [ctx, kvd] (stored as int16 bits or f16)."""
+    _need(k, torch.float32, "k"); _need(v, torch.float32, "v")
+    nt, kvd = k.shape
+    for c in (kc, vc):
+        if c.dtype not in (torch.float16, torch.int16) or not c.is_contiguous() or c.shape[-1] != kvd:
+            raise ValueError("kc/vc must be contiguous [ctx, kvd] f16")
+        if c.shape[0] < pos0 + nt:
+            raise ValueError("cache too short")
+    call("it_kv_append_f16", k.data_ptr(), v.data_ptr(), kvd, kc.data_ptr(), vc.data_ptr(), pos0, nt, kvd,
+         round_mode, _stream())
+
+
+def attn_scratch_bytes(pos0: int, nt: int, nh: int, nkv: int, hd: int = 256, kernel: int = KERNEL_AUTO,
+                       chunk: int = 0) -> int:
+    return lib().it_attn_scratch_bytes_ex(pos0, nt, hd, nh, nkv, kernel, chunk)
+
+
+def attn_f16(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int, nh: int, nkv: int,
+             scale: float | None = None, out: torch.Tensor | None = None, scratch: torch.Tensor | None = None,
+             kernel: int = KERNEL_AUTO, chunk: int = 0) -> torch.Tensor:
+    """q [nt, nh*2*hd] f32 (q | gate per head), kc/vc [ctx, nkv*hd] f16 -> out [nt, nh*hd] f32."""
+    _need(q, torch.float32, "q")
+    nt = q.shape[0]
+    hd = q.shape[-1] // (2 * nh) if q.dim() == 2 else q.shape[-1] // 2
+    kvd = nkv * hd
+    if scale is None:
+        scale = 1.0 / hd ** 0.5
+    for c in (kc, vc):
+        if c.dtype not in (torch.float16, torch.int16) or not c.is_contiguous() or c.shape[-1] != kvd:
+            raise ValueError("kc/vc must be contiguous [ctx, nkv*hd] f16")
+        if c.shape[0] < pos0 + nt:
+            raise ValueError("cache shorter than pos0 + nt")
+    if out is None:
+        out = torch.empty(nt, nh * hd, device=q.device, dtype=torch.float32)
+    _need(out, torch.float32, "out")
+    need = attn_scratch_bytes(pos0, nt, nh, nkv, hd, kernel, chunk)
+    if scratch is None and need:
+        scratch = torch.empty(need, device=q.device, dtype=torch.uint8)
+    nbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
+    call("it_attn_f16_ex", q.data_ptr(), nh * 2 * hd, kc.data_ptr(), vc.data_ptr(), kvd, pos0, hd, nh, nkv, nt,
+         float(scale), out.data_ptr(), nh * hd, _ptr(scratch), nbytes, kernel, chunk, _stream())
+    return out
+
+
+def gdn_conv(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [nt, cd] f32, w [cd, K], state [K-1, cd] (updated in place) -> silu(conv) [nt, cd]."""
+    _need(x, torch.float32, "x"); _need(w, torch.float32, "w"); _need(state, torch.float32, "state")
+    nt, cd = x.shape
+    K = w.shape[1]
+    if out is None:
+        out = torch.empty_like(x)
+    call("it_gdn_conv", x.data_ptr(), cd, w.data_ptr(), state.data_ptr(), out.data_ptr(), cd, cd, nt, K, _stream())
+    return out
+
+
+def l2norm_heads(x: torch.Tensor, nheads: int, d: int, eps: float = 1e-6) -> torch.Tensor:
+    """In place on the first nheads*d columns of each row of x [nt, C]."""
+    _need(x, torch.float32, "x")
+    call("it_l2norm_heads", x.data_ptr(), x.shape[1], nheads, d, x.shape[0], float(eps), _stream())
+    return x
+
+
+def gdn_step(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, out=None, chunked: bool = False,
+             scratch=None):
+    """co [nt, (2nk+nv)S], beta_raw/alpha_raw [nt, nv], dt/a [nv], state [nv, S, S] (in place)
+    -> out [nt, nv*S]. chunked=True uses the chunk-64 scan (it_gdn_chunked)."""
+    for t, n in ((co, "co"), (beta_raw, "beta_raw"), (alpha_raw, "alpha_raw"), (dt, "dt"), (a, "a"), (state, "state")):
+        _need(t, torch.float32, n)
+    nt = co.shape[0]
+    S = state.shape[-1]
+    if out is None:
+        out = torch.empty(nt, nv * S, device=co.device, dtype=torch.float32)
+    args = [co.data_ptr(), co.shape[1], beta_raw.data_ptr(), alpha_raw.data_ptr(), beta_raw.shape[1], dt.data_ptr(),
+            a.data_ptr(), state.data_ptr(), out.data_ptr(), out.shape[1], nt, nv, nk, S]
+    if chunked:
+        need = lib().it_gdn_chunked_scratch_bytes(nt, nv, S)
+        if scratch is None and need:
+            scratch = torch.empty(need, device=co.device, dtype=torch.uint8)
+        nbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
+        call("it_gdn_chunked", *args, _ptr(scratch), nbytes, _stream())
+    else:
+        call("it_gdn_step", *args, _stream())
+    return out

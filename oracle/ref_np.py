@@ -1,0 +1,107 @@
+"""TEST INFRASTRUCTURE ONLY: float64 references that pin the oracle (see oracle/__init__.py)."""
+from __future__ import annotations
+
+import numpy as np
+
+
+def f16_to_f64(bits: np.ndarray) -> np.ndarray:
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float64)
+
+
+def attn_f64(q: np.ndarray, kf: np.ndarray, vf: np.ndarray, pos0: int, nh: int, nkv: int, hd: int,
+             scale: float) -> np.ndarray:
+    """Softmax attention with sigmoid gate in float64, the known-answer oracle of
+    src/vk/r012_parity.rs:22-27. q [nt, nh*2*hd]; kf/vf [>= pos0+nt, nkv*hd] float64 key/value
+    values (already f16-rounded as the cache holds them). Token t sees n = pos0+t+1 keys."""
+    nt = q.shape[0]
+    q = q.reshape(nt, nh, 2 * hd).astype(np.float64)
+    g = nh // nkv
+    out = np.zeros((nt, nh, hd))
+    for t in range(nt):
+        n = pos0 + t + 1
+        for kh in range(nkv):
+            K = kf[:n, kh * hd:(kh + 1) * hd]
+            V = vf[:n, kh * hd:(kh + 1) * hd]
+            qs = q[t, kh * g:(kh + 1) * g, :hd]
+            s = qs @ K.T * scale
+            s -= s.max(axis=1, keepdims=True)
+            e = np.exp(s)
+            o = (e @ V) / e.sum(axis=1, keepdims=True)
+            gate = q[t, kh * g:(kh + 1) * g, hd:]
+            out[t, kh * g:(kh + 1) * g] = o / (1.0 + np.exp(-gate))
+    return out.reshape(nt, nh * hd)
+
+
+def _softplus(x):
+    return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+
+
+def gdn_decay_beta(beta_raw, alpha_raw, dt, a):
+    """beta = sigmoid(b), g = softplus(alpha + dt) * a (cpu.rs:222), float64 [nt, nv]."""
+    beta = 1.0 / (1.0 + np.exp(-np.asarray(beta_raw, np.float64)))
+    g = _softplus(np.asarray(alpha_raw, np.float64) + np.asarray(dt, np.float64)) * np.asarray(a, np.float64)
+    return beta, g
+
+
+def gdn_seq_f64(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int):
+    """Brute-force float64 gated-delta recurrence, written from the update rule itself:
+    S <- e^g S;  S <- S + beta k (v - S^T k)^T;  o = S^T q / sqrt(S).
+    state [nv, S, S] indexed [h][i = key][j = value]. Returns (out [nt, nv*S], state)."""
+    co = np.asarray(co, np.float64)
+    st = np.asarray(state, np.float64).copy()
+    nt = co.shape[0]
+    S = st.shape[-1]
+    qk = nk * S
+    beta, g = gdn_decay_beta(beta_raw, alpha_raw, dt, a)
+    out = np.zeros((nt, nv, S))
+    for t in range(nt):
+        for h in range(nv):
+            kh = h % nk
+            q = co[t, kh * S:(kh + 1) * S]
+            k = co[t, qk + kh * S:qk + (kh + 1) * S]
+            v = co[t, 2 * qk + h * S:2 * qk + (h + 1) * S]
+            M = st[h] * np.exp(g[t, h])
+            M = M + beta[t, h] * np.outer(k, v - M.T @ k)
+            st[h] = M
+            out[t, h] = M.T @ q / np.sqrt(S)
+    return out.reshape(nt, nv * S), st
+
+
+def gdn_chunked_f64(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, C: int = 64):
+    """Chunked (WY/UT) form of the same recurrence in float64. Per chunk of L <= C tokens with
+    in-chunk cumulative log-decay G (inclusive), D[t,s] = exp(G_t - G_s):
+        A  = strict_lower(D * K K^T)             T = (I + diag(beta) A)^-1 diag(beta)
+        W  = T diag(e^G) K                       U = T V - W S0
+        O  = (diag(e^G) Q S0 + lower_incl(D * Q K^T) U) / sqrt(S)
+        S1 = e^{G_L} S0 + (diag(e^{G_L - G}) K)^T U
+    Only decay differences G_t - G_s <= 0 (t >= s) are exponentiated, so nothing overflows."""
+    co = np.asarray(co, np.float64)
+    st = np.asarray(state, np.float64).copy()
+    nt = co.shape[0]
+    S = st.shape[-1]
+    qk = nk * S
+    beta, g = gdn_decay_beta(beta_raw, alpha_raw, dt, a)
+    out = np.zeros((nt, nv, S))
+    for h in range(nv):
+        kh = h % nk
+        Qa = co[:, kh * S:(kh + 1) * S]
+        Ka = co[:, qk + kh * S:qk + (kh + 1) * S]
+        Va = co[:, 2 * qk + h * S:2 * qk + (h + 1) * S]
+        S0 = st[h]
+        for c0 in range(0, nt, C):
+            c1 = min(nt, c0 + C)
+            Q, K, V = Qa[c0:c1], Ka[c0:c1], Va[c0:c1]
+            b = beta[c0:c1, h]
+            G = np.cumsum(g[c0:c1, h])
+            D = np.exp(np.minimum(G[:, None] - G[None, :], 0.0))
+            L = c1 - c0
+            A = np.tril(D * (K @ K.T), -1)
+            Minv = np.linalg.inv(np.eye(L) + b[:, None] * A)
+            T = Minv * b[None, :]
+            W = T @ (np.exp(G)[:, None] * K)
+            U = T @ V - W @ S0
+            O = np.exp(G)[:, None] * (Q @ S0) + np.tril(D * (Q @ K.T)) @ U
+            out[c0:c1, h] = O / np.sqrt(S)
+            S0 = np.exp(G[-1]) * S0 + (np.exp(G[-1] - G)[:, None] * K).T @ U
+        st[h] = S0
+    return out.reshape(nt, nv * S), st

@@ -1,0 +1,99 @@
+"""The C-ABI library loads, exports every symbol include/it_attn.h declares, and its host-side
+policy / validation behaves like the reference's (no device work in these tests)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from irontimber_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "it_attn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(it_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported_and_bound():
+    lib = _lib.lib()
+    syms = header_symbols()
+    assert len(syms) >= 15
+    for s in syms:
+        assert hasattr(lib, s), s
+        assert s in _lib.SIGNATURES, f"{s} missing from the ctypes binding"
+
+
+def test_abi_version():
+    assert _lib.lib().it_abi_version() == 1
+
+
+def test_scratch_words_and_room_match_reference():
+    """prefill_review.rs:18, 27: attention_scratch_words / attention_dispatch_room."""
+    lib = _lib.lib()
+    assert lib.it_attention_scratch_words(8192, 24) == 64 * 8192 * 24
+    assert lib.it_attention_scratch_words(16, 24) == 64 * 260 * 24
+    for nt in [1, 2, 22, 43, 64, 128, 256, 512]:
+        assert lib.it_attention_dispatch_room(8192, 24, nt) == (nt + 63) // 64 * 64 * 8192 * 24
+    assert lib.it_attention_dispatch_room(8192, 24, 0) == 0
+    assert lib.it_attention_dispatch_room(8192, 24, 513) == 0
+
+
+@pytest.mark.parametrize("ctx", [1, 16, 192, 256, 260, 8192])
+def test_chunk_policy_fits_room(ctx):
+    """prefill_review.rs:35-40: for nt = min(ctx,64) the chosen C keeps the partials in the room."""
+    lib = _lib.lib()
+    room = lib.it_attention_scratch_words(ctx, 24)
+    nt = min(ctx, 64)
+    c = lib.it_attention_chunk(nt, 24, ctx - nt, room)
+    assert c in (64, 128, 256, 512, 1024)
+    assert nt * 24 * ((ctx + c - 1) // c) * 260 <= room
+
+
+def test_chunk_policy_decode_is_64():
+    lib = _lib.lib()
+    room = lib.it_attention_dispatch_room(8192, 16, 1)
+    assert lib.it_attention_chunk(1, 16, 8191, room) == 64
+
+
+def test_validate_geometry():
+    """r012_review.rs:6-7: production geometry passes, each broken field fails, ctx 0/8193 fail."""
+    lib = _lib.lib()
+    ok = dict(ctx_len=8192, head_dim=256, n_head=16, n_head_kv=2, ssm_state=128, ssm_groups=16,
+              ssm_vheads=32, ssm_inner=4096, conv_k=4)
+    assert lib.it_validate_geometry(*ok.values()) == 0
+    for k, bad in [("head_dim", 128), ("n_head_kv", 0), ("conv_k", 5), ("ssm_state", 64), ("ssm_groups", 0),
+                   ("ctx_len", 0), ("ctx_len", 8193), ("n_head", 15), ("ssm_inner", 4000)]:
+        g = dict(ok, **{k: bad})
+        assert lib.it_validate_geometry(*g.values()) != 0, k
+        assert _lib.last_error()
+
+
+def test_attn_rejects_bad_geometry_before_device_work():
+    """Validation fails before any launch (the MUST_NOT_QUERY_DEVICE sentinels of prefill_review.rs:42)."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(1 << 20)   # never dereferenced: validation must fail first
+    rc = lib.it_attn_f16(fake, 512, fake, fake, 256, 0, 128, 1, 1, 1, 0.1, fake, 128, None, 0, None)
+    assert rc != 0 and "head_dim" in _lib.last_error()
+    rc = lib.it_attn_f16(fake, 8192, fake, fake, 512, 0, 256, 15, 2, 1, 0.1, fake, 4096, None, 0, None)
+    assert rc != 0 and "n_head" in _lib.last_error()
+    rc = lib.it_attn_f16_ex(fake, 8192, fake, fake, 512, 0, 256, 16, 2, 1, 0.1, fake, 4096, None, 0, 1, 64, None)
+    assert rc != 0 and "scratch" in _lib.last_error()
+    rc = lib.it_attn_f16_ex(fake, 8192, fake, fake, 512, 0, 256, 16, 2, 4, 0.1, fake, 4096, fake, 1 << 30, 2, 0, None)
+    assert rc != 0 and "nt >= 16" in _lib.last_error()
+    rc = lib.it_gdn_step(fake, 8192, fake, fake, 32, fake, fake, fake, fake, 4096, 1, 32, 16, 64, None)
+    assert rc != 0 and "state size" in _lib.last_error()
+    rc = lib.it_gdn_conv(fake, 8192, fake, fake, fake, 8192, 8192, 1, 5, None)
+    assert rc != 0 and "kernel size" in _lib.last_error()
+    rc = lib.it_kv_append_f16(fake, fake, 512, fake, fake, 0, 1, 512, 2, None)
+    assert rc != 0 and "round_mode" in _lib.last_error()
+
+
+def test_scratch_bytes_policy():
+    lib = _lib.lib()
+    # decode: split-K, C = 64 -> 128 splits of 260 words per head
+    assert lib.it_attn_scratch_bytes(8191, 1, 256, 16, 2) == 16 * 128 * 260 * 4
+    # whole-prompt prefill: flash, no scratch
+    assert lib.it_attn_scratch_bytes_ex(0, 8192, 256, 16, 2, 2, 0) == 0

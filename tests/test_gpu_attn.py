@@ -1,0 +1,98 @@
+"""GPU parity of the attention path (C ABI through irontimber_amd.ops) against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle.ref_np import attn_f64, f16_to_f64
+from irontimber_amd import ops
+from irontimber_amd.synth import attn_inputs, f16_bits, f16_bits_rtz
+from tests.gpu_util import announce, argmax_projection, dev_f16bits, dev_f32, host
+from tests.r012 import CASES, GEOMS, arena
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3   # max abs error on attention outputs
+
+
+def run_case(dev, seed, ctx, nt, nh=16, nkv=2, kernel=ops.KERNEL_AUTO, chunk=0):
+    pos0 = ctx - nt
+    q, kb, vb = attn_inputs(seed, ctx=ctx, nt=nt, nh=nh, nkv=nkv)
+    announce(f"attn seed={seed} ctx={ctx} nt={nt} nh={nh} nkv={nkv} kernel={kernel} chunk={chunk}")
+    out = ops.attn_f16(dev_f32(q.reshape(nt, -1), dev), dev_f16bits(kb, dev), dev_f16bits(vb, dev), pos0, nh, nkv,
+                       kernel=kernel, chunk=chunk)
+    got = host(out)
+    want = oracle.attn(q.reshape(nt, -1), kb, vb, pos0, nh, nkv)
+    return got, want
+
+
+@pytest.mark.parametrize("seed,ctx,nt", [(0, 512, 1), (1, 8192, 1), (1, 8192, 4), (2, 4096 + 64, 64)])
+def test_baseline_configs(dev, seed, ctx, nt):
+    got, want = run_case(dev, seed, ctx, nt)
+    err = np.abs(got - want).max()
+    print(f"max_abs={err:.3g}")
+    assert np.isfinite(got).all() and err <= TOL
+    assert (argmax_projection(got) == argmax_projection(want)).all()
+
+
+@pytest.mark.parametrize("ctx,nt,nh,nkv", [(1, 1, 16, 2), (65, 1, 16, 2), (100, 3, 16, 2), (64, 2, 24, 4),
+                                           (300, 5, 8, 8), (129, 7, 4, 1), (777, 33, 16, 2), (64, 64, 16, 2)])
+def test_ragged_and_group_shapes(dev, ctx, nt, nh, nkv):
+    got, want = run_case(dev, 21, ctx, nt, nh, nkv, kernel=ops.KERNEL_SPLITK)
+    assert np.abs(got - want).max() <= 1e-5
+
+
+@pytest.mark.parametrize("chunk", [64, 128, 256, 1024, 8192])
+def test_split_invariance(dev, chunk):
+    """The result does not depend on how the keys are split (invariant of the LSE merge)."""
+    got, want = run_case(dev, 3, 2000, 4, kernel=ops.KERNEL_SPLITK, chunk=chunk)
+    assert np.abs(got - want).max() <= 1e-5
+
+
+@pytest.mark.parametrize("nh,nkv,hd", GEOMS)
+@pytest.mark.parametrize("pos0,nt", CASES)
+def test_r012_known_answer(dev, pos0, nt, nh, nkv, hd):
+    """src/vk/r012_parity.rs:6-28 on the GPU path: RTZ KV append (bit-exact), then split-K attention
+    against the f64 softmax oracle at the reference's own bound, max_abs < 2e-6."""
+    announce(f"r012 pos0={pos0} nt={nt} nh={nh}")
+    q, k, v = arena(pos0, nt, nh, nkv, hd)
+    total = pos0 + nt
+    kc = torch.zeros(total, nkv * hd, dtype=torch.int16, device=dev)
+    vc = torch.zeros_like(kc)
+    for start in range(0, total, 64):       # append in <= 64-row pieces like r012_parity.rs:12
+        n = min(64, total - start)
+        ops.kv_append_f16(dev_f32(k[start:start + n], dev), dev_f32(v[start:start + n], dev), kc, vc, start,
+                          round_mode=1)
+    kb = host(kc).view(np.uint16)
+    np.testing.assert_array_equal(kb, f16_bits_rtz(k))
+    np.testing.assert_array_equal(host(vc).view(np.uint16), f16_bits_rtz(v))
+    kern = ops.KERNEL_SPLITK if nt < 16 else ops.KERNEL_AUTO
+    got = host(ops.attn_f16(dev_f32(q, dev), kc, vc, pos0, nh, nkv, scale=1.0 / 16, kernel=kern))
+    want = attn_f64(q, f16_to_f64(kb), f16_to_f64(host(vc).view(np.uint16)), pos0, nh, nkv, hd, 1.0 / 16)
+    err = np.abs(got - want).max()
+    print(f"r012 gpu max_abs={err:.3g}")
+    assert np.isfinite(got).all() and err < 2e-6
+
+
+def test_kv_append_rne_bits(dev):
+    rng = np.random.default_rng(0)
+    k = (rng.standard_normal((5, 512)) * 3).astype(np.float32)
+    v = (rng.standard_normal((5, 512)) * 1e-3).astype(np.float32)
+    kc = torch.full((9, 512), -1, dtype=torch.int16, device=dev)
+    vc = torch.full((9, 512), -1, dtype=torch.int16, device=dev)
+    ops.kv_append_f16(dev_f32(k, dev), dev_f32(v, dev), kc, vc, 3)
+    kb, vb = host(kc).view(np.uint16), host(vc).view(np.uint16)
+    np.testing.assert_array_equal(kb[3:8], f16_bits(k))
+    np.testing.assert_array_equal(vb[3:8], f16_bits(v))
+    assert (kb[:3] == 0xFFFF).all() and (kb[8:] == 0xFFFF).all()
+
+
+def test_decode_sequence_matches_block(dev):
+    """Token-by-token decode (nt=1 at pos0, pos0+1, ...) equals one nt-token call (MTP verify)."""
+    ctx, nt = 1000, 4
+    q, kb, vb = attn_inputs(5, ctx=ctx, nt=nt)
+    qd = dev_f32(q.reshape(nt, -1), dev)
+    kc, vc = dev_f16bits(kb, dev), dev_f16bits(vb, dev)
+    block = host(ops.attn_f16(qd, kc, vc, ctx - nt, 16, 2))
+    for t in range(nt):
+        one = host(ops.attn_f16(qd[t:t + 1].contiguous(), kc, vc, ctx - nt + t, 16, 2))
+        np.testing.assert_allclose(one[0], block[t], atol=1e-6)

@@ -1,0 +1,104 @@
+"""Pins the GDN oracle (oracle/cpu_ref.cpp it_ref_gdn_*, restating src/cpu.rs:201-232) and the
+float64 chunked WY/UT statement (oracle/ref_np.py), which has no reference counterpart."""
+import numpy as np
+import pytest
+
+import oracle
+from oracle.ref_np import gdn_chunked_f64, gdn_seq_f64
+from irontimber_amd.synth import gdn_inputs, gdn_step_inputs
+
+
+def small(seed=5, nt=6, nv=4, nk=2):
+    return gdn_step_inputs(seed, nt, nv=nv, nk=nk)
+
+
+def test_step_matches_float64_recurrence():
+    d = small()
+    out, st = oracle.gdn_step(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    o64, s64 = gdn_seq_f64(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    np.testing.assert_allclose(out, o64, atol=2e-6)
+    np.testing.assert_allclose(st, s64, atol=2e-6)
+
+
+def test_step_qk_head_mapping_is_modulo():
+    """V head h reads q/k head h % nk (cpu.rs:219), not h // (nv/nk): perturb k head 0 and check
+    that exactly V heads 0 and 2 (nv=4, nk=2) change."""
+    d = small()
+    base, _ = oracle.gdn_step(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    co = d["co"].copy()
+    co[:, 2 * 128:3 * 128] *= -1.0        # k head 0 (k block starts at nk*S = 256)
+    pert, _ = oracle.gdn_step(co, d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    changed = [not np.allclose(base[:, h * 128:(h + 1) * 128], pert[:, h * 128:(h + 1) * 128]) for h in range(4)]
+    assert changed == [True, False, True, False]
+
+
+def test_step_beta_zero_only_decays():
+    d = small(nt=1)
+    br = np.full_like(d["beta_raw"], -200.0)       # sigmoid -> 0
+    out, st = oracle.gdn_step(d["co"], br, d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    g = np.log1p(np.exp(d["alpha_raw"][0].astype(np.float64))) * d["a"]
+    want = d["state"] * np.exp(g)[:, None, None]
+    np.testing.assert_allclose(st, want, rtol=1e-6, atol=1e-9)
+    q = d["co"][0, :128]  # kh = h % 2 -> q heads 0,1,0,1
+    for h in range(4):
+        qh = d["co"][0, (h % 2) * 128:(h % 2 + 1) * 128]
+        np.testing.assert_allclose(out[0, h * 128:(h + 1) * 128], want[h].T @ qh / np.sqrt(128), atol=1e-6)
+    del q
+
+
+def test_step_full_decay_resets_to_outer_product():
+    d = small(nt=1)
+    ar = np.full_like(d["alpha_raw"], 200.0)       # softplus = 200, times a <= -0.37 -> e^g == 0
+    out, st = oracle.gdn_step(d["co"], d["beta_raw"], ar, d["dt"], d["a"], d["state"], 4, 2)
+    beta = 1 / (1 + np.exp(-d["beta_raw"][0].astype(np.float64)))
+    for h in range(4):
+        k = d["co"][0, 256 + (h % 2) * 128:256 + (h % 2 + 1) * 128].astype(np.float64)
+        v = d["co"][0, 512 + h * 128:512 + (h + 1) * 128].astype(np.float64)
+        np.testing.assert_allclose(st[h], beta[h] * np.outer(k, v), atol=1e-6)
+
+
+def test_conv_multi_token_equals_single_calls():
+    d = gdn_inputs(6, nt=9, nv=2, nk=1)
+    out, st = oracle.gdn_conv(d["x"], d["w"], d["conv_state"])
+    s = d["conv_state"].copy()
+    for t in range(9):
+        o1, s = oracle.gdn_conv(d["x"][t:t + 1], d["w"], s)
+        np.testing.assert_array_equal(o1[0], out[t])
+    np.testing.assert_array_equal(s, st)
+    np.testing.assert_array_equal(st, d["x"][-3:])
+
+
+def test_conv_closed_form():
+    """silu(sum_i w_i x_{t-3+i}) in float64, with the carried state as x_{-3..-1}."""
+    d = gdn_inputs(7, nt=5, nv=2, nk=1)
+    out, _ = oracle.gdn_conv(d["x"], d["w"], d["conv_state"])
+    xs = np.concatenate([d["conv_state"], d["x"]]).astype(np.float64)
+    pre = sum(xs[i:i + 5] * d["w"][:, i].astype(np.float64) for i in range(4))
+    np.testing.assert_allclose(out, pre / (1 + np.exp(-pre)), rtol=1e-5, atol=1e-6)
+
+
+def test_l2norm_unit_rows():
+    x = np.random.default_rng(1).standard_normal((3, 512)).astype(np.float32)
+    y = oracle.l2norm_heads(x, 4, 128)
+    np.testing.assert_allclose(np.linalg.norm(y.reshape(3, 4, 128), axis=-1), 1.0, rtol=1e-6)
+
+
+@pytest.mark.parametrize("nt,C", [(1, 64), (64, 64), (100, 64), (130, 16), (37, 8)])
+def test_chunked_f64_equals_sequential(nt, C):
+    d = gdn_step_inputs(8, nt, nv=4, nk=2)
+    o1, s1 = gdn_seq_f64(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    o2, s2 = gdn_chunked_f64(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2, C=C)
+    np.testing.assert_allclose(o2, o1, atol=1e-10)
+    np.testing.assert_allclose(s2, s1, atol=1e-10)
+
+
+def test_layer_matches_pieces():
+    """conv -> L2 -> recurrence, one token at a time (cpu.rs:201-232)."""
+    nv, nk, S, nt = 4, 2, 128, 3
+    d = gdn_inputs(9, nt=nt, nv=nv, nk=nk)
+    co, _ = oracle.gdn_conv(d["x"], d["w"], d["conv_state"])
+    co = oracle.l2norm_heads(co, 2 * nk, S)
+    o1, s1 = oracle.gdn_step(co, d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
+    o64, s64 = gdn_seq_f64(co, d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
+    np.testing.assert_allclose(o1, o64, atol=2e-6)
+    np.testing.assert_allclose(s1, s64, atol=2e-6)
