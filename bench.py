@@ -1,0 +1,304 @@
+"""Benchmark of the attention / Gated-DeltaNet hot path on one MI355X.
+
+Headline (BASELINE.json metric "decode attn us/layer + HBM GB/s @ctx 8192; prefill attn TFLOP/s
+@8192 tok"): one step = one decode attention layer (config 2: batch 1, 16 q / 2 KV heads,
+head_dim 256, f16 KV cache of 8192 positions, seed 1) through it_attn_f16. `value` is its HBM
+throughput in algorithmic bytes (K+V f16 + q/gate + out) per second. Beside it the run measures
+MTP verify (nt=4), decode at ctx 512, chunked / whole-prompt causal prefill TFLOP/s (config 3) and
+the GDN decode step (config 4), and times the CPU restatement of src/cpu.rs on host cores.
+
+Method: every timed sequence is captured once into a HIP graph (torch.cuda.graph) and replayed,
+so the figures are device time for back-to-back launches, not Python call overhead; HIP events on
+the capture stream bracket the replay. Decode KV caches rotate through 40 distinct copies
+(640 MiB) so the 256 MB MALL cannot serve them; GDN states rotate through 160 copies (320 MiB).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+NH, NKV, HD = 16, 2, 256
+KVD = NKV * HD
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(n_keys: int, nt: int = 1) -> int:
+    """Algorithmic HBM bytes of one decode/verify attention layer: K+V f16 rows once, q+gate f32 in,
+    out f32 written."""
+    return 2 * n_keys * KVD * 2 + nt * NH * 2 * HD * 4 + nt * NH * HD * 4
+
+
+def prefill_flops(pos0: int, nt: int) -> int:
+    """4*hd*nh*sum_t (pos0+t+1): QK^T and PV over visible keys, masked work not counted."""
+    return 4 * HD * NH * sum(pos0 + t + 1 for t in range(nt))
+
+
+def graph_time_ms(torch, fn, reps: int, warm: int = 3) -> float:
+    """Capture `fn` (which enqueues work on the current stream) into a graph, replay `warm` times,
+    then time one more replay with events on the capture stream. Returns ms per replay."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()   # eager warm-up on the side stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        fn()
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        best = ms if best is None else min(best, ms)
+    return best
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (every GPU box here has "
+              "one GPU); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from irontimber_amd import ops
+    from irontimber_amd._lib import call
+    from irontimber_amd.synth import attn_inputs, gdn_inputs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream_of = lambda: torch.cuda.current_stream().cuda_stream
+    res = {}
+
+    # ------------------------------------------------------------------ decode attention, ctx 8192
+    ctx = 8192
+    q_np, kb, vb = attn_inputs(1, ctx=ctx, nt=4)
+    q4 = torch.from_numpy(q_np.reshape(4, -1)).to(dev)
+    q1 = q4[3:4].contiguous()
+    NSETS = 40
+    kc0 = torch.from_numpy(kb.view(np.int16)).to(dev)
+    vc0 = torch.from_numpy(vb.view(np.int16)).to(dev)
+    kcs = [kc0.clone() for _ in range(NSETS)]
+    vcs = [vc0.clone() for _ in range(NSETS)]
+    out = torch.empty(4, NH * HD, device=dev)
+    chunk = 128   # decode split: 128 keys -> the 8-wave partial kernel, 64 splits per KV head
+    part_bytes = ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, chunk)
+    part = torch.empty(max(part_bytes, ops.attn_scratch_bytes(ctx - 4, 4, NH, NKV, HD, ops.KERNEL_SPLITK, 64)),
+                       dtype=torch.uint8, device=dev)
+    scale = 1.0 / 16
+
+    def decode_step(i, q=q1, nt=1):
+        call("it_attn_f16_ex", q.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,
+             ctx - nt, HD, NH, NKV, nt, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(),
+             ops.KERNEL_AUTO, 0, stream_of())
+
+    def decode_partials(i):
+        call("it_attn_partials", q1.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,
+             ctx - 1, HD, NH, NKV, 1, scale, part.data_ptr(), part.numel(), chunk, stream_of())
+
+    # correctness guard on the benchmarked path (eager vs graph replays)
+    decode_step(0)
+    torch.cuda.synchronize()
+    ref_out = out[:1].clone()
+
+    # headline: exactly K steps in the timed region (warmup W untimed), graph of K steps
+    K, W = args.steps, args.warmup
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(W):
+            decode_step(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(K):
+            decode_step(i)
+    g.replay()   # untimed replay (graph upload)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    total_ms = e0.elapsed_time(e1)
+    assert torch.equal(out[:1], ref_out), "graph replay changed the decode result"
+    us_layer = total_ms * 1000.0 / K
+    dbytes = decode_bytes(ctx)
+    value_gbs = dbytes / (us_layer * 1e-6) / 1e9
+    res["decode_ctx8192_us_per_layer"] = round(us_layer, 3)
+    res["decode_ctx8192_GBs"] = round(value_gbs, 1)
+    log(f"decode ctx8192: {us_layer:.2f} us/layer, {value_gbs:.0f} GB/s")
+
+    # dominant kernel alone: the split-K partial kernel, K launches per graph
+    ms_part = graph_time_ms(torch, lambda: [decode_partials(i) for i in range(K)], reps=3)
+    part_us = ms_part * 1000.0 / K
+    part_gbs = dbytes / (part_us * 1e-6) / 1e9
+    log(f"decode partial kernel: {part_us:.2f} us, {part_gbs:.0f} GB/s")
+
+    # MTP verify: 4 query positions attending 8189..8192 keys
+    ms = graph_time_ms(torch, lambda: [decode_step(i, q4, 4) for i in range(K)], reps=3)
+    res["verify_nt4_us_per_layer"] = round(ms * 1000.0 / K, 3)
+    res["verify_nt4_GBs"] = round(decode_bytes(ctx, 4) / (ms * 1e-3 / K) / 1e9, 1)
+
+    # decode at ctx 512 (config 1, seed 0)
+    q5, kb5, vb5 = attn_inputs(0, ctx=512, nt=1)
+    q5 = torch.from_numpy(q5.reshape(1, -1)).to(dev)
+    k5 = [torch.from_numpy(kb5.view(np.int16)).to(dev) for _ in range(8)]
+    v5 = [torch.from_numpy(vb5.view(np.int16)).to(dev) for _ in range(8)]
+
+    def d512(i):
+        call("it_attn_f16_ex", q5.data_ptr(), NH * 2 * HD, k5[i % 8].data_ptr(), v5[i % 8].data_ptr(), KVD, 511, HD,
+             NH, NKV, 1, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(), ops.KERNEL_SPLITK, chunk,
+             stream_of())
+    ms = graph_time_ms(torch, lambda: [d512(i) for i in range(K)], reps=3)
+    res["decode_ctx512_us_per_layer"] = round(ms * 1000.0 / K, 3)
+    del kcs, vcs, k5, v5
+
+    # ------------------------------------------------------------------ prefill attention (config 3)
+    T = 8192
+    qp_np, kbp, vbp = attn_inputs(2, ctx=T, nt=T)
+    qp = torch.from_numpy(qp_np.reshape(T, -1)).to(dev)
+    kp = torch.from_numpy(kbp.view(np.int16)).to(dev)
+    vp = torch.from_numpy(vbp.view(np.int16)).to(dev)
+    outp = torch.empty(T, NH * HD, device=dev)
+    sb = max(ops.attn_scratch_bytes(c * 64, 64, NH, NKV, HD) for c in range(128))
+    sb = max(sb, ops.attn_scratch_bytes(0, T, NH, NKV, HD))
+    scr = torch.empty(max(sb, 16), dtype=torch.uint8, device=dev)
+
+    def chunk_call(c):
+        call("it_attn_f16", qp[c * 64].data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, c * 64, HD, NH, NKV,
+             64, scale, outp[c * 64].data_ptr(), NH * HD, scr.data_ptr(), scr.numel(), stream_of())
+
+    ms = graph_time_ms(torch, lambda: chunk_call(64), reps=5)
+    f = prefill_flops(4096, 64)
+    res["prefill_chunk64_at4096_us"] = round(ms * 1000, 2)
+    res["prefill_chunk64_at4096_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
+    ms = graph_time_ms(torch, lambda: [chunk_call(c) for c in range(128)], reps=3)
+    f = prefill_flops(0, T)
+    res["prefill_8192_as_128_chunks_ms"] = round(ms, 3)
+    res["prefill_8192_as_128_chunks_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
+
+    def whole():
+        call("it_attn_f16", qp.data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, 0, HD, NH, NKV, T, scale,
+             outp.data_ptr(), NH * HD, scr.data_ptr(), scr.numel(), stream_of())
+    ms = graph_time_ms(torch, whole, reps=3)
+    res["prefill_8192_single_call_ms"] = round(ms, 3)
+    res["prefill_8192_single_call_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
+    prefill_tflops = max(res["prefill_8192_single_call_TFLOPs"], res["prefill_8192_as_128_chunks_TFLOPs"])
+    log(f"prefill: chunk@4096 {res['prefill_chunk64_at4096_TFLOPs']} TF/s, 128 chunks "
+        f"{res['prefill_8192_as_128_chunks_TFLOPs']} TF/s, single call {res['prefill_8192_single_call_TFLOPs']} TF/s")
+    del qp, kp, vp, outp, scr
+
+    # ------------------------------------------------------------------ GDN decode step (config 4)
+    nv, nk, S = 32, 16, 128
+    d = gdn_inputs(3, nt=1, nv=nv, nk=nk)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+    NST = 160
+    states = [t(d["state"]) for _ in range(NST)]
+    x, w, cst = t(d["x"]), t(d["w"]), t(d["conv_state"])
+    br, ar, dtv, av = t(d["beta_raw"]), t(d["alpha_raw"]), t(d["dt"]), t(d["a"])
+    co = torch.empty(1, d["cd"], device=dev)
+    og = torch.empty(1, nv * S, device=dev)
+
+    def gdn_layer(i):
+        call("it_gdn_conv", x.data_ptr(), d["cd"], w.data_ptr(), cst.data_ptr(), co.data_ptr(), d["cd"], d["cd"], 1, 4,
+             stream_of())
+        call("it_l2norm_heads", co.data_ptr(), d["cd"], 2 * nk, S, 1, 1e-6, stream_of())
+        call("it_gdn_step", co.data_ptr(), d["cd"], br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
+             states[i % NST].data_ptr(), og.data_ptr(), nv * S, 1, nv, nk, S, stream_of())
+
+    def gdn_only(i):
+        call("it_gdn_step", co.data_ptr(), d["cd"], br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
+             states[i % NST].data_ptr(), og.data_ptr(), nv * S, 1, nv, nk, S, stream_of())
+    ms = graph_time_ms(torch, lambda: [gdn_layer(i) for i in range(K)], reps=3)
+    res["gdn_decode_layer_us"] = round(ms * 1000 / K, 3)
+    ms = graph_time_ms(torch, lambda: [gdn_only(i) for i in range(K)], reps=3)
+    gst_us = ms * 1000 / K
+    gbytes = 2 * nv * S * S * 4
+    res["gdn_step_us"] = round(gst_us, 3)
+    res["gdn_step_state_GBs"] = round(gbytes / (gst_us * 1e-6) / 1e9, 1)
+    log(f"gdn: layer {res['gdn_decode_layer_us']} us, step {gst_us:.2f} us ({res['gdn_step_state_GBs']} GB/s state)")
+    del states
+
+    # ------------------------------------------------------------------ CPU baseline (oracle, host cores)
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        threads = min(16, oracle.hardware_threads())
+        q_c = q_np[3:4].reshape(1, -1)
+        n_runs, t0 = 0, time.perf_counter()
+        while True:
+            oracle.attn(q_c, kb, vb, ctx - 1, NH, NKV, threads=threads)
+            n_runs += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds or n_runs >= 2000:
+                break
+        cpu_us = el / n_runs * 1e6
+        cpu = {"value": round(dbytes / (cpu_us * 1e-6) / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+               "us_per_layer": round(cpu_us, 1),
+               "sample": f"{n_runs} decode-attention layers at ctx 8192 (config 2) through oracle/cpu_ref.cpp "
+                         f"(restatement of src/cpu.rs:260-272), {threads} threads, {el:.1f} s"}
+        log(f"cpu baseline: {cpu_us:.0f} us/layer on {threads} threads")
+
+    line = {
+        "metric": "decode attn µs/layer + HBM GB/s @ctx 8192; prefill attn TFLOP/s @8192 tok",
+        "value": round(value_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(us_layer / 1000.0, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded splitmix64 N(0,1), BASELINE configs 1-4)",
+        "config": {"workload": "decode attention, 1 layer, batch 1, 16 q / 2 KV heads, head_dim 256, "
+                               "f16 KV cache 8192 positions (config 2, seed 1)",
+                   "kv_rotation_sets": NSETS, "split_keys": chunk, "timing": "hip graph replay, hip events"},
+        "decode_us_per_layer": round(us_layer, 3),
+        "prefill_attn_TFLOPs": prefill_tflops,
+        "results": res,
+        "roofline": {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "attn_partial_kernel<1, 8>", "kernel_us": round(part_us, 3),
+                     "bytes_per_launch": dbytes},
+        "roofline_prefill": {"bound": "mfma", "achieved": prefill_tflops, "peak": F16_MFMA_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

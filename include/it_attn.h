@@ -74,6 +74,22 @@ int it_attn_f16_ex(const float* q, int q_tok_stride, const uint16_t* kc, const u
                    int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
                    void* scratch, size_t scratch_bytes, int kernel, int chunk, void* stream);
 
+/* The two phases of the split-K path as separate calls (the reference dispatches them separately
+ * too: attn_s_h then attn_comb, src/vk/mod.rs:725-727). Partial record of (token t, q-head h,
+ * split s) is 260 floats {m, l, 0, 0, o[256]} at part + ((t*nh + h)*smax + s)*260 with
+ * smax = ceil((pos0+nt)/chunk): m = max score, l = sum exp(score - m), o = sum exp(score - m) v
+ * over the split's keys visible to token t (kernels/src/lib.rs:753-798). Records of splits a token
+ * cannot see are left untouched. A sequence-sharded caller can exchange these records and run
+ * it_attn_combine locally.
+ *   it_attn_partials: part must hold it_attn_scratch_bytes_ex(pos0,nt,hd,nh,nkv,1,chunk) bytes.
+ *   it_attn_combine : out = merge of the records of splits 0..ceil((pos0+t+1)/chunk)-1, times
+ *                     sigmoid(gate) (kernels/src/lib.rs:722-740). */
+int it_attn_partials(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
+                     int hd, int nh, int nkv, int nt, float scale, float* part, size_t part_bytes, int chunk,
+                     void* stream);
+int it_attn_combine(const float* q, int q_tok_stride, const float* part, int pos0, int hd, int nh, int nt, int chunk,
+                    float* out, int out_tok_stride, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Gated DeltaNet: short causal conv, q/k L2 norm, gated-delta recurrence.
  * ---------------------------------------------------------------------------------------------- */

@@ -21,6 +21,9 @@ SIGNATURES = {
     "it_attn_scratch_bytes_ex": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "it_attn_f16_ex": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P, c_size_t,
                                c_int, c_int, P]),
+    "it_attn_partials": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_size_t, c_int,
+                                 P]),
+    "it_attn_combine": (c_int, [P, c_int, P, c_int, c_int, c_int, c_int, c_int, P, c_int, P]),
     "it_gdn_conv": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
     "it_l2norm_heads": (c_int, [P, c_int, c_int, c_int, c_int, c_float, P]),
     "it_gdn_step": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),

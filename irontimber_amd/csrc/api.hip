@@ -34,9 +34,11 @@ constexpr int KERNEL_AUTO = 0, KERNEL_SPLITK = 1, KERNEL_FLASH = 2;
 constexpr size_t AUTO_SCRATCH_CAP = size_t(256) << 20;   // keep automatic split-K scratch under 256 MiB
 
 // Keys per split for the split-K kernel when the caller leaves it to us.
-int auto_chunk(int pos0, int nt, int nh) {
+// Decode-shaped calls (at most 8 query rows per KV head) start at 128-key splits, which run the
+// 8-wave partial kernel; wider row blocks start at 64.
+int auto_chunk(int pos0, int nt, int nh, int nkv) {
     const size_t total = (size_t)pos0 + nt;
-    int c = 64;
+    int c = (nt * (nh / nkv) <= 8) ? 128 : 64;
     while (c < (1 << 20) && (size_t)nt * nh * ((total + c - 1) / c) * PART_WORDS * 4 > AUTO_SCRATCH_CAP) c *= 2;
     return c;
 }
@@ -82,11 +84,11 @@ int it_kv_append_f16(const float* k, const float* v, int src_tok_stride, uint16_
 }
 
 size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int kernel, int chunk) {
-    (void)hd; (void)nkv;
-    if (nt <= 0 || pos0 < 0 || nh <= 0) return 0;
+    (void)hd;
+    if (nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv) return 0;
     if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
     if (kernel == KERNEL_FLASH) return 0;
-    if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh);
+    if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
     return splitk_scratch(pos0, nt, nh, chunk);
 }
 size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv) {
@@ -104,7 +106,7 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
         return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st), "it_attn_f16 (flash)");
     }
     if (kernel != KERNEL_SPLITK) return fail("it_attn_f16: unknown kernel %d", kernel);
-    if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh);
+    if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
     if (chunk % 64 != 0) return fail("it_attn_f16: chunk %d must be a multiple of 64", chunk);
     const size_t need = splitk_scratch(pos0, nt, nh, chunk);
     if (scratch_bytes < need || (need && !scratch))
@@ -118,6 +120,28 @@ int it_attn_f16(const float* q, int qts, const uint16_t* kc, const uint16_t* vc,
                 int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes, void* stream) {
     return it_attn_f16_ex(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, ots, scratch, scratch_bytes,
                           KERNEL_AUTO, 0, stream);
+}
+
+int it_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
+                     int nkv, int nt, float scale, float* part, size_t part_bytes, int chunk, void* stream) {
+    if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, q, qts)) return -1;
+    if (chunk <= 0 || chunk % 64 != 0) return fail("it_attn_partials: chunk %d must be a positive multiple of 64", chunk);
+    const size_t need = splitk_scratch(pos0, nt, nh, chunk);
+    if (!part || part_bytes < need) return fail("it_attn_partials: %zu bytes of partials < %zu required", part_bytes, need);
+    if (!aligned16(part)) return fail("it_attn_partials: part must be 16-byte aligned");
+    return check(it::launch_attn_partials(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, (hipStream_t)stream),
+                 "it_attn_partials");
+}
+
+int it_attn_combine(const float* q, int qts, const float* part, int pos0, int hd, int nh, int nt, int chunk, float* out,
+                    int ots, void* stream) {
+    if (hd != HD || nh <= 0 || nt <= 0 || pos0 < 0) return fail("it_attn_combine: bad geometry");
+    if (chunk <= 0 || chunk % 64 != 0) return fail("it_attn_combine: chunk %d must be a positive multiple of 64", chunk);
+    if (!q || !part || !out || !aligned16(q) || !aligned16(part) || !aligned16(out))
+        return fail("it_attn_combine: buffers must be non-null and 16-byte aligned");
+    if (qts % 4 != 0 || ots % 4 != 0) return fail("it_attn_combine: token strides must be multiples of 4");
+    return check(it::launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, (hipStream_t)stream),
+                 "it_attn_combine");
 }
 
 int it_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt, int K,

@@ -23,6 +23,19 @@ __device__ __forceinline__ f16v mfma32x32x16(h8 a, h8 b, f16v c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group, source lane s points
+// at 4 consecutive 16-bit values; result lane i, slot e is element (i & 3) of source lane 4e + i/4.
+// With a row-major [row][col] tile and source lane s addressing &T[r0 + s/4][c0 + 4*(s & 3)], lane i
+// receives T[r0 + e][c0 + i] for e = 0..3: four consecutive rows of one column.
+typedef short s4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ h4 lds_tr4(const _Float16* p) {
+    typedef __attribute__((address_space(3))) s4v lds_s4v;
+    const s4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v*)(__attribute__((address_space(3))) char*)(p));
+    return __builtin_bit_cast(h4, v);
+}
+__device__ __forceinline__ h8 cat_h4(h4 a, h4 b) { return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
+
 __device__ __forceinline__ h8 ld_h8(const void* p) { return __builtin_bit_cast(h8, *(const u4*)p); }
 __device__ __forceinline__ f4 ld_f4(const float* p) { return *(const f4*)p; }
 

@@ -41,10 +41,12 @@ def test_ragged_and_group_shapes(dev, ctx, nt, nh, nkv):
     assert np.abs(got - want).max() <= 1e-5
 
 
-@pytest.mark.parametrize("chunk", [64, 128, 256, 1024, 8192])
-def test_split_invariance(dev, chunk):
-    """The result does not depend on how the keys are split (invariant of the LSE merge)."""
-    got, want = run_case(dev, 3, 2000, 4, kernel=ops.KERNEL_SPLITK, chunk=chunk)
+@pytest.mark.parametrize("nt", [1, 4])
+@pytest.mark.parametrize("chunk", [64, 128, 192, 256, 1024, 8192])
+def test_split_invariance(dev, chunk, nt):
+    """The result does not depend on how the keys are split (invariant of the LSE merge). nt=1 with
+    chunk % 128 == 0 runs the 8-wave decode kernel, the rest the 4-wave one."""
+    got, want = run_case(dev, 3, 2000, nt, kernel=ops.KERNEL_SPLITK, chunk=chunk)
     assert np.abs(got - want).max() <= 1e-5
 
 
@@ -96,3 +98,22 @@ def test_decode_sequence_matches_block(dev):
     for t in range(nt):
         one = host(ops.attn_f16(qd[t:t + 1].contiguous(), kc, vc, ctx - nt + t, 16, 2))
         np.testing.assert_allclose(one[0], block[t], atol=1e-6)
+
+
+def test_two_phase_abi_equals_single_call(dev):
+    """it_attn_partials + it_attn_combine (the exchangeable split-K records) == it_attn_f16."""
+    from irontimber_amd._lib import call
+    ctx, nt, nh, nkv, chunk = 700, 3, 16, 2, 128
+    q, kb, vb = attn_inputs(6, ctx=ctx, nt=nt)
+    qd = dev_f32(q.reshape(nt, -1), dev)
+    kc, vc = dev_f16bits(kb, dev), dev_f16bits(vb, dev)
+    ref = host(ops.attn_f16(qd, kc, vc, ctx - nt, nh, nkv, kernel=ops.KERNEL_SPLITK, chunk=chunk))
+    nbytes = ops.attn_scratch_bytes(ctx - nt, nt, nh, nkv, 256, ops.KERNEL_SPLITK, chunk)
+    part = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(nt, nh * 256, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    call("it_attn_partials", qd.data_ptr(), nh * 512, kc.data_ptr(), vc.data_ptr(), nkv * 256, ctx - nt, 256, nh, nkv,
+         nt, 1 / 16, part.data_ptr(), nbytes, chunk, s)
+    call("it_attn_combine", qd.data_ptr(), nh * 512, part.data_ptr(), ctx - nt, 256, nh, nt, chunk, out.data_ptr(),
+         nh * 256, s)
+    np.testing.assert_array_equal(host(out), ref)
