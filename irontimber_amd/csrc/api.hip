@@ -42,7 +42,7 @@ int auto_chunk(int pos0, int nt, int nh, int nkv) {
     while (c < (1 << 20) && (size_t)nt * nh * ((total + c - 1) / c) * PART_WORDS * 4 > AUTO_SCRATCH_CAP) c *= 2;
     return c;
 }
-int auto_kernel(int nt) { (void)nt; return KERNEL_SPLITK; }
+int auto_kernel(int nt) { return nt >= 16 ? KERNEL_FLASH : KERNEL_SPLITK; }
 
 size_t splitk_scratch(int pos0, int nt, int nh, int chunk) {
     const size_t smax = ((size_t)pos0 + nt + chunk - 1) / chunk;

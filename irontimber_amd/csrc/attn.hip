@@ -89,29 +89,43 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
 
     const size_t head_off = (size_t)kh * HD;
     const int lrow = tid >> 5, lch = tid & 31;   // load role: rows lrow + (NTH/32)*i, 16-byte chunk lch
-    // Software pipeline: the next tile's K/V rows are loaded into registers while the current
-    // tile is computed. Rows past pend are clamped to a valid row (masked scores, P = 0).
+    // Loads are issued in the order they are consumed -- query rows, then the tile's K rows, then
+    // its V rows -- so the scores and the softmax run while V is still arriving, and the next
+    // tile's K/V are loaded while the current P.V runs. Rows past pend are clamped to a valid row
+    // (masked scores, P = 0).
     u4 kr[8], vr[8];
-    auto load_tile = [&](int kb) {
+    auto load_k = [&](int kb) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const size_t row = (size_t)min(kb + lrow + (NTH / 32) * i, pend - 1) * kvd + head_off + 8 * lch;
-            kr[i] = *(const u4*)(kc + row);
-            vr[i] = *(const u4*)(vc + row);
-        }
+        for (int i = 0; i < 8; ++i)
+            kr[i] = *(const u4*)(kc + (size_t)min(kb + lrow + (NTH / 32) * i, pend - 1) * kvd + head_off + 8 * lch);
     };
-    load_tile(p0);
-    // stage the query rows once, as f16 hi + lo (loads issued behind the first tile's)
+    auto load_v = [&](int kb) {
 #pragma unroll
-    for (int it = 0; it < (ROWS * HD / 8 + NTH - 1) / NTH; ++it) {
+        for (int i = 0; i < 8; ++i)
+            vr[i] = *(const u4*)(vc + (size_t)min(kb + lrow + (NTH / 32) * i, pend - 1) * kvd + head_off + 8 * lch);
+    };
+    constexpr int QIT = (ROWS * HD / 8 + NTH - 1) / NTH;
+    f4 qx[QIT][2];
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
         const int idx = tid + NTH * it;          // 8-float piece: row idx/32, dims 8*(idx%32)
+        const int row = idx >> 5, rr = r0 + row;
+        qx[it][0] = qx[it][1] = f4{0.f, 0.f, 0.f, 0.f};
+        if (idx < ROWS * HD / 8 && rr < R) {
+            const float* src = q + (size_t)(rr / G) * qts + (size_t)(kh * G + rr % G) * 2 * HD + 8 * (idx & 31);
+            qx[it][0] = ld_f4(src); qx[it][1] = ld_f4(src + 4);
+        }
+    }
+    load_k(p0);
+    load_v(p0);
+    // stage the query rows once, as f16 hi + lo
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
+        const int idx = tid + NTH * it;
         if (idx < ROWS * HD / 8) {
-            const int row = idx >> 5, d0 = 8 * (idx & 31), rr = r0 + row;
-            h8 hi = {}, lo = {};
-            if (rr < R) {
-                const float* src = q + (size_t)(rr / G) * qts + (size_t)(kh * G + rr % G) * 2 * HD + d0;
-                split_hi_lo(ld_f4(src), ld_f4(src + 4), hi, lo);
-            }
+            const int row = idx >> 5, d0 = 8 * (idx & 31);
+            h8 hi, lo;
+            split_hi_lo(qx[it][0], qx[it][1], hi, lo);
             *(h8*)&Qs[0][row][d0] = hi;
             *(h8*)&Qs[1][row][d0] = lo;
         }
@@ -119,11 +133,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
 
     for (int kb = p0; kb < pend; kb += KT) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            *(u4*)&Ks[(lrow + (NTH / 32) * i) * KST + 8 * lch] = kr[i];
-            *(u4*)&Vs[(lrow + (NTH / 32) * i) * VST + 8 * lch] = vr[i];
-        }
-        if (kb + KT < pend) load_tile(kb + KT);
+        for (int i = 0; i < 8; ++i) *(u4*)&Ks[(lrow + (NTH / 32) * i) * KST + 8 * lch] = kr[i];
         __syncthreads();
         // ---- scores for every row block
         const int pk = kb + 16 * w + (l & 15);
@@ -176,6 +186,9 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
             *(f4*)&Ps[sr][8 * c8 + 4] = x1;
             if (c8 == 0) alpha_s[sr] = a;
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *(u4*)&Vs[(lrow + (NTH / 32) * i) * VST + 8 * lch] = vr[i];
+        if (kb + KT < pend) { load_k(kb + KT); load_v(kb + KT); }
         __syncthreads();
         // ---- O = diag(alpha) O + P V; wave w owns dims (256/WAVES)*w ..
         const int g = l >> 4, si = l & 15;

@@ -98,4 +98,4 @@ def test_scratch_bytes_policy():
     # MTP verify (32 rows per KV head): C = 64
     assert lib.it_attn_scratch_bytes(8188, 4, 256, 16, 2) == 4 * 16 * 128 * 260 * 4
     # whole-prompt prefill: flash, no scratch
-    assert lib.it_attn_scratch_bytes_ex(0, 8192, 256, 16, 2, 2, 0) == 0
+    assert lib.it_attn_scratch_bytes(0, 8192, 256, 16, 2) == 0

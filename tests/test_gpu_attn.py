@@ -67,12 +67,55 @@ def test_r012_known_answer(dev, pos0, nt, nh, nkv, hd):
     kb = host(kc).view(np.uint16)
     np.testing.assert_array_equal(kb, f16_bits_rtz(k))
     np.testing.assert_array_equal(host(vc).view(np.uint16), f16_bits_rtz(v))
-    kern = ops.KERNEL_SPLITK if nt < 16 else ops.KERNEL_AUTO
-    got = host(ops.attn_f16(dev_f32(q, dev), kc, vc, pos0, nh, nkv, scale=1.0 / 16, kernel=kern))
+    got = host(ops.attn_f16(dev_f32(q, dev), kc, vc, pos0, nh, nkv, scale=1.0 / 16, kernel=ops.KERNEL_SPLITK))
     want = attn_f64(q, f16_to_f64(kb), f16_to_f64(host(vc).view(np.uint16)), pos0, nh, nkv, hd, 1.0 / 16)
     err = np.abs(got - want).max()
     print(f"r012 gpu max_abs={err:.3g}")
     assert np.isfinite(got).all() and err < 2e-6
+
+
+@pytest.mark.parametrize("pos0,nt", [(0, 64), (0, 16), (63, 17), (4032, 64)])
+@pytest.mark.parametrize("nh,nkv,hd", GEOMS)
+def test_r012_flash(dev, pos0, nt, nh, nkv, hd):
+    """The flash prefill kernel (f16 q and P on the matrix cores) on the r012 closed-form inputs,
+    against the f64 softmax oracle at the north-star bound 2e-3."""
+    announce(f"r012 flash pos0={pos0} nt={nt} nh={nh}")
+    q, k, v = arena(pos0, nt, nh, nkv, hd)
+    kb, vb = f16_bits_rtz(k), f16_bits_rtz(v)
+    got = host(ops.attn_f16(dev_f32(q, dev), dev_f16bits(kb, dev), dev_f16bits(vb, dev), pos0, nh, nkv,
+                            scale=1.0 / 16, kernel=ops.KERNEL_FLASH))
+    want = attn_f64(q, f16_to_f64(kb), f16_to_f64(vb), pos0, nh, nkv, hd, 1.0 / 16)
+    err = np.abs(got - want).max()
+    print(f"r012 flash max_abs={err:.3g}")
+    assert np.isfinite(got).all() and err <= TOL
+
+
+@pytest.mark.parametrize("ctx,nt,nh,nkv", [(16, 16, 16, 2), (100, 37, 16, 2), (300, 300, 16, 2), (333, 129, 24, 4),
+                                           (200, 50, 8, 8), (1000, 64, 4, 1), (4096 + 64, 64, 16, 2)])
+def test_flash_shapes(dev, ctx, nt, nh, nkv):
+    got, want = run_case(dev, 31, ctx, nt, nh, nkv, kernel=ops.KERNEL_FLASH)
+    err = np.abs(got - want).max()
+    print(f"flash max_abs={err:.3g}")
+    assert err <= TOL
+    assert (argmax_projection(got) == argmax_projection(want)).all()
+
+
+def test_flash_whole_prompt_8192(dev):
+    """BASELINE config 3 at full size (seed 2): one 8192-token causal call. The oracle checks the
+    first and last 16 tokens; the whole output equals 128 chunked 64-token calls (split-K path)
+    within the same tolerance (chunked prefill == single-pass causal)."""
+    T = 8192
+    q, kb, vb = attn_inputs(2, ctx=T, nt=T)
+    announce("flash whole prompt 8192")
+    qd = dev_f32(q.reshape(T, -1), dev)
+    kc, vc = dev_f16bits(kb, dev), dev_f16bits(vb, dev)
+    whole = host(ops.attn_f16(qd, kc, vc, 0, 16, 2, kernel=ops.KERNEL_FLASH))
+    for t0 in (0, T - 16):
+        want = oracle.attn(q[t0:t0 + 16].reshape(16, -1), kb, vb, t0, 16, 2)
+        assert np.abs(whole[t0:t0 + 16] - want).max() <= TOL
+    chunked = np.concatenate([host(ops.attn_f16(qd[c:c + 64].contiguous(), kc, vc, c, 16, 2, kernel=ops.KERNEL_SPLITK))
+                              for c in range(0, T, 64)])
+    assert np.abs(whole - chunked).max() <= TOL
 
 
 def test_kv_append_rne_bits(dev):
