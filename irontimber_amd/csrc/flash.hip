@@ -14,8 +14,8 @@
 //   O^T += V^T P^T        A = V^T through the LDS transpose read of the row-major V tile, B = P^T
 //                         straight from the S^T accumulator (f16); O^T lives in 8 accumulator
 //                         tiles (256 dims x 32 queries per wave).
-// K/V tiles are staged in LDS with fully coalesced 16-byte loads; the next tile is loaded into
-// registers while the current one is computed. Row tiles are scheduled heaviest (most keys) first.
+// K/V tiles go straight from HBM/L2 into double-buffered LDS (global_load_lds, 16 bytes per lane,
+// no registers): tile t+1 streams in while tile t is computed, one barrier per tile.
 #include "common.h"
 #include "internal.h"
 
@@ -24,16 +24,43 @@ namespace it {
 namespace {
 constexpr int HD = 256;
 constexpr int BM = 128, BN = 64;
-constexpr int KST = HD + 8;    // K tile row stride (halves)
-constexpr int VST = HD + 16;   // V tile row stride (halves)
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr float RESCALE_SLACK = 8.0f;   // log2 units
 }
+
+// LDS tiles are unpadded 512-byte rows of 32 16-byte chunks; logical chunk j of row r lives at
+// physical chunk j ^ swz(r). swz spreads 8 consecutive rows over 8 chunk positions (conflict-free
+// K operand reads) and the 4 rows x 2 chunks of one transpose read over 8 positions.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// Issue the direct-to-LDS loads of one 64-row tile: wave w moves rows 16w..16w+15, two rows
+// (64 lanes x 16 bytes) per instruction, each lane fetching the logical chunk that belongs at its
+// physical slot.
+__device__ __forceinline__ void tile_to_lds(const uint16_t* __restrict__ src, int kvd, size_t head_off, int kb,
+                                            int kend, _Float16* lds, int w, int l) {
+    typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = 16 * w + 2 * i + (l >> 5);
+        const int j = (l & 31) ^ swz(r);
+        const uint16_t* g = src + (size_t)min(kb + r, kend - 1) * kvd + head_off + 8 * j;
+        __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + (16 * w + 2 * i) * HD), 16, 0, 0);
+    }
+}
+
+// s_waitcnt immediates (gfx9 encoding): wait until at most N vector-memory ops are outstanding
+// (expcnt/lgkmcnt left unconstrained).
+#define IT_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
 
 __global__ __launch_bounds__(256) void attn_flash_kernel(
     const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int kvd,
     int pos0, int nh, int nkv, int nt, float scale, float* __restrict__ out, int ots) {
-    __shared__ __align__(16) _Float16 Ks[BN * KST];
-    __shared__ __align__(16) _Float16 Vs[BN * VST];
+    // two K and two V buffers as distinct objects, so the compiler can tell that the loads
+    // streaming into one buffer never alias the reads of the other (no conservative waits)
+    __shared__ __align__(16) _Float16 K0[BN * HD];
+    __shared__ __align__(16) _Float16 K1[BN * HD];
+    __shared__ __align__(16) _Float16 V0[BN * HD];
+    __shared__ __align__(16) _Float16 V1[BN * HD];
 
     const int G = nh / nkv, R = nt * G;
     const int nrt = (R + BM - 1) / BM;
@@ -48,61 +75,68 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     const int kend = pos0 + tmax + 1;                   // keys any row of the tile sees
     const int kfull = pos0 + tmin + 1;                  // keys every row of the tile sees
     const int qlim = pos0 + t;                          // this row sees keys <= qlim
+    const size_t head_off = (size_t)kh * HD;
 
-    // q as the B operand: column = query c, k = dims 16*ks + 8*hh + 0..7, scaled into log2 units
+    // q as the B operand: column = query c, k = dims 16*ks + 8*hh + 0..7, scaled into log2 units.
+    // All q loads are issued before the first tile's, and consumed after them all, so the
+    // prologue costs one memory round trip.
     h8 qb[16];
     {
-        const float sc = scale * LOG2E;
+        f4 qx[32];
         const float* src = q + (size_t)t * qts + (size_t)head * 2 * HD + 8 * hh;
 #pragma unroll
         for (int ks = 0; ks < 16; ++ks) {
-            if (rvalid) qb[ks] = to_h8(ld_f4(src + 16 * ks) * sc, ld_f4(src + 16 * ks + 4) * sc);
-            else qb[ks] = h8{};
+            qx[2 * ks] = rvalid ? ld_f4(src + 16 * ks) : f4{};
+            qx[2 * ks + 1] = rvalid ? ld_f4(src + 16 * ks + 4) : f4{};
         }
+        tile_to_lds(kc, kvd, head_off, 0, kend, K0, w, l);
+        tile_to_lds(vc, kvd, head_off, 0, kend, V0, w, l);
+        const float sc = scale * LOG2E;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) qb[ks] = to_h8(qx[2 * ks] * sc, qx[2 * ks + 1] * sc);
     }
     f16v o[8];
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[db] = f16v{};
     float m_run = -INFINITY, l_run = 0.f;
 
-    const size_t head_off = (size_t)kh * HD;
-    const int lrow = tid >> 5, lch = tid & 31;          // load role: rows lrow + 8i, chunk lch
-    u4 kr[8], vr[8];
-    auto load_tile = [&](int kb) {
+    // Per-lane LDS offsets (halves). K operand: row c (+32 per block), logical chunk 2ks+hh.
+    int koff[4];
+    {
+        const int sw = swz(c);          // swz(32b + c) == swz(c)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const size_t row = (size_t)min(kb + lrow + 8 * i, kend - 1) * kvd + head_off + 8 * lch;
-            kr[i] = *(const u4*)(kc + row);
-        }
+        for (int k2 = 0; k2 < 4; ++k2) koff[k2] = c * HD + 8 * ((2 * k2 + hh) ^ sw);
+    }
+    // V transpose read: source lane provides row 4hh + vrow (+16ks, +8 for the second half) and
+    // logical column 32db + vcol; swz of those rows is (vrow << 1) | hh for every ks.
+    int voff[2];
+    {
+        const int vrow = (l & 15) >> 2, vcol = 16 * ((l >> 4) & 1) + 4 * (l & 3);
+        const int sv = (vrow << 1) | hh, jj = vcol >> 3, inner = vcol & 7;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const size_t row = (size_t)min(kb + lrow + 8 * i, kend - 1) * kvd + head_off + 8 * lch;
-            vr[i] = *(const u4*)(vc + row);
-        }
-    };
-    load_tile(0);
+        for (int par = 0; par < 2; ++par) voff[par] = (4 * hh + vrow) * HD + 8 * ((4 * par + jj) ^ sv) + inner;
+    }
 
-    // V^T operand addressing for the transpose read: lane l provides &V[key0 + (l&15)/4][col0 + 4*(l&3)]
-    const int vrow = (l & 15) >> 2, vcol = 16 * ((l >> 4) & 1) + 4 * (l & 3);
-
-    for (int kb = 0; kb < kend; kb += BN) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            *(u4*)&Ks[(lrow + 8 * i) * KST + 8 * lch] = kr[i];
-            *(u4*)&Vs[(lrow + 8 * i) * VST + 8 * lch] = vr[i];
-        }
-        if (kb + BN < kend) load_tile(kb + BN);
+    // one 64-key tile: K/V hold tile kb (issued one tile earlier); tile kb+BN streams into Kn/Vn
+    auto tile = [&](int kb, const _Float16* K, const _Float16* V, _Float16* Kn, _Float16* Vn) {
+        // tile kb has landed for this wave; after the barrier for every wave, and every wave is
+        // done with the buffers that tile kb+BN goes into
+        IT_WAIT_VMCNT(0);
         __syncthreads();
-
-        // ---- S^T = K Q^T for two 32-key blocks
-        f16v s[2];
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            s[b] = f16v{};
-            const _Float16* ka = &Ks[(32 * b + c) * KST + 8 * hh];
-#pragma unroll
-            for (int ks = 0; ks < 16; ++ks) s[b] = mfma32x32x16(ld_h8(ka + 16 * ks), qb[ks], s[b]);
+        if (kb + BN < kend) {
+            tile_to_lds(kc, kvd, head_off, kb + BN, kend, Kn, w, l);
+            tile_to_lds(vc, kvd, head_off, kb + BN, kend, Vn, w, l);
         }
+        // ---- S^T = K Q^T for two 32-key blocks. Logical chunk 2ks+hh of row rr sits at physical
+        // chunk 8*(ks/4) + ((2*(ks%4) + hh) ^ swz(rr)): four per-lane offsets plus immediates.
+        f16v sc[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) sc[b] = f16v{};
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                sc[b] = mfma32x32x16(ld_h8(K + (32 * b) * HD + koff[ks & 3] + 64 * (ks >> 2)), qb[ks], sc[b]);
         // ---- causal mask (only tiles that reach past the first row's diagonal)
         if (kb + BN > kfull) {
 #pragma unroll
@@ -110,19 +144,29 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int key = kb + 32 * b + 8 * (i >> 2) + 4 * hh + (i & 3);
-                    if (!rvalid || key > qlim) s[b][i] = -INFINITY;
+                    if (!rvalid || key > qlim) sc[b][i] = -INFINITY;
                 }
         }
-        // ---- online softmax (log2 domain)
+        // ---- online softmax in the log2 domain with a lazily raised reference max: m_run only
+        // moves when a row's max exceeds it by more than RESCALE_SLACK, so O and l are rescaled
+        // on few tiles; P = 2^(s - m_run) <= 2^RESCALE_SLACK stays exact enough in f16 and the
+        // final O / l does not depend on the reference.
         float mx = -INFINITY;
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[b][i]);
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[b][i]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = fmaxf(m_run, mx);
-        const float alpha = (mnew == -INFINITY) ? 1.0f : exp2f(m_run - mnew);
-        const float msub = (mnew == -INFINITY) ? 0.0f : mnew;
+        const bool grow = mx > m_run + RESCALE_SLACK;
+        if (__any(grow)) {
+            const float mnew = grow ? mx : m_run;
+            const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - mnew);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) o[db] *= alpha;
+            m_run = mnew;
+        }
+        const float msub = (m_run == -INFINITY) ? 0.0f : m_run;
         float lsum = 0.f;
         h8 pb[4];
 #pragma unroll
@@ -131,26 +175,26 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
             for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float p = exp2f(s[b][8 * kk + j] - msub);
+                    const float p = __builtin_amdgcn_exp2f(sc[b][8 * kk + j] - msub);
                     lsum += p;
                     pb[2 * b + kk][j] = (_Float16)p;
                 }
         lsum += __shfl_xor(lsum, 32);
-        l_run = l_run * alpha + lsum;
-        m_run = mnew;
+        l_run += lsum;
+        // ---- O^T += V^T P^T: k-step ks covers keys 16ks + {4hh + 0..3, 8 + 4hh + 0..3}; the
+        // transpose-read address is voff[db & 1] plus immediates
 #pragma unroll
-        for (int db = 0; db < 8; ++db) o[db] *= alpha;
-        // ---- O^T += V^T P^T: k-step ks covers keys 16ks + {4hh + 0..3, 8 + 4hh + 0..3}
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const _Float16* vsrc = &Vs[(16 * ks + 4 * hh + vrow) * VST + vcol];
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
-                const h8 va = cat_h4(lds_tr4(vsrc + 32 * db), lds_tr4(vsrc + 8 * VST + 32 * db));
+                const _Float16* v = V + voff[db & 1] + (16 * ks) * HD + 64 * (db >> 1);
+                const h8 va = cat_h4(lds_tr4(v), lds_tr4(v + 8 * HD));
                 o[db] = mfma32x32x16(va, pb[ks], o[db]);
             }
-        }
-        __syncthreads();
+    };
+    for (int kb = 0; kb < kend; kb += 2 * BN) {
+        tile(kb, K0, V0, K1, V1);
+        if (kb + BN < kend) tile(kb + BN, K1, V1, K0, V0);
     }
     // ---- out = O / l * sigmoid(gate): lane holds query c, dims 32db + 8*(i/4) + 4hh + (i&3)
     if (!rvalid) return;
