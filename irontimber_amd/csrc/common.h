@@ -27,6 +27,8 @@ __device__ __forceinline__ f16v mfma32x32x16(h8 a, h8 b, f16v c) {
 // at 4 consecutive 16-bit values; result lane i, slot e is element (i & 3) of source lane 4e + i/4.
 // With a row-major [row][col] tile and source lane s addressing &T[r0 + s/4][c0 + 4*(s & 3)], lane i
 // receives T[r0 + e][c0 + i] for e = 0..3: four consecutive rows of one column.
+// The lanes exchange data: issue it with the whole wave active (no divergent branch around it),
+// and keep each 4-lane 32-byte segment 32-byte aligned (row pitch a multiple of 32 bytes).
 typedef short s4v __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ h4 lds_tr4(const _Float16* p) {

@@ -1,10 +1,394 @@
-// Chunk-64 WY/UT gated-delta scan on the matrix cores.
+// Chunk-64 WY/UT form of the gated delta rule on the matrix cores (a new algorithm: the reference
+// runs the recurrence token by token, kernels/src/lib.rs:285-331, cpu.rs:216-232). Per V head h
+// and chunk of L <= 64 tokens with in-chunk cumulative log-decay G (G_t = g_0 + ... + g_t) and
+// D[t,s] = exp(G_t - G_s), starting from the state S0 (key x value):
+//   A'  = strict_lower(diag(beta) (D * K K^T))        (I + A') [W | U] = diag(beta) [e^G K | V]
+//   V'  = U - W S0
+//   O   = (diag(e^G) Q S0 + lower_incl(D * Q K^T) V') / sqrt(128)
+//   S1  = e^{G_last} S0 + (diag(e^{G_last - G}) K)^T V'
+// which is the token-sequential recurrence S <- e^g S + beta k (v - e^g S^T k)^T regrouped; only
+// decay differences G_t - G_s <= 0 (t >= s) are exponentiated, so nothing overflows.
+//
+// Kernel 1 (gdn_chunk_prep, one workgroup per (chunk, V head), all chunks in parallel) produces
+// everything that does not depend on S0: W and e^G Q (f16), U (f32), the decayed K^T (f16),
+// the masked Q K^T block (f16) and e^{G_last}. K K^T / Q K^T are f16 MFMA products of hi+lo
+// splits (three products, ~f32 accurate); the triangular solve is blocked by 16 rows: small
+// substitutions for the diagonal blocks, MFMA hi+lo products for the rest.
+// Kernel 2 (gdn_chunk_scan, one workgroup per (32-column block of the state, V head)) walks the
+// chunks in order with its 128x32 slice of S in MFMA accumulators; S0 and V' enter the products
+// as f16 hi+lo pairs through LDS, so the state path keeps f32 accuracy.
 #include "common.h"
 #include "internal.h"
+
 namespace it {
-size_t gdn_chunked_scratch_bytes(int, int, int) { return 0; }
-hipError_t launch_gdn_chunked(const float*, int, const float*, const float*, int, const float*, const float*, float*,
-                              float*, int, int, int, int, void*, hipStream_t) {
-    return hipErrorNotSupported;
+
+namespace {
+constexpr int C = 64;      // chunk length
+constexpr int SD = 128;    // state size (d_k = d_v)
+// per-(V head, chunk) record in scratch, byte offsets
+constexpr size_t OFF_W = 0;                        // f16 [C][SD]   W (token-major)
+constexpr size_t OFF_QG = OFF_W + C * SD * 2;       // f16 [C][SD]   e^{G_t} q_t
+constexpr size_t OFF_KT = OFF_QG + C * SD * 2;      // f16 [SD][C]   e^{G_last - G_t} k_t, transposed
+constexpr size_t OFF_AQK = OFF_KT + SD * C * 2;     // f16 [C][C]    lower_incl(D * Q K^T)
+constexpr size_t OFF_U = OFF_AQK + C * C * 2;       // f32 [C][SD]   U
+constexpr size_t OFF_GC = OFF_U + C * SD * 4;       // f32           e^{G_last}
+constexpr size_t REC = (OFF_GC + 16 + 255) / 256 * 256;
+constexpr int FPAD = SD + 4;                        // f32 LDS row stride of the K/Q/V tiles
+// f16 LDS row stride of the solve buffers; transpose reads need every 4-lane 32-byte segment
+// 32-byte aligned, so the row pitch (288 B) is a multiple of 32 bytes
+constexpr int XS = SD + 16;
 }
+
+size_t gdn_chunked_scratch_bytes(int nt, int nv, int S) {
+    (void)S;
+    const size_t nch = (size_t)(nt + C - 1) / C;
+    return nch * (size_t)nv * REC;
+}
+
+__device__ __forceinline__ void split8(const float* p, h8& hi, h8& lo) {
+    split_hi_lo(*(const f4*)p, *(const f4*)(p + 4), hi, lo);
+}
+
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gdn_chunk_prep(const float* __restrict__ co, int cts, const float* __restrict__ br,
+                                                      const float* __restrict__ ar, int bts, const float* __restrict__ dt,
+                                                      const float* __restrict__ A, int nt, int nk,
+                                                      char* __restrict__ scr) {
+    __shared__ __align__(16) float Kf[C][FPAD];
+    // Q rows (f32) are only needed until Q K^T and e^G q are out; the solve's hi/lo rows reuse them
+    constexpr int QXWORDS = (2 * C * XS * 2 > C * FPAD * 4 ? 2 * C * XS * 2 : C * FPAD * 4) / 4;
+    __shared__ __align__(16) float QXbuf[QXWORDS];
+    float(*Qf)[FPAD] = (float(*)[FPAD])QXbuf;
+    _Float16(*Xs)[C][XS] = (_Float16(*)[C][XS])QXbuf;
+    __shared__ __align__(16) float Vf[C][FPAD];
+    __shared__ __align__(16) float Ap[C][C + 4];
+    __shared__ float sG[C], sB[C];
+    __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
+    __shared__ __align__(16) _Float16 Rs[2][16][XS];         // right-hand side of the current block
+
+    const int c = blockIdx.x, h = blockIdx.y, nch = gridDim.x;
+    const int t0 = c * C, L = min(C, nt - t0);
+    const int kh = h % nk, qk = nk * SD;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    char* rec = scr + ((size_t)h * nch + c) * REC;
+
+    // ---- q/k rows (zero past the prompt), beta and the cumulative log-decay
+    for (int idx = tid; idx < C * SD / 4; idx += 256) {
+        const int t = idx >> 5, d4 = 4 * (idx & 31);
+        f4 kv = {0.f, 0.f, 0.f, 0.f}, qv = kv, vv = kv;
+        if (t < L) {
+            const float* row = co + (size_t)(t0 + t) * cts;
+            qv = ld_f4(row + kh * SD + d4);
+            kv = ld_f4(row + qk + kh * SD + d4);
+            vv = ld_f4(row + 2 * qk + h * SD + d4);
+        }
+        *(f4*)&Kf[t][d4] = kv;
+        *(f4*)&Qf[t][d4] = qv;
+        *(f4*)&Vf[t][d4] = vv;
+    }
+    if (w == 0) {
+        float g = 0.f, b = 0.f;
+        if (l < L) {
+            b = sigmoidf_(br[(size_t)(t0 + l) * bts + h]);
+            g = softplusf_(ar[(size_t)(t0 + l) * bts + h] + dt[h]) * A[h];
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(g, off);
+            if (l >= off) g += y;
+        }
+        sG[l] = g;
+        sB[l] = b;
+    }
+    __syncthreads();
+
+    // ---- lower 16x16 tiles of K K^T (tiles 0..9) and Q K^T (tiles 10..19), hi+lo products
+    for (int tile = w; tile < 20; tile += 4) {
+        const bool isq = tile >= 10;
+        const int tt = isq ? tile - 10 : tile;
+        const int mt = tt >= 6 ? 3 : tt >= 3 ? 2 : tt >= 1 ? 1 : 0;
+        const int nt_ = tt - mt * (mt + 1) / 2;
+        const float(*Ar)[FPAD] = isq ? (const float(*)[FPAD])Qf : (const float(*)[FPAD])Kf;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            h8 ah, al, bh, bl;
+            split8(&Ar[16 * mt + (l & 15)][32 * ks + 8 * (l >> 4)], ah, al);
+            split8(&Kf[16 * nt_ + (l & 15)][32 * ks + 8 * (l >> 4)], bh, bl);
+            acc = mfma16x16x32(ah, bh, acc);
+            acc = mfma16x16x32(ah, bl, acc);
+            acc = mfma16x16x32(al, bh, acc);
+        }
+        _Float16* aqk = (_Float16*)(rec + OFF_AQK);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 16 * mt + 4 * (l >> 4) + i, s = 16 * nt_ + (l & 15);
+            const float d = expf(fminf(sG[t] - sG[s], 0.f));
+            if (!isq) Ap[t][s] = s < t ? sB[t] * d * acc[i] : 0.f;
+            else aqk[t * C + s] = (_Float16)(s <= t ? d * acc[i] : 0.f);
+        }
+    }
+    // upper tiles of the Q K^T block are zero
+    {
+        _Float16* aqk = (_Float16*)(rec + OFF_AQK);
+        for (int idx = tid; idx < C * C; idx += 256) {
+            const int t = idx >> 6, s = idx & 63;
+            if ((s >> 4) > (t >> 4)) aqk[idx] = (_Float16)0.f;
+        }
+    }
+    __syncthreads();
+
+    // ---- e^G q (token-major) and e^{G_last - G} k (dim-major)
+    {
+        _Float16* QG = (_Float16*)(rec + OFF_QG);
+        _Float16* KT = (_Float16*)(rec + OFF_KT);
+        const float glast = sG[C - 1];
+        for (int idx = tid; idx < C * SD; idx += 256) {
+            const int t = idx >> 7, d = idx & 127;
+            QG[idx] = (_Float16)(expf(sG[t]) * Qf[t][d]);
+        }
+        for (int idx = tid; idx < C * SD; idx += 256) {
+            const int d = idx >> 6, t = idx & 63;
+            KT[idx] = (_Float16)(expf(fminf(glast - sG[t], 0.f)) * Kf[t][d]);
+        }
+        if (tid == 0) *(float*)(rec + OFF_GC) = expf(glast);
+    }
+    __syncthreads();   // Q tile dead from here on: its LDS becomes the solve buffers
+    // ---- (I + A') [W | U] = diag(beta) [e^G K | V], blocked by 16 rows:
+    //   T_i = (I + A'_ii)^-1 (16x16, one wave, forward substitution per column)
+    //   X_i = T_i (diag(beta) B_i - sum_{k<i} A'_ik X_k)          (MFMA, hi+lo products)
+    // W and U are solved one after the other (128 columns each) to bound LDS.
+    if (w == 0) {
+        const int kb = l >> 4, ci = l & 15;
+        float y[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float acc = r == ci ? 1.0f : 0.0f;
+#pragma unroll
+            for (int q = 0; q < r; ++q) acc -= Ap[16 * kb + r][16 * kb + q] * y[q];
+            y[r] = acc;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) Td[kb][r][ci] = y[r];
+    }
+    const int g = l >> 4, li = l & 15;
+    for (int hf = 0; hf < 2; ++hf) {
+        for (int idx = tid; idx < 2 * C * XS / 8; idx += 256) ((u4*)&Xs[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
+        __syncthreads();
+        for (int i = 0; i < 4; ++i) {
+            // R = beta B_i - sum_{k<i} A'_ik X_k for this wave's two 16-column tiles
+            f4 acc[2];
+#pragma unroll
+            for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = 16 * i + 4 * g + e, col = 16 * (2 * w + nt2) + li;
+                    const float b = hf == 0 ? expf(sG[t]) * Kf[t][col] : Vf[t][col];
+                    acc[nt2][e] = sB[t] * b;
+                }
+            for (int ks = 0; ks < (i + 1) / 2; ++ks) {
+                // A operand: -A'[16i + li][32ks + 8g + j], zero at and past column 16i
+                f4 a0, a1;
+                const int s0 = 32 * ks + 8 * g;
+                const float* arow = &Ap[16 * i + li][s0];
+                a0 = s0 < 16 * i ? -*(const f4*)arow : f4{0.f, 0.f, 0.f, 0.f};
+                a1 = s0 + 4 < 16 * i ? -*(const f4*)(arow + 4) : f4{0.f, 0.f, 0.f, 0.f};
+                h8 ah, al;
+                split_hi_lo(a0, a1, ah, al);
+#pragma unroll
+                for (int nt2 = 0; nt2 < 2; ++nt2) {
+                    const int c0 = 16 * (2 * w + nt2);
+                    const _Float16* xh = &Xs[0][s0 + (li >> 2)][c0 + 4 * (li & 3)];
+                    const _Float16* xl = &Xs[1][s0 + (li >> 2)][c0 + 4 * (li & 3)];
+                    const h8 bh = cat_h4(lds_tr4(xh), lds_tr4(xh + 4 * XS));
+                    const h8 bl = cat_h4(lds_tr4(xl), lds_tr4(xl + 4 * XS));
+                    acc[nt2] = mfma16x16x32(ah, bh, acc[nt2]);
+                    acc[nt2] = mfma16x16x32(ah, bl, acc[nt2]);
+                    acc[nt2] = mfma16x16x32(al, bh, acc[nt2]);
+                }
+            }
+            // R -> LDS (hi/lo) so it can be the B operand of T_i R
+#pragma unroll
+            for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v = acc[nt2][e];
+                    const _Float16 hi = (_Float16)v;
+                    const int col = 16 * (2 * w + nt2) + li;
+                    Rs[0][4 * g + e][col] = hi;
+                    Rs[1][4 * g + e][col] = (_Float16)(v - (float)hi);
+                }
+            __syncthreads();
+            // X_i = T_i R: K = 16 (k-groups g >= 2 are zero padding)
+            h8 th = {}, tl = {};
+            if (g < 2) split_hi_lo(*(const f4*)&Td[i][li][8 * g], *(const f4*)&Td[i][li][8 * g + 4], th, tl);
+            f4 xo[2];
+#pragma unroll
+            for (int nt2 = 0; nt2 < 2; ++nt2) {
+                const int c0 = 16 * (2 * w + nt2);
+                // transpose reads run with the whole wave active (the instruction exchanges data
+                // between lanes); k-groups 2 and 3 read rows 0..7 again and are zeroed after
+                const int gr = g & 1;
+                const _Float16* rh = &Rs[0][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
+                const _Float16* rl = &Rs[1][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
+                h8 bh = cat_h4(lds_tr4(rh), lds_tr4(rh + 4 * XS));
+                h8 bl = cat_h4(lds_tr4(rl), lds_tr4(rl + 4 * XS));
+                if (g >= 2) { bh = h8{}; bl = h8{}; }
+                f4 z = {0.f, 0.f, 0.f, 0.f};
+                z = mfma16x16x32(th, bh, z);
+                z = mfma16x16x32(th, bl, z);
+                z = mfma16x16x32(tl, bh, z);
+                xo[nt2] = z;
+            }
+            // X_i -> scratch (W f16 / U f32) and -> LDS (hi/lo) for the later block rows
+#pragma unroll
+            for (int nt2 = 0; nt2 < 2; ++nt2)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = 16 * i + 4 * g + e, col = 16 * (2 * w + nt2) + li;
+                    const float v = xo[nt2][e];
+                    const _Float16 hi = (_Float16)v;
+                    Xs[0][t][col] = hi;
+                    Xs[1][t][col] = (_Float16)(v - (float)hi);
+                    if (hf == 0) ((_Float16*)(rec + OFF_W))[t * SD + col] = hi;
+                    else ((float*)(rec + OFF_U))[t * SD + col] = v;
+                }
+            __syncthreads();
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ scr, int nch, float* __restrict__ state,
+                                                      float* __restrict__ out, int ots, int nt) {
+    constexpr int SP = SD + 8, VP = C + 8;
+    __shared__ __align__(16) _Float16 S0T[2][32][SP];   // [hi|lo][state column][key dim]
+    __shared__ __align__(16) _Float16 VpT[2][32][VP];   // [hi|lo][state column][token]
+
+    const int cb = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
+    const int n0 = 32 * cb;
+    float* sh = state + (size_t)h * SD * SD;
+    const float rs = 1.0f / sqrtf((float)SD);
+
+    // state slice in accumulator layout: st[mi][ni][i] = S[16(2w+mi) + 4g + i][n0 + 16ni + li]
+    f4 st[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) st[mi][ni][i] = sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li];
+
+    for (int c = 0; c < nch; ++c) {
+        const char* rec = scr + ((size_t)h * nch + c) * REC;
+        const _Float16* W = (const _Float16*)(rec + OFF_W);
+        const _Float16* QG = (const _Float16*)(rec + OFF_QG);
+        const _Float16* KT = (const _Float16*)(rec + OFF_KT);
+        const _Float16* AQK = (const _Float16*)(rec + OFF_AQK);
+        const float* U = (const float*)(rec + OFF_U);
+        const float gc = *(const float*)(rec + OFF_GC);
+        const int t0 = c * C, L = min(C, nt - t0);
+
+        // ---- S0 -> LDS as hi/lo, transposed to [column][key dim]
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float v = st[mi][ni][i];
+                    const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+                    const int col = 16 * ni + li, dk = 16 * (2 * w + mi) + 4 * g + i;
+                    S0T[0][col][dk] = hi;
+                    S0T[1][col][dk] = lo;
+                }
+        __syncthreads();
+        // ---- V' = U - W S0 for tokens 16w..16w+15
+        f4 vp[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const h8 a = ld_h8(W + (16 * w + li) * SD + 32 * ks + 8 * g);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                vp[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
+                vp[ni] = mfma16x16x32(a, ld_h8(&S0T[1][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
+            }
+        }
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * w + 4 * g + i, col = 16 * ni + li;
+                const float v = U[t * SD + n0 + col] - vp[ni][i];
+                const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+                VpT[0][col][t] = hi;
+                VpT[1][col][t] = lo;
+            }
+        __syncthreads();
+        // ---- O = (e^G Q S0 + Aqk V') / sqrt(128) for tokens 16w..16w+15
+        f4 oa[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const h8 a = ld_h8(QG + (16 * w + li) * SD + 32 * ks + 8 * g);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                oa[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+                oa[ni] = mfma16x16x32(a, ld_h8(&S0T[1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const h8 a = ld_h8(AQK + (16 * w + li) * C + 32 * ks + 8 * g);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                oa[ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+                oa[ni] = mfma16x16x32(a, ld_h8(&VpT[1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+            }
+        }
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * w + 4 * g + i;
+                if (t < L) out[(size_t)(t0 + t) * ots + (size_t)h * SD + n0 + 16 * ni + li] = oa[ni][i] * rs;
+            }
+        // ---- S1 = e^{G_last} S0 + Ktilde^T V'
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) st[mi][ni] *= gc;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                const h8 a = ld_h8(KT + (16 * (2 * w + mi) + li) * C + 32 * ks + 8 * g);
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni) {
+                    st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
+                    st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
+                }
+            }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li] = st[mi][ni][i];
+}
+
+// ------------------------------------------------------------------------------------------------
+hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+                              const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
+                              hipStream_t st) {
+    const int nch = (nt + C - 1) / C;
+    gdn_chunk_prep<<<dim3(nch, nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, nt, nk, (char*)scratch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    gdn_chunk_scan<<<dim3(SD / 32, nv), 256, 0, st>>>((const char*)scratch, nch, state, out, ots, nt);
+    return hipGetLastError();
+}
+
 }  // namespace it
