@@ -82,6 +82,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 5 plain device copies of 256 MiB (reference reading for the FETCH_SIZE / "
+                         "WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every GPU box here has "
@@ -95,6 +98,14 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 256 << 20, "copies": 5}))
+        return
     stream_of = lambda: torch.cuda.current_stream().cuda_stream
     res = {}
 
@@ -249,6 +260,56 @@ def main():
     res["gdn_step_state_GBs"] = round(gbytes / (gst_us * 1e-6) / 1e9, 1)
     log(f"gdn: layer {res['gdn_decode_layer_us']} us, step {gst_us:.2f} us ({res['gdn_step_state_GBs']} GB/s state)")
     del states
+
+    # ------------------------------------------------------------------ GDN chunked prefill (config 5)
+    T5 = 8192
+    d5 = gdn_inputs(4, nt=T5, nv=nv, nk=nk)
+    x5, w5, cs5 = t(d5["x"]), t(d5["w"]), t(d5["conv_state"])
+    br5, ar5, dt5, a5 = t(d5["beta_raw"]), t(d5["alpha_raw"]), t(d5["dt"]), t(d5["a"])
+    st5 = t(d5["state"])
+    co5 = torch.empty(T5, d5["cd"], device=dev)
+    o5 = torch.empty(T5, nv * S, device=dev)
+    from irontimber_amd._lib import lib as _l
+    scr5 = torch.empty(_l().it_gdn_chunked_scratch_bytes(T5, nv, S), dtype=torch.uint8, device=dev)
+
+    def gdn_prefill():
+        call("it_gdn_conv", x5.data_ptr(), d5["cd"], w5.data_ptr(), cs5.data_ptr(), co5.data_ptr(), d5["cd"], d5["cd"],
+             T5, 4, stream_of())
+        call("it_l2norm_heads", co5.data_ptr(), d5["cd"], 2 * nk, S, T5, 1e-6, stream_of())
+        call("it_gdn_chunked", co5.data_ptr(), d5["cd"], br5.data_ptr(), ar5.data_ptr(), nv, dt5.data_ptr(),
+             a5.data_ptr(), st5.data_ptr(), o5.data_ptr(), nv * S, T5, nv, nk, S, scr5.data_ptr(), scr5.numel(),
+             stream_of())
+
+    def gdn_scan_only():
+        call("it_gdn_chunked", co5.data_ptr(), d5["cd"], br5.data_ptr(), ar5.data_ptr(), nv, dt5.data_ptr(),
+             a5.data_ptr(), st5.data_ptr(), o5.data_ptr(), nv * S, T5, nv, nk, S, scr5.data_ptr(), scr5.numel(),
+             stream_of())
+    ms = graph_time_ms(torch, gdn_prefill, reps=3)
+    res["gdn_prefill_8192_layer_ms"] = round(ms, 4)
+    ms_s = graph_time_ms(torch, gdn_scan_only, reps=3)
+    gflop = 47.96e9   # chunked-form flops for 8192 tokens, 32 V heads, C=64
+    res["gdn_prefill_8192_scan_ms"] = round(ms_s, 4)
+    res["gdn_prefill_8192_scan_TFLOPs"] = round(gflop / (ms_s * 1e-3) / 1e12, 2)
+    io = T5 * (2 * nk + nv) * S * 4 + T5 * nv * S * 4 + 2 * 2 * nv * S * S * 4 + 2 * T5 * nv * 4
+    res["gdn_prefill_8192_scan_io_GBs"] = round(io / (ms_s * 1e-3) / 1e9, 1)
+    log(f"gdn prefill 8192: layer {ms:.3f} ms, scan {ms_s:.3f} ms ({res['gdn_prefill_8192_scan_TFLOPs']} TF/s chunked)")
+
+    # hybrid stack (config 5): 3 GDN prefill layers then 1 attention prefill layer, 8192 tokens
+    T = 8192
+    qp_np, kbp, vbp = attn_inputs(2, ctx=T, nt=T)
+    qp = torch.from_numpy(qp_np.reshape(T, -1)).to(dev)
+    kp = torch.from_numpy(kbp.view(np.int16)).to(dev)
+    vp = torch.from_numpy(vbp.view(np.int16)).to(dev)
+    outp = torch.empty(T, NH * HD, device=dev)
+
+    def hybrid():
+        for _ in range(3):
+            gdn_prefill()
+        call("it_attn_f16", qp.data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, 0, HD, NH, NKV, T, scale,
+             outp.data_ptr(), NH * HD, None, 0, stream_of())
+    ms = graph_time_ms(torch, hybrid, reps=2)
+    res["hybrid_3gdn_1attn_prefill_8192_ms"] = round(ms, 3)
+    del qp, kp, vp, outp, co5, o5, scr5
 
     # ------------------------------------------------------------------ CPU baseline (oracle, host cores)
     cpu = None

@@ -33,7 +33,6 @@ constexpr size_t OFF_AQK = OFF_KT + SD * C * 2;     // f16 [C][C]    lower_incl(
 constexpr size_t OFF_U = OFF_AQK + C * C * 2;       // f32 [C][SD]   U
 constexpr size_t OFF_GC = OFF_U + C * SD * 4;       // f32           e^{G_last}
 constexpr size_t REC = (OFF_GC + 16 + 255) / 256 * 256;
-constexpr int FPAD = SD + 4;                        // f32 LDS row stride of the K/Q/V tiles
 // f16 LDS row stride of the solve buffers; transpose reads need every 4-lane 32-byte segment
 // 32-byte aligned, so the row pitch (288 B) is a multiple of 32 bytes
 constexpr int XS = SD + 16;
@@ -45,76 +44,76 @@ size_t gdn_chunked_scratch_bytes(int nt, int nv, int S) {
     return nch * (size_t)nv * REC;
 }
 
-__device__ __forceinline__ void split8(const float* p, h8& hi, h8& lo) {
-    split_hi_lo(*(const f4*)p, *(const f4*)(p + 4), hi, lo);
-}
-
 // ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gdn_chunk_prep(const float* __restrict__ co, int cts, const float* __restrict__ br,
-                                                      const float* __restrict__ ar, int bts, const float* __restrict__ dt,
-                                                      const float* __restrict__ A, int nt, int nk,
-                                                      char* __restrict__ scr) {
-    __shared__ __align__(16) float Kf[C][FPAD];
-    // Q rows (f32) are only needed until Q K^T and e^G q are out; the solve's hi/lo rows reuse them
-    constexpr int QXWORDS = (2 * C * XS * 2 > C * FPAD * 4 ? 2 * C * XS * 2 : C * FPAD * 4) / 4;
-    __shared__ __align__(16) float QXbuf[QXWORDS];
-    float(*Qf)[FPAD] = (float(*)[FPAD])QXbuf;
-    _Float16(*Xs)[C][XS] = (_Float16(*)[C][XS])QXbuf;
-    __shared__ __align__(16) float Vf[C][FPAD];
+// 8 waves. LDS: K and Q rows as f16 hi/lo pairs (split once), A', the diagonal-block inverses,
+// and the solve buffers, which reuse the Q rows' space once Q K^T and e^G q are out.
+constexpr int PREP_THREADS = 512;
+constexpr int KP = SD + 16;    // f16 row pitch of the K/Q tiles (288 B, 32-byte multiple)
+
+__global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __restrict__ co, int cts,
+                                                               const float* __restrict__ br, const float* __restrict__ ar,
+                                                               int bts, const float* __restrict__ dt,
+                                                               const float* __restrict__ A, int nt, int nk,
+                                                               char* __restrict__ scr) {
+    __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows, hi / lo
+    __shared__ __align__(16) _Float16 QX[2][C][KP];          // Q rows hi / lo, then the solve rows X
     __shared__ __align__(16) float Ap[C][C + 4];
     __shared__ float sG[C], sB[C];
     __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
     __shared__ __align__(16) _Float16 Rs[2][16][XS];         // right-hand side of the current block
+    static_assert(KP == XS, "solve rows reuse the Q tile");
+    _Float16(*Xs)[C][XS] = QX;
 
     const int c = blockIdx.x, h = blockIdx.y, nch = gridDim.x;
     const int t0 = c * C, L = min(C, nt - t0);
     const int kh = h % nk, qk = nk * SD;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
     char* rec = scr + ((size_t)h * nch + c) * REC;
 
-    // ---- q/k rows (zero past the prompt), beta and the cumulative log-decay
-    for (int idx = tid; idx < C * SD / 4; idx += 256) {
-        const int t = idx >> 5, d4 = 4 * (idx & 31);
-        f4 kv = {0.f, 0.f, 0.f, 0.f}, qv = kv, vv = kv;
+    // ---- q/k rows (zero past the prompt) as hi/lo, beta and the cumulative log-decay
+    for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
+        const int t = idx >> 4, d8 = 8 * (idx & 15);
+        f4 k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0, q0 = k0, q1 = k0;
         if (t < L) {
             const float* row = co + (size_t)(t0 + t) * cts;
-            qv = ld_f4(row + kh * SD + d4);
-            kv = ld_f4(row + qk + kh * SD + d4);
-            vv = ld_f4(row + 2 * qk + h * SD + d4);
+            q0 = ld_f4(row + kh * SD + d8); q1 = ld_f4(row + kh * SD + d8 + 4);
+            k0 = ld_f4(row + qk + kh * SD + d8); k1 = ld_f4(row + qk + kh * SD + d8 + 4);
         }
-        *(f4*)&Kf[t][d4] = kv;
-        *(f4*)&Qf[t][d4] = qv;
-        *(f4*)&Vf[t][d4] = vv;
+        h8 hi, lo;
+        split_hi_lo(k0, k1, hi, lo);
+        *(h8*)&Kx[0][t][d8] = hi; *(h8*)&Kx[1][t][d8] = lo;
+        split_hi_lo(q0, q1, hi, lo);
+        *(h8*)&QX[0][t][d8] = hi; *(h8*)&QX[1][t][d8] = lo;
     }
     if (w == 0) {
-        float g = 0.f, b = 0.f;
+        float gg = 0.f, b = 0.f;
         if (l < L) {
             b = sigmoidf_(br[(size_t)(t0 + l) * bts + h]);
-            g = softplusf_(ar[(size_t)(t0 + l) * bts + h] + dt[h]) * A[h];
+            gg = softplusf_(ar[(size_t)(t0 + l) * bts + h] + dt[h]) * A[h];
         }
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            const float y = __shfl_up(g, off);
-            if (l >= off) g += y;
+            const float y = __shfl_up(gg, off);
+            if (l >= off) gg += y;
         }
-        sG[l] = g;
+        sG[l] = gg;
         sB[l] = b;
     }
     __syncthreads();
 
     // ---- lower 16x16 tiles of K K^T (tiles 0..9) and Q K^T (tiles 10..19), hi+lo products
-    for (int tile = w; tile < 20; tile += 4) {
+    for (int tile = w; tile < 20; tile += PREP_THREADS / 64) {
         const bool isq = tile >= 10;
         const int tt = isq ? tile - 10 : tile;
         const int mt = tt >= 6 ? 3 : tt >= 3 ? 2 : tt >= 1 ? 1 : 0;
         const int nt_ = tt - mt * (mt + 1) / 2;
-        const float(*Ar)[FPAD] = isq ? (const float(*)[FPAD])Qf : (const float(*)[FPAD])Kf;
+        const _Float16(*Ar)[C][KP] = isq ? QX : Kx;
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            h8 ah, al, bh, bl;
-            split8(&Ar[16 * mt + (l & 15)][32 * ks + 8 * (l >> 4)], ah, al);
-            split8(&Kf[16 * nt_ + (l & 15)][32 * ks + 8 * (l >> 4)], bh, bl);
+            const int d = 32 * ks + 8 * g;
+            const h8 ah = ld_h8(&Ar[0][16 * mt + li][d]), al = ld_h8(&Ar[1][16 * mt + li][d]);
+            const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
             acc = mfma16x16x32(ah, bh, acc);
             acc = mfma16x16x32(ah, bl, acc);
             acc = mfma16x16x32(al, bh, acc);
@@ -122,42 +121,51 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(const float* __restrict__ 
         _Float16* aqk = (_Float16*)(rec + OFF_AQK);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int t = 16 * mt + 4 * (l >> 4) + i, s = 16 * nt_ + (l & 15);
+            const int t = 16 * mt + 4 * g + i, s = 16 * nt_ + li;
             const float d = expf(fminf(sG[t] - sG[s], 0.f));
             if (!isq) Ap[t][s] = s < t ? sB[t] * d * acc[i] : 0.f;
             else aqk[t * C + s] = (_Float16)(s <= t ? d * acc[i] : 0.f);
         }
     }
-    // upper tiles of the Q K^T block are zero
+    // upper tiles of the Q K^T block are zero (16-byte stores)
     {
-        _Float16* aqk = (_Float16*)(rec + OFF_AQK);
-        for (int idx = tid; idx < C * C; idx += 256) {
-            const int t = idx >> 6, s = idx & 63;
-            if ((s >> 4) > (t >> 4)) aqk[idx] = (_Float16)0.f;
+        u4* aqk = (u4*)(rec + OFF_AQK);
+        for (int idx = tid; idx < C * C / 8; idx += PREP_THREADS) {
+            const int t = idx >> 3, s8 = 8 * (idx & 7);
+            if ((s8 >> 4) > (t >> 4)) aqk[idx] = u4{0u, 0u, 0u, 0u};
         }
     }
-    __syncthreads();
-
-    // ---- e^G q (token-major) and e^{G_last - G} k (dim-major)
+    // ---- e^G q (token-major) and e^{G_last - G} k (dim-major), 8 halves per store
     {
-        _Float16* QG = (_Float16*)(rec + OFF_QG);
-        _Float16* KT = (_Float16*)(rec + OFF_KT);
+        u4* QG = (u4*)(rec + OFF_QG);
+        u4* KT = (u4*)(rec + OFF_KT);
         const float glast = sG[C - 1];
-        for (int idx = tid; idx < C * SD; idx += 256) {
-            const int t = idx >> 7, d = idx & 127;
-            QG[idx] = (_Float16)(expf(sG[t]) * Qf[t][d]);
+        for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
+            const int t = idx >> 4, d8 = 8 * (idx & 15);
+            const float e = expf(sG[t]);
+            const h8 hi = ld_h8(&QX[0][t][d8]), lo = ld_h8(&QX[1][t][d8]);
+            h8 r;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) r[j] = (_Float16)(e * ((float)hi[j] + (float)lo[j]));
+            QG[idx] = __builtin_bit_cast(u4, r);
         }
-        for (int idx = tid; idx < C * SD; idx += 256) {
-            const int d = idx >> 6, t = idx & 63;
-            KT[idx] = (_Float16)(expf(fminf(glast - sG[t], 0.f)) * Kf[t][d]);
+        for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
+            const int d = idx >> 3, t8 = 8 * (idx & 7);
+            h8 r;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int t = t8 + j;
+                r[j] = (_Float16)(expf(fminf(glast - sG[t], 0.f)) * ((float)Kx[0][t][d] + (float)Kx[1][t][d]));
+            }
+            KT[idx] = __builtin_bit_cast(u4, r);
         }
         if (tid == 0) *(float*)(rec + OFF_GC) = expf(glast);
     }
-    __syncthreads();   // Q tile dead from here on: its LDS becomes the solve buffers
+    __syncthreads();   // Q tile dead from here on: its LDS becomes the solve rows
     // ---- (I + A') [W | U] = diag(beta) [e^G K | V], blocked by 16 rows:
     //   T_i = (I + A'_ii)^-1 (16x16, one wave, forward substitution per column)
     //   X_i = T_i (diag(beta) B_i - sum_{k<i} A'_ik X_k)          (MFMA, hi+lo products)
-    // W and U are solved one after the other (128 columns each) to bound LDS.
+    // W and U are solved one after the other (128 columns each, one 16-column tile per wave).
     if (w == 0) {
         const int kb = l >> 4, ci = l & 15;
         float y[16];
@@ -171,101 +179,99 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(const float* __restrict__ 
 #pragma unroll
         for (int r = 0; r < 16; ++r) Td[kb][r][ci] = y[r];
     }
-    const int g = l >> 4, li = l & 15;
+    const int col = 16 * w + li;                 // this lane's column within the half
     for (int hf = 0; hf < 2; ++hf) {
-        for (int idx = tid; idx < 2 * C * XS / 8; idx += 256) ((u4*)&Xs[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
+        // right-hand sides of this lane's 16 (row, column) cells, V straight from global
+        float rhs[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = 16 * i + 4 * g + e;
+                float b;
+                if (hf == 0) b = expf(sG[t]) * ((float)Kx[0][t][col] + (float)Kx[1][t][col]);
+                else b = t < L ? co[(size_t)(t0 + t) * cts + 2 * qk + h * SD + col] : 0.f;
+                rhs[i][e] = sB[t] * b;
+            }
+        for (int idx = tid; idx < 2 * C * XS / 8; idx += PREP_THREADS) ((u4*)&Xs[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
         __syncthreads();
+#pragma unroll
         for (int i = 0; i < 4; ++i) {
-            // R = beta B_i - sum_{k<i} A'_ik X_k for this wave's two 16-column tiles
-            f4 acc[2];
+            // R = beta B_i - sum_{k<i} A'_ik X_k for this wave's 16-column tile
+            f4 acc;
 #pragma unroll
-            for (int nt2 = 0; nt2 < 2; ++nt2)
+            for (int e = 0; e < 4; ++e) acc[e] = rhs[i][e];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int t = 16 * i + 4 * g + e, col = 16 * (2 * w + nt2) + li;
-                    const float b = hf == 0 ? expf(sG[t]) * Kf[t][col] : Vf[t][col];
-                    acc[nt2][e] = sB[t] * b;
-                }
             for (int ks = 0; ks < (i + 1) / 2; ++ks) {
                 // A operand: -A'[16i + li][32ks + 8g + j], zero at and past column 16i
-                f4 a0, a1;
                 const int s0 = 32 * ks + 8 * g;
                 const float* arow = &Ap[16 * i + li][s0];
-                a0 = s0 < 16 * i ? -*(const f4*)arow : f4{0.f, 0.f, 0.f, 0.f};
-                a1 = s0 + 4 < 16 * i ? -*(const f4*)(arow + 4) : f4{0.f, 0.f, 0.f, 0.f};
+                const f4 a0 = s0 < 16 * i ? -*(const f4*)arow : f4{0.f, 0.f, 0.f, 0.f};
+                const f4 a1 = s0 + 4 < 16 * i ? -*(const f4*)(arow + 4) : f4{0.f, 0.f, 0.f, 0.f};
                 h8 ah, al;
                 split_hi_lo(a0, a1, ah, al);
-#pragma unroll
-                for (int nt2 = 0; nt2 < 2; ++nt2) {
-                    const int c0 = 16 * (2 * w + nt2);
-                    const _Float16* xh = &Xs[0][s0 + (li >> 2)][c0 + 4 * (li & 3)];
-                    const _Float16* xl = &Xs[1][s0 + (li >> 2)][c0 + 4 * (li & 3)];
-                    const h8 bh = cat_h4(lds_tr4(xh), lds_tr4(xh + 4 * XS));
-                    const h8 bl = cat_h4(lds_tr4(xl), lds_tr4(xl + 4 * XS));
-                    acc[nt2] = mfma16x16x32(ah, bh, acc[nt2]);
-                    acc[nt2] = mfma16x16x32(ah, bl, acc[nt2]);
-                    acc[nt2] = mfma16x16x32(al, bh, acc[nt2]);
-                }
+                const int c0 = 16 * w;
+                const _Float16* xh = &Xs[0][s0 + (li >> 2)][c0 + 4 * (li & 3)];
+                const _Float16* xl = &Xs[1][s0 + (li >> 2)][c0 + 4 * (li & 3)];
+                const h8 bh = cat_h4(lds_tr4(xh), lds_tr4(xh + 4 * XS));
+                const h8 bl = cat_h4(lds_tr4(xl), lds_tr4(xl + 4 * XS));
+                acc = mfma16x16x32(ah, bh, acc);
+                acc = mfma16x16x32(ah, bl, acc);
+                acc = mfma16x16x32(al, bh, acc);
             }
             // R -> LDS (hi/lo) so it can be the B operand of T_i R
 #pragma unroll
-            for (int nt2 = 0; nt2 < 2; ++nt2)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float v = acc[nt2][e];
-                    const _Float16 hi = (_Float16)v;
-                    const int col = 16 * (2 * w + nt2) + li;
-                    Rs[0][4 * g + e][col] = hi;
-                    Rs[1][4 * g + e][col] = (_Float16)(v - (float)hi);
-                }
+            for (int e = 0; e < 4; ++e) {
+                const float v = acc[e];
+                const _Float16 hi = (_Float16)v;
+                Rs[0][4 * g + e][col] = hi;
+                Rs[1][4 * g + e][col] = (_Float16)(v - (float)hi);
+            }
             __syncthreads();
-            // X_i = T_i R: K = 16 (k-groups g >= 2 are zero padding)
+            // X_i = T_i R: K = 16 (k-groups 2 and 3 are zero padding)
             h8 th = {}, tl = {};
             if (g < 2) split_hi_lo(*(const f4*)&Td[i][li][8 * g], *(const f4*)&Td[i][li][8 * g + 4], th, tl);
-            f4 xo[2];
-#pragma unroll
-            for (int nt2 = 0; nt2 < 2; ++nt2) {
-                const int c0 = 16 * (2 * w + nt2);
-                // transpose reads run with the whole wave active (the instruction exchanges data
-                // between lanes); k-groups 2 and 3 read rows 0..7 again and are zeroed after
-                const int gr = g & 1;
-                const _Float16* rh = &Rs[0][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
-                const _Float16* rl = &Rs[1][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
-                h8 bh = cat_h4(lds_tr4(rh), lds_tr4(rh + 4 * XS));
-                h8 bl = cat_h4(lds_tr4(rl), lds_tr4(rl + 4 * XS));
-                if (g >= 2) { bh = h8{}; bl = h8{}; }
-                f4 z = {0.f, 0.f, 0.f, 0.f};
-                z = mfma16x16x32(th, bh, z);
-                z = mfma16x16x32(th, bl, z);
-                z = mfma16x16x32(tl, bh, z);
-                xo[nt2] = z;
-            }
+            // transpose reads run with the whole wave active; k-groups 2 and 3 reread rows 0..7
+            const int gr = g & 1, c0 = 16 * w;
+            const _Float16* rh = &Rs[0][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
+            const _Float16* rl = &Rs[1][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
+            h8 bh = cat_h4(lds_tr4(rh), lds_tr4(rh + 4 * XS));
+            h8 bl = cat_h4(lds_tr4(rl), lds_tr4(rl + 4 * XS));
+            if (g >= 2) { bh = h8{}; bl = h8{}; }
+            f4 z = {0.f, 0.f, 0.f, 0.f};
+            z = mfma16x16x32(th, bh, z);
+            z = mfma16x16x32(th, bl, z);
+            z = mfma16x16x32(tl, bh, z);
             // X_i -> scratch (W f16 / U f32) and -> LDS (hi/lo) for the later block rows
 #pragma unroll
-            for (int nt2 = 0; nt2 < 2; ++nt2)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int t = 16 * i + 4 * g + e, col = 16 * (2 * w + nt2) + li;
-                    const float v = xo[nt2][e];
-                    const _Float16 hi = (_Float16)v;
-                    Xs[0][t][col] = hi;
-                    Xs[1][t][col] = (_Float16)(v - (float)hi);
-                    if (hf == 0) ((_Float16*)(rec + OFF_W))[t * SD + col] = hi;
-                    else ((float*)(rec + OFF_U))[t * SD + col] = v;
-                }
+            for (int e = 0; e < 4; ++e) {
+                const int t = 16 * i + 4 * g + e;
+                const float v = z[e];
+                const _Float16 hi = (_Float16)v;
+                Xs[0][t][col] = hi;
+                Xs[1][t][col] = (_Float16)(v - (float)hi);
+                if (hf == 0) ((_Float16*)(rec + OFF_W))[t * SD + col] = hi;
+                else ((float*)(rec + OFF_U))[t * SD + col] = v;
+            }
             __syncthreads();
         }
     }
 }
 
 // ------------------------------------------------------------------------------------------------
+constexpr int NCB = SD / 32;   // 32-column blocks of the state per head
 __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ scr, int nch, float* __restrict__ state,
-                                                      float* __restrict__ out, int ots, int nt) {
+                                                      float* __restrict__ out, int ots, int nt, int nv) {
     constexpr int SP = SD + 8, VP = C + 8;
     __shared__ __align__(16) _Float16 S0T[2][32][SP];   // [hi|lo][state column][key dim]
     __shared__ __align__(16) _Float16 VpT[2][32][VP];   // [hi|lo][state column][token]
 
-    const int cb = blockIdx.x, h = blockIdx.y;
+    // XCD-aware placement: workgroups are dealt to the 8 XCDs round-robin by linear id, so id L
+    // runs on XCD L % 8. All column blocks of one head go to the same XCD (head = xcd + 8*(slot/4))
+    // and re-read that head's chunk records from the XCD's L2 instead of HBM.
+    const int L_id = blockIdx.x, xcd = L_id & 7, slot = L_id >> 3;
+    const int h = xcd + 8 * (slot / NCB), cb = slot % NCB;
+    if (h >= nv) return;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
     const int n0 = 32 * cb;
     float* sh = state + (size_t)h * SD * SD;
@@ -280,14 +286,36 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
 #pragma unroll
             for (int i = 0; i < 4; ++i) st[mi][ni][i] = sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li];
 
-    for (int c = 0; c < nch; ++c) {
+    // Operands of one chunk as this lane reads them; the next chunk's are loaded into registers
+    // while the current chunk is computed.
+    struct ChunkOps { h8 w[4], qg[4], aqk[2], kt[2][2]; float u[2][4]; float gc; };
+    auto load_ops = [&](int c, ChunkOps& o) {
         const char* rec = scr + ((size_t)h * nch + c) * REC;
         const _Float16* W = (const _Float16*)(rec + OFF_W);
         const _Float16* QG = (const _Float16*)(rec + OFF_QG);
         const _Float16* KT = (const _Float16*)(rec + OFF_KT);
         const _Float16* AQK = (const _Float16*)(rec + OFF_AQK);
         const float* U = (const float*)(rec + OFF_U);
-        const float gc = *(const float*)(rec + OFF_GC);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            o.w[ks] = ld_h8(W + (16 * w + li) * SD + 32 * ks + 8 * g);
+            o.qg[ks] = ld_h8(QG + (16 * w + li) * SD + 32 * ks + 8 * g);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            o.aqk[ks] = ld_h8(AQK + (16 * w + li) * C + 32 * ks + 8 * g);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) o.kt[ks][mi] = ld_h8(KT + (16 * (2 * w + mi) + li) * C + 32 * ks + 8 * g);
+        }
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o.u[ni][i] = U[(16 * w + 4 * g + i) * SD + n0 + 16 * ni + li];
+        o.gc = *(const float*)(rec + OFF_GC);
+    };
+    // one chunk of the scan with its operands already in registers
+    auto step = [&](int c, const ChunkOps& cur) {
+        const float gc = cur.gc;
         const int t0 = c * C, L = min(C, nt - t0);
 
         // ---- S0 -> LDS as hi/lo, transposed to [column][key dim]
@@ -308,7 +336,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         f4 vp[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const h8 a = ld_h8(W + (16 * w + li) * SD + 32 * ks + 8 * g);
+            const h8 a = cur.w[ks];
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
                 vp[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
@@ -320,7 +348,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = 16 * w + 4 * g + i, col = 16 * ni + li;
-                const float v = U[t * SD + n0 + col] - vp[ni][i];
+                const float v = cur.u[ni][i] - vp[ni][i];
                 const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
                 VpT[0][col][t] = hi;
                 VpT[1][col][t] = lo;
@@ -330,7 +358,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         f4 oa[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const h8 a = ld_h8(QG + (16 * w + li) * SD + 32 * ks + 8 * g);
+            const h8 a = cur.qg[ks];
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
                 oa[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
@@ -339,7 +367,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         }
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const h8 a = ld_h8(AQK + (16 * w + li) * C + 32 * ks + 8 * g);
+            const h8 a = cur.aqk[ks];
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
                 oa[ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
@@ -362,7 +390,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi) {
-                const h8 a = ld_h8(KT + (16 * (2 * w + mi) + li) * C + 32 * ks + 8 * g);
+                const h8 a = cur.kt[ks][mi];
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni) {
                     st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
@@ -370,6 +398,20 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
                 }
             }
         __syncthreads();
+    };
+    // operands are loaded two chunks ahead (three register sets, loop unrolled by three)
+    ChunkOps o0, o1, o2;
+    load_ops(0, o0);
+    if (nch > 1) load_ops(1, o1);
+    for (int c = 0; c < nch; c += 3) {
+        if (c + 2 < nch) load_ops(c + 2, o2);
+        step(c, o0);
+        if (c + 1 >= nch) break;
+        if (c + 3 < nch) load_ops(c + 3, o0);
+        step(c + 1, o1);
+        if (c + 2 >= nch) break;
+        if (c + 4 < nch) load_ops(c + 4, o1);
+        step(c + 2, o2);
     }
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
@@ -384,10 +426,11 @@ hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const f
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
                               hipStream_t st) {
     const int nch = (nt + C - 1) / C;
-    gdn_chunk_prep<<<dim3(nch, nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, nt, nk, (char*)scratch);
+    gdn_chunk_prep<<<dim3(nch, nv), PREP_THREADS, 0, st>>>(co, cts, br, ar, bts, dt, a, nt, nk, (char*)scratch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    gdn_chunk_scan<<<dim3(SD / 32, nv), 256, 0, st>>>((const char*)scratch, nch, state, out, ots, nt);
+    // linear grid of 8 * NCB * ceil(nv / 8) workgroups, mapped to (head, column block) in-kernel
+    gdn_chunk_scan<<<dim3(8 * NCB * ((nv + 7) / 8)), 256, 0, st>>>((const char*)scratch, nch, state, out, ots, nt, nv);
     return hipGetLastError();
 }
 
