@@ -82,6 +82,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-chunk", type=int, default=0, help="keys per split for decode (0 = library policy)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain device copies of 256 MiB (reference reading for the FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
@@ -120,16 +121,19 @@ def main():
     kcs = [kc0.clone() for _ in range(NSETS)]
     vcs = [vc0.clone() for _ in range(NSETS)]
     out = torch.empty(4, NH * HD, device=dev)
-    chunk = 128   # decode split: 128 keys -> the 8-wave partial kernel, 64 splits per KV head
+    # decode split: the library's automatic choice unless --decode-chunk overrides it
+    chunk = args.decode_chunk or 128
     part_bytes = ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, chunk)
-    part = torch.empty(max(part_bytes, ops.attn_scratch_bytes(ctx - 4, 4, NH, NKV, HD, ops.KERNEL_SPLITK, 64)),
+    part = torch.empty(max(part_bytes, ops.attn_scratch_bytes(ctx - 4, 4, NH, NKV, HD, ops.KERNEL_SPLITK, 64),
+                           ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, 64)),
                        dtype=torch.uint8, device=dev)
     scale = 1.0 / 16
 
     def decode_step(i, q=q1, nt=1):
         call("it_attn_f16_ex", q.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,
              ctx - nt, HD, NH, NKV, nt, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(),
-             ops.KERNEL_AUTO, 0, stream_of())
+             ops.KERNEL_AUTO if nt > 1 or not args.decode_chunk else ops.KERNEL_SPLITK, 0 if nt > 1 else args.decode_chunk,
+             stream_of())
 
     def decode_partials(i):
         call("it_attn_partials", q1.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,

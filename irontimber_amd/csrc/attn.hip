@@ -58,18 +58,28 @@ constexpr int VST = HD + 16;   // LDS row stride (halves) of the V tile: 544 B, 
 // WAVES waves per workgroup; a tile is KT = 16*WAVES keys (each wave scores 16 keys). The decode
 // shape (8 rows) uses 8 waves / 128-key tiles so one workgroup covers a whole split with all of
 // its loads in flight at once; wider row blocks use 4 waves / 64-key tiles to fit LDS.
+// Scores are kept in log2 units (q.k * scale * log2 e) so the exponentials are single v_exp_f32;
+// the MFMA rows of the q hi and q lo halves land in separate LDS score rows and are summed when
+// read (no cross-lane shuffle); the softmax gives each wave whole rows and reduces with DPP.
+constexpr float LOG2E_F = 1.4426950408889634f;
+constexpr float LN2_F = 0.6931471805599453f;
+
 template <int NB, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
     const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     int kvd, int pos0, int nh, int nkv, int nt, float scale, float* __restrict__ part, int chunk, int smax) {
     constexpr int ROWS = 8 * NB, KT = 16 * WAVES, NTH = 64 * WAVES;
-    constexpr int CPR = KT / 8;              // softmax threads per row (8 columns each)
     constexpr int NTW = 16 / WAVES;          // 16-dim output tiles per wave
+    constexpr int VPL = KT / 64;             // softmax values per lane
+    constexpr int RPW = ROWS / WAVES;        // softmax rows per wave (1 for decode)
+    static_assert(ROWS % WAVES == 0, "rows spread evenly over waves");
     __shared__ __align__(16) _Float16 Ks[KT * KST];
     __shared__ __align__(16) _Float16 Vs[KT * VST];
     __shared__ __align__(16) _Float16 Qs[2][ROWS][KST];   // [hi|lo][row][dim]
-    __shared__ __align__(16) float Ps[ROWS][KT + 4];
+    __shared__ __align__(16) float Ps[2][ROWS][KT + 4];   // scores of the q-hi / q-lo MFMA rows
     __shared__ float alpha_s[ROWS];
+    __shared__ int lim_s[ROWS];                            // row sees keys < lim (0 for padding rows)
+    __shared__ int qoff_s[ROWS];                           // row's q offset (floats), -1 for padding
 
     const int s = blockIdx.x, kh = blockIdx.y, rg = blockIdx.z;
     const int G = nh / nkv, R = nt * G, r0 = rg * ROWS;
@@ -78,9 +88,18 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
     const int p0 = s * chunk;
     const int pend = min(p0 + chunk, pos0 + tmax + 1);
     if (p0 >= pend) return;  // no row of this group sees these keys; the combine never reads them
+    const float sc2 = scale * LOG2E_F;
 
-    const int sr = tid / CPR, c8 = tid % CPR;   // softmax role: row sr, columns 8*c8..8*c8+7
-    float m_run = -INFINITY, l_run = 0.0f;
+    if (tid < ROWS) {
+        const int rr = r0 + tid;
+        const bool ok = rr < R;
+        const int t = ok ? rr / G : 0;
+        lim_s[tid] = ok ? pos0 + t + 1 : 0;
+        qoff_s[tid] = ok ? t * qts + (kh * G + rr % G) * 2 * HD : -1;
+    }
+    float m_run[RPW], l_run[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) { m_run[j] = -INFINITY; l_run[j] = 0.f; }
     f4 acc[NB][NTW];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -104,16 +123,19 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
         for (int i = 0; i < 8; ++i)
             vr[i] = *(const u4*)(vc + (size_t)min(kb + lrow + (NTH / 32) * i, pend - 1) * kvd + head_off + 8 * lch);
     };
+    __syncthreads();                                 // lim_s / qoff_s
     constexpr int QIT = (ROWS * HD / 8 + NTH - 1) / NTH;
     f4 qx[QIT][2];
 #pragma unroll
     for (int it = 0; it < QIT; ++it) {
         const int idx = tid + NTH * it;          // 8-float piece: row idx/32, dims 8*(idx%32)
-        const int row = idx >> 5, rr = r0 + row;
         qx[it][0] = qx[it][1] = f4{0.f, 0.f, 0.f, 0.f};
-        if (idx < ROWS * HD / 8 && rr < R) {
-            const float* src = q + (size_t)(rr / G) * qts + (size_t)(kh * G + rr % G) * 2 * HD + 8 * (idx & 31);
-            qx[it][0] = ld_f4(src); qx[it][1] = ld_f4(src + 4);
+        if (idx < ROWS * HD / 8) {
+            const int qo = qoff_s[idx >> 5];
+            if (qo >= 0) {
+                const float* src = q + qo + 8 * (idx & 31);
+                qx[it][0] = ld_f4(src); qx[it][1] = ld_f4(src + 4);
+            }
         }
     }
     load_k(p0);
@@ -135,8 +157,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) *(u4*)&Ks[(lrow + (NTH / 32) * i) * KST + 8 * lch] = kr[i];
         __syncthreads();
-        // ---- scores for every row block
-        const int pk = kb + 16 * w + (l & 15);
+        // ---- scores for every row block: MFMA rows 0-7 = q_hi, 8-15 = q_lo of the block's 8 rows
         const _Float16* krow = &Ks[(16 * w + (l & 15)) * KST + 8 * (l >> 4)];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -150,41 +171,44 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
 #pragma unroll
                 for (int ks = 0; ks < 8; ++ks) sacc = mfma16x16x32(qa[ks], kbv[ks], sacc);
             }
+            // lane l holds MFMA rows 4*(l>>4)+i: rows 0-7 (l < 32) are q_hi, rows 8-15 are q_lo
+            const int half = l >> 5;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float tot = sacc[i] + __shfl_xor(sacc[i], 32);
-                if (l < 32) {
-                    const int rloc = 4 * (l >> 4) + i;
-                    const int rq = r0 + b * 8 + rloc;
-                    const bool valid = rq < R && pk < pos0 + rq / G + 1;
-                    Ps[b * 8 + rloc][16 * w + (l & 15)] = valid ? tot * scale : -INFINITY;
-                }
+                const int rloc = (4 * (l >> 4) + i) & 7;
+                Ps[half][b * 8 + rloc][16 * w + (l & 15)] = sacc[i];
             }
         }
         __syncthreads();
-        // ---- online softmax update (ROWS*CPR is a multiple of 64: whole waves take part)
-        if (sr < ROWS) {
-            f4 x0 = *(const f4*)&Ps[sr][8 * c8], x1 = *(const f4*)&Ps[sr][8 * c8 + 4];
-            float mx = fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])),
-                             fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3])));
+        // ---- online softmax: wave w owns rows w, w + WAVES, ...; lane covers VPL key columns
 #pragma unroll
-            for (int m = 1; m < CPR; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
-            const float mnew = fmaxf(m_run, mx);
-            const float a = (mnew == -INFINITY) ? 1.0f : expf(m_run - mnew);
+        for (int j = 0; j < RPW; ++j) {
+            const int row = w + WAVES * j;
+            const int lim = lim_s[row];
+            float x[VPL];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < VPL; ++v) {
+                const int col = l + 64 * v;
+                const bool ok = kb + col < lim;
+                x[v] = ok ? (Ps[0][row][col] + Ps[1][row][col]) * sc2 : -INFINITY;
+                mx = fmaxf(mx, x[v]);
+            }
+            mx = wave_max(mx);
+            const float mnew = fmaxf(m_run[j], mx);
+            const float a = (mnew == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run[j] - mnew);
+            const float msub = (mnew == -INFINITY) ? 0.0f : mnew;
             float sum = 0.f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                x0[j] = (x0[j] == -INFINITY) ? 0.f : expf(x0[j] - mnew);
-                x1[j] = (x1[j] == -INFINITY) ? 0.f : expf(x1[j] - mnew);
-                sum += x0[j] + x1[j];
+            for (int v = 0; v < VPL; ++v) {
+                x[v] = __builtin_amdgcn_exp2f(x[v] - msub);
+                sum += x[v];
+                Ps[0][row][l + 64 * v] = x[v];
             }
-#pragma unroll
-            for (int m = 1; m < CPR; m <<= 1) sum += __shfl_xor(sum, m);
-            l_run = l_run * a + sum;
-            m_run = mnew;
-            *(f4*)&Ps[sr][8 * c8] = x0;
-            *(f4*)&Ps[sr][8 * c8 + 4] = x1;
-            if (c8 == 0) alpha_s[sr] = a;
+            sum = wave_sum(sum);
+            l_run[j] = l_run[j] * a + sum;
+            m_run[j] = mnew;
+            if (l == 0) alpha_s[row] = a;
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) *(u4*)&Vs[(lrow + (NTH / 32) * i) * VST + 8 * lch] = vr[i];
@@ -202,7 +226,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
 #pragma unroll
                 for (int n = 0; n < NTW; ++n) acc[b][n][i] *= a;
             }
-            const float* prow = &Ps[b * 8 + (si & 7)][0];
+            const float* prow = &Ps[0][b * 8 + (si & 7)][0];
 #pragma unroll
             for (int ks = 0; ks < KT / 32; ++ks) {
                 h8 hi, lo;
@@ -218,28 +242,30 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
         }
         __syncthreads();
     }
-    // ---- write the partial records {m, l, 0, 0, o[256]}: stage o in LDS (reusing the K tile),
-    // then 16-byte coalesced stores of whole 1040-byte records
+    // ---- write the partial records {m, l, 0, 0, o[256]} (m in natural-log units): the P-hi and
+    // P-lo MFMA rows of O are summed across the two lane halves, staged in LDS (reusing the K
+    // tile), then stored as whole 1040-byte records with 16-byte stores
     float* Os = (float*)Ks;   // [ROWS][256]
+    static_assert(ROWS * HD * 4 <= KT * KST * 2, "O fits in the K tile");
     const int dw = (HD / WAVES) * w;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int n = 0; n < NTW; ++n) {
+        for (int n = 0; n < NTW; ++n)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float o = acc[b][n][i] + __shfl_xor(acc[b][n][i], 32);
                 if (l < 32) Os[(b * 8 + 4 * (l >> 4) + i) * HD + dw + 16 * n + (l & 15)] = o;
             }
-        }
-    }
-    if (sr < ROWS && c8 == 0) { Ps[sr][0] = m_run; Ps[sr][1] = l_run; }
+#pragma unroll
+    for (int j = 0; j < RPW; ++j)
+        if (l == 0) { Ps[1][w + WAVES * j][0] = m_run[j] * LN2_F; Ps[1][w + WAVES * j][1] = l_run[j]; }
     __syncthreads();
     for (int idx = tid; idx < ROWS * 65; idx += NTH) {
         const int row = idx / 65, c = idx % 65, rq = r0 + row;
         if (rq >= R) continue;
         const int t = rq / G, h = kh * G + rq % G;
-        const f4 v = c == 0 ? f4{Ps[row][0], Ps[row][1], 0.f, 0.f} : *(const f4*)&Os[row * HD + 4 * (c - 1)];
+        const f4 v = c == 0 ? f4{Ps[1][row][0], Ps[1][row][1], 0.f, 0.f} : *(const f4*)&Os[row * HD + 4 * (c - 1)];
         *(f4*)(part + ((size_t)(t * nh + h) * smax + s) * PART + 4 * c) = v;
     }
 }
@@ -248,31 +274,52 @@ __global__ __launch_bounds__(64 * WAVES) void attn_partial_kernel(
 // Merge the partials of (head h, token t): M = max m_s, den = sum l_s e^(m_s-M),
 // out = sum o_s e^(m_s-M) / den * sigmoid(gate). Same merge as kernels/src/lib.rs:722-740, spread
 // over the splits: workgroup (h, t, quarter of the 256 dims); thread = (split lane sg = tid/16,
-// 4 dims); the 16 split lanes reduce through LDS.
+// 4 dims). Each thread loads the m, l and o of its splits in one batch (one memory round trip),
+// the maxima and sums reduce through LDS.
+constexpr int COMB_SPL = 8;   // splits per split lane held in registers (larger ns loops)
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ q, int qts, int pos0, int nh,
                                                           const float* __restrict__ part, int chunk, int smax,
                                                           float* __restrict__ out, int ots) {
-    __shared__ float red_m[4];
+    __shared__ float red_m[16];
     __shared__ f4 red_o[16][16];
     __shared__ float red_d[16];
-    const int h = blockIdx.x, t = blockIdx.y, dq = blockIdx.z, tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+    const int h = blockIdx.x, t = blockIdx.y, dq = blockIdx.z, tid = threadIdx.x;
     const int n = pos0 + t + 1, ns = (n + chunk - 1) / chunk;
     const float* base = part + (size_t)(t * nh + h) * smax * PART;
-    float M = -INFINITY;
-    for (int s = tid; s < ns; s += 256) M = fmaxf(M, base[(size_t)s * PART]);
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) M = fmaxf(M, __shfl_xor(M, m));
-    if (l == 0) red_m[w] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
     const int sg = tid >> 4, dl = tid & 15, d0 = 64 * dq + 4 * dl;
-    float den = 0.f;
+    float M = -INFINITY, den = 0.f;
     f4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int s = sg; s < ns; s += 16) {
-        const float* rec = base + (size_t)s * PART;
-        const float wgt = expf(rec[0] - M);
-        den += rec[1] * wgt;
-        o += ld_f4(rec + 4 + d0) * wgt;
+    for (int s0 = 0; s0 < ns; s0 += 16 * COMB_SPL) {
+        float mv[COMB_SPL], lv[COMB_SPL];
+        f4 ov[COMB_SPL];
+#pragma unroll
+        for (int j = 0; j < COMB_SPL; ++j) {
+            const int s = s0 + sg + 16 * j;
+            mv[j] = -INFINITY; lv[j] = 0.f; ov[j] = f4{0.f, 0.f, 0.f, 0.f};
+            if (s < ns) {
+                const float* rec = base + (size_t)s * PART;
+                mv[j] = rec[0]; lv[j] = rec[1]; ov[j] = ld_f4(rec + 4 + d0);
+            }
+        }
+        float mloc = M;
+#pragma unroll
+        for (int j = 0; j < COMB_SPL; ++j) mloc = fmaxf(mloc, mv[j]);
+        // group maximum over the 16 split lanes (lanes with the same dl share nothing else)
+        if (dl == 0) red_m[sg] = mloc;
+        __syncthreads();
+        float Mn = red_m[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) Mn = fmaxf(Mn, red_m[j]);
+        __syncthreads();
+        const float r = (M == -INFINITY) ? 0.f : expf(M - Mn);
+        den *= r; o *= r;
+#pragma unroll
+        for (int j = 0; j < COMB_SPL; ++j) {
+            const float wgt = mv[j] == -INFINITY ? 0.f : expf(mv[j] - Mn);
+            den += lv[j] * wgt;
+            o += ov[j] * wgt;
+        }
+        M = Mn;
     }
     red_o[sg][dl] = o;
     if (dl == 0) red_d[sg] = den;
@@ -281,12 +328,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
         f4 acc = red_o[0][tid];
         float dd = red_d[0];
         for (int j = 1; j < 16; ++j) { acc += red_o[j][tid]; dd += red_d[j]; }
-        const int dd0 = 64 * dq + 4 * tid;
-        const f4 g = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + dd0);
+        const f4 gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + 64 * dq + 4 * tid);
         f4 r;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r[j] = acc[j] / dd * sigmoidf_(g[j]);
-        *(f4*)(out + (size_t)t * ots + (size_t)h * HD + dd0) = r;
+        for (int j = 0; j < 4; ++j) r[j] = acc[j] / dd * sigmoidf_(gt[j]);
+        *(f4*)(out + (size_t)t * ots + (size_t)h * HD + 64 * dq + 4 * tid) = r;
     }
 }
 

@@ -58,6 +58,35 @@ __device__ __forceinline__ h8 to_h8(f4 x0, f4 x1) {
     return r;
 }
 
+// Wave-wide max / sum of a float: DPP within 16-lane rows (xor 1, xor 2 by quad_perm, then the
+// half-row and row mirrors), then the four row results through readlane. Every lane returns the
+// full result; no LDS round trip.
+template <int CTRL> __device__ __forceinline__ float dppc(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dppc<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dppc<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dppc<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dppc<0x140>(v));   // row_mirror
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dppc<0xB1>(v);
+    v += dppc<0x4E>(v);
+    v += dppc<0x141>(v);
+    v += dppc<0x140>(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (a + b) + (c + d);
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
