@@ -29,9 +29,10 @@ constexpr float RESCALE_SLACK = 8.0f;   // log2 units
 }
 
 // LDS tiles are unpadded 512-byte rows of 32 16-byte chunks; logical chunk j of row r lives at
-// physical chunk j ^ swz(r). swz spreads 8 consecutive rows over 8 chunk positions (conflict-free
-// K operand reads) and the 4 rows x 2 chunks of one transpose read over 8 positions.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// physical chunk j ^ swz(r). With 512-byte rows a chunk's bank group is (chunk mod 16), so swz
+// gives 16 consecutive rows 16 distinct values (K operand reads: one row per lane) and 4
+// consecutive rows distinct chunk pairs (V transpose reads: 4 rows x 2 chunks per 16 lanes).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1) | (((r >> 3) & 1) << 3); }
 
 // Issue the direct-to-LDS loads of one 64-row tile: wave w moves rows 16w..16w+15, two rows
 // (64 lanes x 16 bytes) per instruction, each lane fetching the logical chunk that belongs at its
@@ -101,20 +102,26 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     float m_run = -INFINITY, l_run = 0.f;
 
     // Per-lane LDS offsets (halves). K operand: row c (+32 per block), logical chunk 2ks+hh.
-    int koff[4];
+    int koff[8];
     {
         const int sw = swz(c);          // swz(32b + c) == swz(c)
 #pragma unroll
-        for (int k2 = 0; k2 < 4; ++k2) koff[k2] = c * HD + 8 * ((2 * k2 + hh) ^ sw);
+        for (int k2 = 0; k2 < 8; ++k2) koff[k2] = c * HD + 8 * ((2 * k2 + hh) ^ sw);
     }
     // V transpose read: source lane provides row 4hh + vrow (+16ks, +8 for the second half) and
     // logical column 32db + vcol; swz of those rows is (vrow << 1) | hh for every ks.
-    int voff[2];
+    int voff[4][2];
     {
         const int vrow = (l & 15) >> 2, vcol = 16 * ((l >> 4) & 1) + 4 * (l & 3);
-        const int sv = (vrow << 1) | hh, jj = vcol >> 3, inner = vcol & 7;
+        const int jj = vcol >> 3, inner = vcol & 7;
 #pragma unroll
-        for (int par = 0; par < 2; ++par) voff[par] = (4 * hh + vrow) * HD + 8 * ((4 * par + jj) ^ sv) + inner;
+        for (int half = 0; half < 2; ++half) {
+            // rows 16ks + 4hh + vrow (+8 for the second transpose read): swz depends on bit 3 too
+            const int r = 4 * hh + vrow + 8 * half;
+            const int sv = swz(r);
+#pragma unroll
+            for (int par = 0; par < 4; ++par) voff[par][half] = r * HD + 8 * ((4 * par + jj) ^ sv) + inner;
+        }
     }
 
     // one 64-key tile: K/V hold tile kb (issued one tile earlier); tile kb+BN streams into Kn/Vn
@@ -128,7 +135,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
             tile_to_lds(vc, kvd, head_off, kb + BN, kend, Vn, w, l);
         }
         // ---- S^T = K Q^T for two 32-key blocks. Logical chunk 2ks+hh of row rr sits at physical
-        // chunk 8*(ks/4) + ((2*(ks%4) + hh) ^ swz(rr)): four per-lane offsets plus immediates.
+        // chunk 16*(ks/8) + ((2*(ks%8) + hh) ^ swz(rr)): eight per-lane offsets plus immediates.
         f16v sc[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) sc[b] = f16v{};
@@ -136,7 +143,17 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         for (int ks = 0; ks < 16; ++ks)
 #pragma unroll
             for (int b = 0; b < 2; ++b)
-                sc[b] = mfma32x32x16(ld_h8(K + (32 * b) * HD + koff[ks & 3] + 64 * (ks >> 2)), qb[ks], sc[b]);
+                sc[b] = mfma32x32x16(ld_h8(K + (32 * b) * HD + koff[ks & 7] + 128 * (ks >> 3)), qb[ks], sc[b]);
+        // keep four operand reads in flight ahead of the matrix cores
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int i = 0; i < 28; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         // ---- causal mask (only tiles that reach past the first row's diagonal)
         if (kb + BN > kfull) {
 #pragma unroll
@@ -182,15 +199,25 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         lsum += __shfl_xor(lsum, 32);
         l_run += lsum;
         // ---- O^T += V^T P^T: k-step ks covers keys 16ks + {4hh + 0..3, 8 + 4hh + 0..3}; the
-        // transpose-read address is voff[db & 1] plus immediates
+        // transpose-read address is voff[db & 3][half] plus immediates
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
-                const _Float16* v = V + voff[db & 1] + (16 * ks) * HD + 64 * (db >> 1);
-                const h8 va = cat_h4(lds_tr4(v), lds_tr4(v + 8 * HD));
+                const _Float16* v = V + (16 * ks) * HD + 128 * (db >> 2);
+                const h8 va = cat_h4(lds_tr4(v + voff[db & 3][0]), lds_tr4(v + voff[db & 3][1]));
                 o[db] = mfma32x32x16(va, pb[ks], o[db]);
             }
+        // two operands (four transpose reads) in flight ahead of the matrix cores
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int i = 0; i < 30; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     };
     for (int kb = 0; kb < kend; kb += 2 * BN) {
         tile(kb, K0, V0, K1, V1);
