@@ -122,7 +122,7 @@ def main():
     vcs = [vc0.clone() for _ in range(NSETS)]
     out = torch.empty(4, NH * HD, device=dev)
     # decode split: the library's automatic choice unless --decode-chunk overrides it
-    chunk = args.decode_chunk or 128
+    chunk = args.decode_chunk or 64
     part_bytes = ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, chunk)
     part = torch.empty(max(part_bytes, ops.attn_scratch_bytes(ctx - 4, 4, NH, NKV, HD, ops.KERNEL_SPLITK, 64),
                            ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, 64)),

@@ -79,7 +79,7 @@ int it_attn_f16_ex(const float* q, int q_tok_stride, const uint16_t* kc, const u
  * split s) is 260 floats {m, l, 0, 0, o[256]} at part + ((t*nh + h)*smax + s)*260 with
  * smax = ceil((pos0+nt)/chunk): m = max score, l = sum exp(score - m), o = sum exp(score - m) v
  * over the split's keys visible to token t (kernels/src/lib.rs:753-798). Records of splits a token
- * cannot see are left untouched. A sequence-sharded caller can exchange these records and run
+ * cannot see are never read (they are left untouched or written as {-inf, 0, 0, 0, 0...}). A sequence-sharded caller can exchange these records and run
  * it_attn_combine locally.
  *   it_attn_partials: part must hold it_attn_scratch_bytes_ex(pos0,nt,hd,nh,nkv,1,chunk) bytes.
  *   it_attn_combine : out = merge of the records of splits 0..ceil((pos0+t+1)/chunk)-1, times

@@ -33,12 +33,13 @@ constexpr size_t PART_WORDS = 260;
 constexpr int KERNEL_AUTO = 0, KERNEL_SPLITK = 1, KERNEL_FLASH = 2;
 constexpr size_t AUTO_SCRATCH_CAP = size_t(256) << 20;   // keep automatic split-K scratch under 256 MiB
 
-// Keys per split for the split-K kernel when the caller leaves it to us.
-// Decode-shaped calls (at most 8 query rows per KV head) start at 128-key splits, which run the
-// 8-wave partial kernel; wider row blocks start at 64.
+// Keys per split for the split-K kernel when the caller leaves it to us: one 64-key tile per
+// workgroup (ctx 8192 -> 128 splits per KV head, 256 workgroups for two KV heads), doubled only
+// when the partial records would outgrow the scratch cap.
 int auto_chunk(int pos0, int nt, int nh, int nkv) {
+    (void)nkv;
     const size_t total = (size_t)pos0 + nt;
-    int c = (nt * (nh / nkv) <= 8) ? 128 : 64;
+    int c = 64;
     while (c < (1 << 20) && (size_t)nt * nh * ((total + c - 1) / c) * PART_WORDS * 4 > AUTO_SCRATCH_CAP) c *= 2;
     return c;
 }
@@ -88,6 +89,7 @@ size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int k
     if (nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv) return 0;
     if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
     if (kernel == KERNEL_FLASH) return 0;
+    if (kernel != KERNEL_SPLITK) return 0;
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
     return splitk_scratch(pos0, nt, nh, chunk);
 }
@@ -135,12 +137,13 @@ int it_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t
 
 int it_attn_combine(const float* q, int qts, const float* part, int pos0, int hd, int nh, int nt, int chunk, float* out,
                     int ots, void* stream) {
+    // the merge only needs the q-head of each record; any nkv dividing nh indexes them the same way
     if (hd != HD || nh <= 0 || nt <= 0 || pos0 < 0) return fail("it_attn_combine: bad geometry");
     if (chunk <= 0 || chunk % 64 != 0) return fail("it_attn_combine: chunk %d must be a positive multiple of 64", chunk);
     if (!q || !part || !out || !aligned16(q) || !aligned16(part) || !aligned16(out))
         return fail("it_attn_combine: buffers must be non-null and 16-byte aligned");
     if (qts % 4 != 0 || ots % 4 != 0) return fail("it_attn_combine: token strides must be multiples of 4");
-    return check(it::launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, (hipStream_t)stream),
+    return check(it::launch_attn_combine(q, qts, part, pos0, nh, 1, nt, chunk, out, ots, (hipStream_t)stream),
                  "it_attn_combine");
 }
 

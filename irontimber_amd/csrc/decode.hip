@@ -1,0 +1,408 @@
+// Split-K partials for decode and MTP verify: short dependency chain after the loads land.
+//
+// Reference behaviour: src/cpu.rs:260-272 (math), kernels/src/lib.rs:753-798 (split-K partial
+// record {m, l, pad, pad, o[256]} per (token, head, split), merged by the combine kernel).
+//
+// One workgroup = one KV head x one split of `chunk` keys x up to 8*NB query rows (rows r = t*G + g,
+// token t, head g of the KV group: they all read the same K/V, so each key is loaded once for all
+// of them). 4 waves; keys are processed in 64-key tiles, wave w scoring keys 16w..16w+15.
+//
+//   K      : loaded straight into MFMA A-operand registers (key row = lane & 15, 8 dims per lane
+//            group), never staged in LDS.
+//   V      : copied to LDS by the DMA path (global_load_lds, 16 bytes a lane, two 512-byte rows an
+//            instruction) with its 16-byte chunks XOR-swizzled by row, read back with the LDS
+//            transpose read as the P.V B operand.
+//   q      : staged once in LDS as f16 hi + lo planes (hi + lo == q to ~2^-22), the B operand of
+//            S^T = K q^T: MFMA columns 0-7 carry q_hi, 8-15 q_lo of the block's 8 rows, so the two
+//            halves of one score sit in lanes c and c ^ 8 and one DPP row rotate sums them.
+//   softmax: in registers. Each lane holds 4 keys of one row; the row maximum of the tile needs the
+//            other 48 keys, exchanged through a 4x8-float LDS table (barrier A). Running sums stay
+//            per wave and are added once at the end (every wave uses the same running max).
+//   P.V    : P (hi + lo f16 rows, as for q) goes to a small LDS plane in MFMA A layout (barrier B,
+//            which also covers V); wave w then owns output dims 64w..64w+63 for all 64 keys.
+// Per tile that is two barriers; the K/V/q loads of the first tile are all in flight before any
+// of them is consumed, and later tiles are prefetched while P.V runs.
+#include "common.h"
+#include "internal.h"
+
+namespace it {
+
+namespace {
+
+constexpr int HD = 256;
+constexpr int PART = 260;
+constexpr int TK = 64;          // keys per tile
+constexpr int QST = HD + 8;     // q plane row stride (halves)
+constexpr int PST = TK + 8;     // P plane row stride (halves): 144 bytes
+constexpr float LOG2E_F = 1.4426950408889634f;
+constexpr float LN2_F = 0.6931471805599453f;
+constexpr int COMB_SPL = 8;     // splits per merge split lane per batch of loads
+
+#define IT_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
+
+// V tile chunk swizzle. The transpose read of one 16-lane group covers rows r0..r0+3 (r0 % 4 == 0)
+// x 32 bytes (two chunks of one 128-byte line); unswizzled, the four 512-byte-apart rows would hit
+// the same banks. XOR-ing the chunk index with 2*(r & 3) moves the four rows to four different
+// 32-byte bank groups of the same 128 bytes and keeps the chunk pair together.
+__device__ __forceinline__ int vswz(int r) { return (r & 3) << 1; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// DMA one 64-key V tile (rows kb .. kb+63 of KV head `head_off`, clamped to kend-1) into LDS.
+// Wave w copies rows 16w .. 16w+15, two rows per instruction; lane l lands at LDS chunk (l & 31) of
+// its row, so it fetches logical chunk (l & 31) ^ vswz(row).
+__device__ __forceinline__ void v_tile_to_lds(const uint16_t* __restrict__ vc, int kvd, size_t head_off, int kb,
+                                              int kend, _Float16* lds, int w, int l) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = 16 * w + 2 * i + (l >> 5);
+        const int j = (l & 31) ^ vswz(r);
+        const uint16_t* g = vc + (size_t)min(kb + r, kend - 1) * kvd + head_off + 8 * j;
+        __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + (16 * w + 2 * i) * HD), 16, 0, 0);
+    }
+}
+
+// K rows as the A operand of S^T = K q^T: lane l holds key kb + 16w + (l & 15), dims 32ks + 8*(l >> 4).
+__device__ __forceinline__ void k_tile_to_regs(const uint16_t* __restrict__ kc, int kvd, size_t head_off, int kb,
+                                               int kend, u4 (&kr)[8], int w, int l) {
+    const uint16_t* g = kc + (size_t)min(kb + 16 * w + (l & 15), kend - 1) * kvd + head_off + 8 * (l >> 4);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) kr[ks] = *(const u4*)(g + 32 * ks);
+}
+
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+}  // namespace
+
+template <int NB>
+__device__ __forceinline__ void decode_partial(const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc,
+                                               const uint16_t* __restrict__ vc, int kvd, int pos0, int nh, int nkv,
+                                               int nt, float scale, float* __restrict__ part, int chunk, int smax,
+                                               int s, int kh, int rg) {
+    constexpr int ROWS = 8 * NB;
+    __shared__ __align__(16) _Float16 V0[TK * HD];
+    __shared__ __align__(16) _Float16 V1[TK * HD];
+    __shared__ __align__(16) _Float16 Qs[2][ROWS][QST];   // [hi|lo][row][dim]
+    __shared__ __align__(16) _Float16 Ps[NB][16][PST];    // rows 0-7 P_hi, 8-15 P_lo of a row block
+    __shared__ float Mx[4][ROWS];                          // per-wave tile maxima, then per-wave sums
+    __shared__ float Al[ROWS];                             // per-row rescale of the tile
+
+    const int G = nh / nkv, R = nt * G, r0 = rg * ROWS;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, c = l & 15, g = l >> 4;
+    const int tmax = (min(R, r0 + ROWS) - 1) / G;
+    const int p0 = s * chunk;
+    const int pend = min(p0 + chunk, pos0 + tmax + 1);
+    if (p0 >= pend) return;   // no row of this group sees these keys; the combine never reads them
+    const float sc2 = scale * LOG2E_F;
+    const size_t head_off = (size_t)kh * HD;
+
+    // ---- issue every load of the first tile: q rows (raw f32), K rows (registers), V rows (DMA)
+    constexpr int QPT = ROWS * HD / 8 / 256;   // 8-float q pieces per thread (NB)
+    f4 qx[QPT][2];
+#pragma unroll
+    for (int it = 0; it < QPT; ++it) {
+        // unconditional loads (padding rows read row R-1 and are zeroed below) keep the wait for q
+        // from also waiting for the K and V loads issued after it
+        const int idx = tid + 256 * it, rr = min(r0 + (idx >> 5), R - 1);
+        const float* src = q + (size_t)(rr / G) * qts + (size_t)(kh * G + rr % G) * 2 * HD + 8 * (idx & 31);
+        qx[it][0] = ld_f4(src);
+        qx[it][1] = ld_f4(src + 4);
+    }
+    u4 kr[8];
+    k_tile_to_regs(kc, kvd, head_off, p0, pend, kr, w, l);
+    v_tile_to_lds(vc, kvd, head_off, p0, pend, V0, w, l);
+#pragma unroll
+    for (int it = 0; it < QPT; ++it) {
+        const int idx = tid + 256 * it, row = idx >> 5, d0 = 8 * (idx & 31);
+        h8 hi, lo;
+        if (r0 + row >= R) qx[it][0] = qx[it][1] = f4{0.f, 0.f, 0.f, 0.f};
+        split_hi_lo(qx[it][0], qx[it][1], hi, lo);
+        *(h8*)&Qs[0][row][d0] = hi;
+        *(h8*)&Qs[1][row][d0] = lo;
+    }
+
+    // per-lane row facts for the S^T columns: lane column c is row 8b + (c & 7) of block b
+    int lim[NB];
+    float m_run[NB], l_run[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int rr = r0 + 8 * b + (c & 7);
+        lim[b] = rr < R ? pos0 + rr / G + 1 : 0;
+        m_run[b] = -INFINITY;
+        l_run[b] = 0.f;
+    }
+    f4 acc[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc[b][n] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // transpose-read source offsets (halves) of this lane inside a V tile, for key rows
+    // 32ks + 8g + 4e' + (c >> 2) and the 16-dim column block of output tile n of wave w
+    int voff[2][4];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int rlo = 8 * g + 4 * e + (c >> 2);   // + 32ks, which keeps vswz (multiple of 4)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            const int col = 64 * w + 16 * n + 4 * (c & 3);
+            voff[e][n] = rlo * HD + 8 * ((col >> 3) ^ vswz(rlo)) + (col & 7);
+        }
+    }
+
+    __syncthreads();   // q planes
+    h8 qb[NB][8];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) qb[b][ks] = ld_h8(&Qs[c >> 3][8 * b + (c & 7)][32 * ks + 8 * g]);
+
+    int it = 0;
+    for (int kb = p0; kb < pend; kb += TK, ++it) {
+        const _Float16* Vt = (it & 1) ? V1 : V0;
+        // ---- scores S^T (rows = this wave's 16 keys, columns = q hi/lo rows)
+        f4 sacc[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            sacc[b] = f4{0.f, 0.f, 0.f, 0.f};
+            if (r0 + 8 * b < R) {   // wave-uniform
+#pragma unroll
+                for (int ks = 0; ks < 8; ++ks)
+                    sacc[b] = mfma16x16x32(__builtin_bit_cast(h8, kr[ks]), qb[b][ks], sacc[b]);
+            }
+        }
+        // ---- hi + lo, scale to log2 units, mask; wave-local maxima
+        float x[NB][4];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int lb = min(lim[b], pend);
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = sacc[b][i] + dpp_f<0x128>(sacc[b][i]);   // row_ror:8 -> column c ^ 8
+                const int key = kb + 16 * w + 4 * g + i;
+                x[b][i] = key < lb ? v * sc2 : -INFINITY;
+                mx = fmaxf(mx, x[b][i]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            if (g == 0 && c < 8) Mx[w][8 * b + c] = mx;
+        }
+        __syncthreads();   // A: tile maxima
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int row = 8 * b + (c & 7);
+            const float mt = fmaxf(fmaxf(Mx[0][row], Mx[1][row]), fmaxf(Mx[2][row], Mx[3][row]));
+            const float mnew = fmaxf(m_run[b], mt);
+            const float a = (mnew == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run[b] - mnew);
+            const float msub = (mnew == -INFINITY) ? 0.0f : mnew;
+            float p[4], sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                p[i] = __builtin_amdgcn_exp2f(x[b][i] - msub);
+                sum += p[i];
+            }
+            sum += __shfl_xor(sum, 16);
+            sum += __shfl_xor(sum, 32);
+            l_run[b] = l_run[b] * a + sum;
+            m_run[b] = mnew;
+            h4 ph;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 hi = (_Float16)p[i];
+                ph[i] = c < 8 ? hi : (_Float16)(p[i] - (float)hi);
+            }
+            *(h4*)&Ps[b][c][16 * w + 4 * g] = ph;
+            if (w == 0 && g == 0 && c < 8) Al[row] = a;
+        }
+        IT_WAIT_VMCNT(0);   // this tile's V
+        __syncthreads();    // B: P planes, alpha, V tile
+        // prefetch the next tile (K registers are free, the other V buffer was last read two
+        // barriers ago)
+        if (kb + TK < pend) {
+            k_tile_to_regs(kc, kvd, head_off, kb + TK, pend, kr, w, l);
+            v_tile_to_lds(vc, kvd, head_off, kb + TK, pend, (it & 1) ? V0 : V1, w, l);
+        }
+        // ---- O = diag(alpha) O + P V over output dims 64w .. 64w+63
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (r0 + 8 * b >= R) continue;   // wave-uniform
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float a = Al[8 * b + ((4 * g + i) & 7)];
+#pragma unroll
+                for (int n = 0; n < 4; ++n) acc[b][n][i] *= a;
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const h8 pa = ld_h8(&Ps[b][c][32 * ks + 8 * g]);
+#pragma unroll
+                for (int n = 0; n < 4; ++n) {
+                    const h8 vb = cat_h4(lds_tr4(Vt + 32 * ks * HD + voff[0][n]), lds_tr4(Vt + 32 * ks * HD + voff[1][n]));
+                    acc[b][n] = mfma16x16x32(pa, vb, acc[b][n]);
+                }
+            }
+        }
+    }
+
+    // ---- records {m (natural log units), l, 0, 0, o[256]}: sums of the per-wave running sums,
+    // P_hi and P_lo halves of O added across the two lane halves, stored straight from registers
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+        if (g == 0 && c < 8) Mx[w][8 * b + c] = l_run[b];
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[b][n][i] += __shfl_xor(acc[b][n][i], 32);
+        if (l < 32) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rr = r0 + 8 * b + 4 * g + i;
+                if (rr < R) {
+                    float* rec = part + ((size_t)((rr / G) * nh + kh * G + rr % G) * smax + s) * PART + 4 + 64 * w + c;
+#pragma unroll
+                    for (int n = 0; n < 4; ++n) rec[16 * n] = acc[b][n][i];
+                }
+            }
+        }
+    }
+    if (w == 0 && l < ROWS) {
+        const int rr = r0 + l;
+        float mrow = m_run[0];
+#pragma unroll
+        for (int b = 1; b < NB; ++b)
+            if ((l >> 3) == b) mrow = m_run[b];
+        if (rr < R) {
+            const float lsum = (Mx[0][l] + Mx[1][l]) + (Mx[2][l] + Mx[3][l]);
+            *(f4*)(part + ((size_t)((rr / G) * nh + kh * G + rr % G) * smax + s) * PART) =
+                f4{mrow * LN2_F, lsum, 0.f, 0.f};
+        }
+    }
+}
+
+template <int NB>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, int qts,
+                                                          const uint16_t* __restrict__ kc,
+                                                          const uint16_t* __restrict__ vc, int kvd, int pos0, int nh,
+                                                          int nkv, int nt, float scale, float* __restrict__ part,
+                                                          int chunk, int smax) {
+    decode_partial<NB>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax, blockIdx.x, blockIdx.y,
+                       blockIdx.z);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Merge of the partial records of one query row over its visible splits, for one quarter of the
+// 256 output dims: M = max m_s, den = sum l_s e^(m_s-M), out = sum o_s e^(m_s-M) / den * sigmoid(gate)
+// (kernels/src/lib.rs:722-740). Thread = (split lane sg = tid/16, 4 dims); each thread loads the
+// headers and its dims of up to 8 splits in one batch of loads before using any of them, and the
+// maxima and sums reduce through LDS.
+__device__ __forceinline__ void decode_merge(const float* __restrict__ q, int qts, int pos0, int nh, int nkv,
+                                             int nt, const float* __restrict__ part, int chunk, int smax,
+                                             float* __restrict__ out, int ots, int rr, int kh, int dq) {
+    __shared__ float red_m[16];
+    __shared__ f4 red_o[16][16];
+    __shared__ float red_d[16];
+    const int G = nh / nkv, R = nt * G, tid = threadIdx.x;
+    const bool live = rr < R;
+    const int t = live ? rr / G : 0, h = live ? kh * G + rr % G : 0;
+    const int sg = tid >> 4, dl = tid & 15, d0 = 64 * dq + 4 * dl;
+    f4 gt = {0.f, 0.f, 0.f, 0.f};
+    if (live && tid < 16) gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + 64 * dq + 4 * tid);
+    if (live) {
+        const int n = pos0 + t + 1, ns = (n + chunk - 1) / chunk;
+        const float* base = part + (size_t)(t * nh + h) * smax * PART;
+        float M = -INFINITY, den = 0.f;
+        f4 o = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < ns; s0 += 16 * COMB_SPL) {
+            f4 hv[COMB_SPL], ov[COMB_SPL];
+            // one batch of loads: record headers {m, l, 0, 0} and this thread's 4 dims
+#pragma unroll
+            for (int j = 0; j < COMB_SPL; ++j) {
+                const float* rec = base + (size_t)min(s0 + sg + 16 * j, ns - 1) * PART;
+                hv[j] = ld_f4(rec);
+                ov[j] = ld_f4(rec + 4 + d0);
+            }
+            float mloc = M;
+#pragma unroll
+            for (int j = 0; j < COMB_SPL; ++j) {
+                if (s0 + sg + 16 * j >= ns) hv[j][0] = -INFINITY;
+                mloc = fmaxf(mloc, hv[j][0]);
+            }
+            if (dl == 0) red_m[sg] = mloc;
+            __syncthreads();
+            float Mn = red_m[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) Mn = fmaxf(Mn, red_m[j]);
+            __syncthreads();
+            const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);
+            den *= r;
+            o *= r;
+#pragma unroll
+            for (int j = 0; j < COMB_SPL; ++j) {
+                const float wgt = hv[j][0] == -INFINITY ? 0.f : __expf(hv[j][0] - Mn);
+                den += hv[j][1] * wgt;
+                o += ov[j] * wgt;
+            }
+            M = Mn;
+        }
+        red_o[sg][dl] = o;
+        if (dl == 0) red_d[sg] = den;
+        __syncthreads();
+        if (tid < 16) {
+            f4 acc = red_o[0][tid];
+            float dd = red_d[0];
+            for (int j = 1; j < 16; ++j) { acc += red_o[j][tid]; dd += red_d[j]; }
+            f4 res;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) res[j] = acc[j] / dd * sigmoidf_(gt[j]);
+            *(f4*)(out + (size_t)t * ots + (size_t)h * HD + 64 * dq + 4 * tid) = res;
+        }
+    }
+}
+
+// Stand-alone merge of the records written by attn_decode_kernel (the two-launch split-K path and
+// it_attn_combine): workgroup (quarter dq, q-head h, token t).
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ q, int qts, int pos0, int nh,
+                                                          int nkv, int nt, const float* __restrict__ part, int chunk,
+                                                          int smax, float* __restrict__ out, int ots) {
+    const int dq = blockIdx.x, h = blockIdx.y, t = blockIdx.z, G = nh / nkv;
+    decode_merge(q, qts, pos0, nh, nkv, nt, part, chunk, smax, out, ots, t * G + h % G, h / G, dq);
+}
+
+hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
+                                       int pos0, int nh, int nkv, int nt, float scale, float* part, int chunk,
+                                       hipStream_t st) {
+    const int G = nh / nkv, R = nt * G;
+    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    const int rows = R <= 8 ? 8 : R <= 16 ? 16 : R <= 24 ? 24 : 32;
+    const dim3 grid(smax, nkv, (R + rows - 1) / rows);
+    switch (rows / 8) {
+        case 1: attn_decode_kernel<1><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax); break;
+        case 2: attn_decode_kernel<2><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax); break;
+        case 3: attn_decode_kernel<3><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax); break;
+        default: attn_decode_kernel<4><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nkv, int nt, int chunk,
+                               float* out, int ots, hipStream_t st) {
+    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    attn_combine_kernel<<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, nkv, nt, part, chunk, smax, out, ots);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
+                              int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
+                              hipStream_t st) {
+    hipError_t e = launch_attn_partials(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, st);
+    if (e != hipSuccess) return e;
+    return launch_attn_combine(q, qts, part, pos0, nh, nkv, nt, chunk, out, ots, st);
+}
+
+}  // namespace it

@@ -8,10 +8,9 @@ namespace it {
 
 hipError_t launch_kv_append(const float* k, const float* v, int sts, uint16_t* kc, uint16_t* vc, int pos0, int nt,
                             int kvd, int rtz, hipStream_t st);
-int attn_partial_rows_per_group(int nt, int G);
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                                 int nh, int nkv, int nt, float scale, float* part, int chunk, hipStream_t st);
-hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
+hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nkv, int nt, int chunk,
                                float* out, int ots, hipStream_t st);
 hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                               int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,

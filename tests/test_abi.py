@@ -93,8 +93,8 @@ def test_attn_rejects_bad_geometry_before_device_work():
 
 def test_scratch_bytes_policy():
     lib = _lib.lib()
-    # decode: split-K, C = 128 -> 64 splits of 260 words per head
-    assert lib.it_attn_scratch_bytes(8191, 1, 256, 16, 2) == 16 * 64 * 260 * 4
+    # decode: split-K, C = 64 -> 128 splits of 260 words per head
+    assert lib.it_attn_scratch_bytes(8191, 1, 256, 16, 2) == 16 * 128 * 260 * 4
     # MTP verify (32 rows per KV head): C = 64
     assert lib.it_attn_scratch_bytes(8188, 4, 256, 16, 2) == 4 * 16 * 128 * 260 * 4
     # whole-prompt prefill: flash, no scratch

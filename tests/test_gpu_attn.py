@@ -44,8 +44,8 @@ def test_ragged_and_group_shapes(dev, ctx, nt, nh, nkv):
 @pytest.mark.parametrize("nt", [1, 4])
 @pytest.mark.parametrize("chunk", [64, 128, 192, 256, 1024, 8192])
 def test_split_invariance(dev, chunk, nt):
-    """The result does not depend on how the keys are split (invariant of the LSE merge). nt=1 with
-    chunk % 128 == 0 runs the 8-wave decode kernel, the rest the 4-wave one."""
+    """The result does not depend on how the keys are split (invariant of the LSE merge); chunks
+    above 64 keys run several 64-key tiles per workgroup (online softmax across tiles)."""
     got, want = run_case(dev, 3, 2000, nt, kernel=ops.KERNEL_SPLITK, chunk=chunk)
     assert np.abs(got - want).max() <= 1e-5
 
