@@ -66,8 +66,11 @@ int it_attn_f16(const float* q, int q_tok_stride, const uint16_t* kc, const uint
 /* it_attn_f16 with the kernel choice exposed (the reference's BONSAI_PREFILL_ATTN / chunk policy,
  * src/vk/mod.rs:714-717 and 192-204):
  *   kernel 0 = automatic (what it_attn_f16 does), 1 = split-K partials + combine,
- *          2 = flash prefill (one pass, no scratch; needs nt >= 16).
- *   chunk  = keys per split for kernel 1 (multiple of 64), 0 = automatic.
+ *          2 = flash prefill (needs nt >= 16): one pass with no scratch, or, when one pass would
+ *          leave most of the GPU idle (a short chunk after a long context), key splits whose
+ *          partial records are merged like kernel 1's.
+ *   chunk  = keys per split (multiple of 64), 0 = automatic. For kernel 2 a chunk of at least
+ *          pos0 + nt means one pass.
  * it_attn_scratch_bytes_ex gives the scratch for the same choice. */
 size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int kernel, int chunk);
 int it_attn_f16_ex(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,

@@ -45,6 +45,13 @@ int auto_chunk(int pos0, int nt, int nh, int nkv) {
 }
 int auto_kernel(int nt) { return nt >= 16 ? KERNEL_FLASH : KERNEL_SPLITK; }
 
+// Keys per split of the flash kernel: the caller's chunk, or the library's choice when 0; 0 back
+// means one pass over all keys (no scratch).
+int flash_chunk(int pos0, int nt, int nh, int nkv, int chunk) {
+    const int c = chunk > 0 ? chunk : it::flash_split_chunk(pos0, nt, nh, nkv);
+    return (c > 0 && c < pos0 + nt) ? c : 0;
+}
+
 size_t splitk_scratch(int pos0, int nt, int nh, int chunk) {
     const size_t smax = ((size_t)pos0 + nt + chunk - 1) / chunk;
     return (size_t)nt * nh * smax * PART_WORDS * sizeof(float);
@@ -88,7 +95,10 @@ size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int k
     (void)hd;
     if (nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv) return 0;
     if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
-    if (kernel == KERNEL_FLASH) return 0;
+    if (kernel == KERNEL_FLASH) {
+        const int c = flash_chunk(pos0, nt, nh, nkv, chunk);
+        return c ? splitk_scratch(pos0, nt, nh, c) : 0;
+    }
     if (kernel != KERNEL_SPLITK) return 0;
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
     return splitk_scratch(pos0, nt, nh, chunk);
@@ -105,7 +115,18 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
     hipStream_t st = (hipStream_t)stream;
     if (kernel == KERNEL_FLASH) {
         if (nt < 16) return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
-        return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st), "it_attn_f16 (flash)");
+        if (chunk < 0 || chunk % 64 != 0) return fail("it_attn_f16: flash chunk %d must be a multiple of 64", chunk);
+        const int c = flash_chunk(pos0, nt, nh, nkv, chunk);
+        if (!c)
+            return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st),
+                         "it_attn_f16 (flash)");
+        const size_t need = splitk_scratch(pos0, nt, nh, c);
+        if (scratch_bytes < need || !scratch)
+            return fail("it_attn_f16: scratch of %zu bytes < %zu required (it_attn_scratch_bytes)", scratch_bytes, need);
+        if (!aligned16(scratch)) return fail("it_attn_f16: scratch must be 16-byte aligned");
+        return check(it::launch_attn_flash_split(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots,
+                                                 (float*)scratch, c, st),
+                     "it_attn_f16 (flash, key splits)");
     }
     if (kernel != KERNEL_SPLITK) return fail("it_attn_f16: unknown kernel %d", kernel);
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
@@ -137,13 +158,12 @@ int it_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t
 
 int it_attn_combine(const float* q, int qts, const float* part, int pos0, int hd, int nh, int nt, int chunk, float* out,
                     int ots, void* stream) {
-    // the merge only needs the q-head of each record; any nkv dividing nh indexes them the same way
     if (hd != HD || nh <= 0 || nt <= 0 || pos0 < 0) return fail("it_attn_combine: bad geometry");
     if (chunk <= 0 || chunk % 64 != 0) return fail("it_attn_combine: chunk %d must be a positive multiple of 64", chunk);
     if (!q || !part || !out || !aligned16(q) || !aligned16(part) || !aligned16(out))
         return fail("it_attn_combine: buffers must be non-null and 16-byte aligned");
     if (qts % 4 != 0 || ots % 4 != 0) return fail("it_attn_combine: token strides must be multiples of 4");
-    return check(it::launch_attn_combine(q, qts, part, pos0, nh, 1, nt, chunk, out, ots, (hipStream_t)stream),
+    return check(it::launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, (hipStream_t)stream),
                  "it_attn_combine");
 }
 

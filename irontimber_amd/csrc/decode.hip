@@ -296,82 +296,78 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
 }
 
 // ------------------------------------------------------------------------------------------------
-// Merge of the partial records of one query row over its visible splits, for one quarter of the
-// 256 output dims: M = max m_s, den = sum l_s e^(m_s-M), out = sum o_s e^(m_s-M) / den * sigmoid(gate)
-// (kernels/src/lib.rs:722-740). Thread = (split lane sg = tid/16, 4 dims); each thread loads the
-// headers and its dims of up to 8 splits in one batch of loads before using any of them, and the
-// maxima and sums reduce through LDS.
-__device__ __forceinline__ void decode_merge(const float* __restrict__ q, int qts, int pos0, int nh, int nkv,
-                                             int nt, const float* __restrict__ part, int chunk, int smax,
-                                             float* __restrict__ out, int ots, int rr, int kh, int dq) {
-    __shared__ float red_m[16];
-    __shared__ f4 red_o[16][16];
-    __shared__ float red_d[16];
-    const int G = nh / nkv, R = nt * G, tid = threadIdx.x;
-    const bool live = rr < R;
-    const int t = live ? rr / G : 0, h = live ? kh * G + rr % G : 0;
-    const int sg = tid >> 4, dl = tid & 15, d0 = 64 * dq + 4 * dl;
-    f4 gt = {0.f, 0.f, 0.f, 0.f};
-    if (live && tid < 16) gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + 64 * dq + 4 * tid);
-    if (live) {
-        const int n = pos0 + t + 1, ns = (n + chunk - 1) / chunk;
-        const float* base = part + (size_t)(t * nh + h) * smax * PART;
-        float M = -INFINITY, den = 0.f;
-        f4 o = {0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < ns; s0 += 16 * COMB_SPL) {
-            f4 hv[COMB_SPL], ov[COMB_SPL];
-            // one batch of loads: record headers {m, l, 0, 0} and this thread's 4 dims
-#pragma unroll
-            for (int j = 0; j < COMB_SPL; ++j) {
-                const float* rec = base + (size_t)min(s0 + sg + 16 * j, ns - 1) * PART;
-                hv[j] = ld_f4(rec);
-                ov[j] = ld_f4(rec + 4 + d0);
-            }
-            float mloc = M;
-#pragma unroll
-            for (int j = 0; j < COMB_SPL; ++j) {
-                if (s0 + sg + 16 * j >= ns) hv[j][0] = -INFINITY;
-                mloc = fmaxf(mloc, hv[j][0]);
-            }
-            if (dl == 0) red_m[sg] = mloc;
-            __syncthreads();
-            float Mn = red_m[0];
-#pragma unroll
-            for (int j = 1; j < 16; ++j) Mn = fmaxf(Mn, red_m[j]);
-            __syncthreads();
-            const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);
-            den *= r;
-            o *= r;
-#pragma unroll
-            for (int j = 0; j < COMB_SPL; ++j) {
-                const float wgt = hv[j][0] == -INFINITY ? 0.f : __expf(hv[j][0] - Mn);
-                den += hv[j][1] * wgt;
-                o += ov[j] * wgt;
-            }
-            M = Mn;
-        }
-        red_o[sg][dl] = o;
-        if (dl == 0) red_d[sg] = den;
-        __syncthreads();
-        if (tid < 16) {
-            f4 acc = red_o[0][tid];
-            float dd = red_d[0];
-            for (int j = 1; j < 16; ++j) { acc += red_o[j][tid]; dd += red_d[j]; }
-            f4 res;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) res[j] = acc[j] / dd * sigmoidf_(gt[j]);
-            *(f4*)(out + (size_t)t * ots + (size_t)h * HD + 64 * dq + 4 * tid) = res;
-        }
-    }
-}
-
-// Stand-alone merge of the records written by attn_decode_kernel (the two-launch split-K path and
-// it_attn_combine): workgroup (quarter dq, q-head h, token t).
+// Merge of the partial records of one query row over its visible splits:
+// M = max m_s, den = sum l_s e^(m_s-M), out = sum o_s e^(m_s-M) / den * sigmoid(gate)
+// (kernels/src/lib.rs:722-740). Thread = (split lane sg of SL, dim lane of 256/SL, 4 dims each).
+// Each thread loads the headers and its dims of up to 8 of its splits in one batch before using any
+// of them; the maxima and sums reduce through LDS.
+//   SL = 16: a quarter of the dims per workgroup (4 per row), for rows with many splits (decode).
+//   SL = 4 : the whole row per workgroup, for rows with at most 32 splits (chunked prefill).
+template <int SL>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ q, int qts, int pos0, int nh,
-                                                          int nkv, int nt, const float* __restrict__ part, int chunk,
-                                                          int smax, float* __restrict__ out, int ots) {
-    const int dq = blockIdx.x, h = blockIdx.y, t = blockIdx.z, G = nh / nkv;
-    decode_merge(q, qts, pos0, nh, nkv, nt, part, chunk, smax, out, ots, t * G + h % G, h / G, dq);
+                                                          const float* __restrict__ part, int chunk, int smax,
+                                                          float* __restrict__ out, int ots) {
+    constexpr int DLN = 256 / SL;            // dim lanes, 4 dims each
+    constexpr int DW = 4 * DLN;              // dims per workgroup
+    __shared__ float red_m[SL];
+    __shared__ f4 red_o[SL][DLN];
+    __shared__ float red_d[SL];
+    const int dq = blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+    const int sg = tid / DLN, dl = tid % DLN, d0 = DW * dq + 4 * dl;
+    const int n = pos0 + t + 1, ns = (n + chunk - 1) / chunk;
+    const float* base = part + (size_t)(t * nh + h) * smax * PART;
+    const f4 gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + d0);
+    float M = -INFINITY, den = 0.f;
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < ns; s0 += SL * COMB_SPL) {
+        const int nb = min(COMB_SPL, (ns - s0 - sg + SL - 1) / SL);   // this lane's splits in the batch
+        f2 hv[COMB_SPL];
+        f4 ov[COMB_SPL];
+        // branch-free batch: slots past the lane's count reload its last split and are masked after.
+        // Headers load as {m, l} only: a wider load with dead lanes lets the register allocator
+        // reuse them while the load is in flight, which costs a wait per load.
+#pragma unroll
+        for (int j = 0; j < COMB_SPL; ++j) {
+            const float* rec = base + (size_t)(s0 + sg + SL * max(0, min(j, nb - 1))) * PART;
+            hv[j] = *(const f2*)rec;
+            ov[j] = ld_f4(rec + 4 + d0);
+        }
+        float mloc = M;
+#pragma unroll
+        for (int j = 0; j < COMB_SPL; ++j) {
+            if (j >= nb) { hv[j] = f2{-INFINITY, 0.f}; ov[j] = f4{0.f, 0.f, 0.f, 0.f}; }
+            mloc = fmaxf(mloc, hv[j][0]);
+        }
+        if (dl == 0) red_m[sg] = mloc;
+        __syncthreads();
+        float Mn = red_m[0];
+#pragma unroll
+        for (int j = 1; j < SL; ++j) Mn = fmaxf(Mn, red_m[j]);
+        __syncthreads();
+        const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);
+        den *= r;
+        o *= r;
+#pragma unroll
+        for (int j = 0; j < COMB_SPL; ++j) {
+            const float wgt = hv[j][0] == -INFINITY ? 0.f : __expf(hv[j][0] - Mn);
+            den += hv[j][1] * wgt;
+            o += ov[j] * wgt;
+        }
+        M = Mn;
+    }
+    red_o[sg][dl] = o;
+    if (dl == 0) red_d[sg] = den;
+    __syncthreads();
+    if (sg == 0) {
+        f4 acc = red_o[0][dl];
+        float dd = red_d[0];
+#pragma unroll
+        for (int j = 1; j < SL; ++j) { acc += red_o[j][dl]; dd += red_d[j]; }
+        f4 res;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) res[j] = acc[j] / dd * sigmoidf_(gt[j]);
+        *(f4*)(out + (size_t)t * ots + (size_t)h * HD + d0) = res;
+    }
 }
 
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
@@ -390,10 +386,13 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
     return hipGetLastError();
 }
 
-hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nkv, int nt, int chunk,
+hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                float* out, int ots, hipStream_t st) {
     const int smax = (pos0 + nt + chunk - 1) / chunk;
-    attn_combine_kernel<<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, nkv, nt, part, chunk, smax, out, ots);
+    if (smax <= 32)
+        attn_combine_kernel<4><<<dim3(1, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
+    else
+        attn_combine_kernel<16><<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
     return hipGetLastError();
 }
 
@@ -402,7 +401,7 @@ hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const
                               hipStream_t st) {
     hipError_t e = launch_attn_partials(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, st);
     if (e != hipSuccess) return e;
-    return launch_attn_combine(q, qts, part, pos0, nh, nkv, nt, chunk, out, ots, st);
+    return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
 }
 
 }  // namespace it

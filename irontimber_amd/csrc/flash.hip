@@ -16,6 +16,12 @@
 //                         tiles (256 dims x 32 queries per wave).
 // K/V tiles go straight from HBM/L2 into double-buffered LDS (global_load_lds, 16 bytes per lane,
 // no registers): tile t+1 streams in while tile t is computed, one barrier per tile.
+//
+// Key-split form (part != null): workgroup (row tile, KV head, split s) covers keys
+// [s*chunk, (s+1)*chunk) only and writes the partial records {m, l, 0, 0, o[256]} of its rows
+// (same layout as the decode partials, kernels/src/lib.rs:753-798) for the merge kernel. Used when
+// one pass would leave most CUs idle: a 64-token chunk after a long context has only
+// 2 * ceil(64*G/128) row tiles.
 #include "common.h"
 #include "internal.h"
 
@@ -55,7 +61,8 @@ __device__ __forceinline__ void tile_to_lds(const uint16_t* __restrict__ src, in
 
 __global__ __launch_bounds__(256) void attn_flash_kernel(
     const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int kvd,
-    int pos0, int nh, int nkv, int nt, float scale, float* __restrict__ out, int ots) {
+    int pos0, int nh, int nkv, int nt, float scale, float* __restrict__ out, int ots, float* __restrict__ part,
+    int chunk, int smax) {
     // two K and two V buffers as distinct objects, so the compiler can tell that the loads
     // streaming into one buffer never alias the reads of the other (no conservative waits)
     __shared__ __align__(16) _Float16 K0[BN * HD];
@@ -73,28 +80,42 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     const int t = rvalid ? r / G : 0;
     const int head = kh * G + (rvalid ? r % G : 0);
     const int tmin = (rt * BM) / G, tmax = (min(R, rt * BM + BM) - 1) / G;
-    const int kend = pos0 + tmax + 1;                   // keys any row of the tile sees
+    const int split = blockIdx.z;
+    const int kb0 = part ? split * chunk : 0;           // this workgroup's keys: [kb0, kend)
+    const int kend = part ? min(pos0 + tmax + 1, kb0 + chunk) : pos0 + tmax + 1;
+    if (kb0 >= kend) return;                            // no row of the tile sees these keys
     const int kfull = pos0 + tmin + 1;                  // keys every row of the tile sees
     const int qlim = pos0 + t;                          // this row sees keys <= qlim
     const size_t head_off = (size_t)kh * HD;
 
     // q as the B operand: column = query c, k = dims 16*ks + 8*hh + 0..7, scaled into log2 units.
-    // All q loads are issued before the first tile's, and consumed after them all, so the
-    // prologue costs one memory round trip.
+    // Wave w reads its 32 rows whole (one 1 KB row per load instruction: a per-lane gather of the
+    // operand layout would touch 32 rows per instruction), then transposes them through its own
+    // 16 KB of the second K/V buffers, which the first tile does not use (rows XOR-swizzled by
+    // 16-byte chunk so the operand reads of 32 rows hit distinct banks). The q loads go out before
+    // the first tile's, so the prologue costs one memory round trip.
     h8 qb[16];
     {
         f4 qx[32];
-        const float* src = q + (size_t)t * qts + (size_t)head * 2 * HD + 8 * hh;
+        const int rw = rt * BM + 32 * w;
 #pragma unroll
-        for (int ks = 0; ks < 16; ++ks) {
-            qx[2 * ks] = rvalid ? ld_f4(src + 16 * ks) : f4{};
-            qx[2 * ks + 1] = rvalid ? ld_f4(src + 16 * ks + 4) : f4{};
+        for (int i = 0; i < 32; ++i) {
+            const int rr = min(rw + i, R - 1);   // rows past R: any valid row, zeroed below
+            qx[i] = ld_f4(q + (size_t)(rr / G) * qts + (size_t)(kh * G + rr % G) * 2 * HD + 4 * l);
         }
-        tile_to_lds(kc, kvd, head_off, 0, kend, K0, w, l);
-        tile_to_lds(vc, kvd, head_off, 0, kend, V0, w, l);
+        tile_to_lds(kc, kvd, head_off, kb0, kend, K0, w, l);
+        tile_to_lds(vc, kvd, head_off, kb0, kend, V0, w, l);
+        _Float16* qs = (w < 2 ? K1 : V1) + (w & 1) * (32 * HD);
         const float sc = scale * LOG2E;
 #pragma unroll
-        for (int ks = 0; ks < 16; ++ks) qb[ks] = to_h8(qx[2 * ks] * sc, qx[2 * ks + 1] * sc);
+        for (int i = 0; i < 32; ++i) {
+            const float si = rw + i < R ? sc : 0.0f;
+            const h4 hv = {(_Float16)(qx[i][0] * si), (_Float16)(qx[i][1] * si), (_Float16)(qx[i][2] * si),
+                           (_Float16)(qx[i][3] * si)};
+            *(h4*)(qs + i * HD + 8 * ((l >> 1) ^ i) + 4 * (l & 1)) = hv;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) qb[ks] = ld_h8(qs + c * HD + 8 * ((2 * ks + hh) ^ c));
     }
     f16v o[8];
 #pragma unroll
@@ -219,34 +240,80 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
 #pragma unroll
         for (int i = 0; i < 2; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     };
-    for (int kb = 0; kb < kend; kb += 2 * BN) {
+    for (int kb = kb0; kb < kend; kb += 2 * BN) {
         tile(kb, K0, V0, K1, V1);
         if (kb + BN < kend) tile(kb + BN, K1, V1, K0, V0);
     }
-    // ---- out = O / l * sigmoid(gate): lane holds query c, dims 32db + 8*(i/4) + 4hh + (i&3)
-    if (!rvalid) return;
-    const float inv = 1.0f / l_run;
-    const float* gate = q + (size_t)t * qts + (size_t)head * 2 * HD + HD;
-    float* dst = out + (size_t)t * ots + (size_t)head * HD;
+    // ---- epilogue. Lane (c, hh) holds O^T of query c at dims 32db + 8*(i/4) + 4hh + (i&3); wave w
+    // stages its 32 rows x 256 f32 in its own 32 KB of the tile buffers (16-byte chunk index XOR
+    // row, conflict-free), then writes whole rows: one 1 KB row per store instruction.
+    __syncthreads();   // every wave is done with the last tile
+    float* os = (float*)(w == 0 ? K0 : w == 1 ? K1 : w == 2 ? V0 : V1);
 #pragma unroll
     for (int db = 0; db < 8; ++db)
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
-            const int d0 = 32 * db + 8 * i4 + 4 * hh;
-            const f4 gt = ld_f4(gate + d0);
-            f4 v;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = o[db][4 * i4 + j] * inv * sigmoidf_(gt[j]);
-            *(f4*)(dst + d0) = v;
+            const int ch = (32 * db + 8 * i4 + 4 * hh) >> 2;   // 16-byte chunk of the row
+            *(f4*)(os + c * HD + 4 * (ch ^ c)) = f4{o[db][4 * i4], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
         }
+    __shared__ float ml[4][2][32];   // per wave: running max and sum of its 32 queries
+    if (hh == 0) { ml[w][0][c] = m_run; ml[w][1][c] = l_run; }
+    const int rw = rt * BM + 32 * w;
+    const int nrow = min(32, R - rw);
+    if (part) {
+        // partial records of (token, head, split): m in natural-log units of the scaled score
+#pragma unroll 4
+        for (int i = 0; i < nrow; ++i) {
+            const int rr = rw + i, tt = rr / G, hd = kh * G + rr % G;
+            float* rec = part + ((size_t)(tt * nh + hd) * smax + split) * 260;
+            if (l == 0) *(f4*)rec = f4{ml[w][0][i] * 0.6931471805599453f, ml[w][1][i], 0.f, 0.f};
+            *(f4*)(rec + 4 + 4 * l) = *(const f4*)(os + i * HD + 4 * (l ^ i));
+        }
+        return;
+    }
+    // out = O / l * sigmoid(gate), gate rows read whole as well
+#pragma unroll 4
+    for (int i = 0; i < nrow; ++i) {
+        const int rr = rw + i, tt = rr / G, hd = kh * G + rr % G;
+        const f4 gt = ld_f4(q + (size_t)tt * qts + (size_t)hd * 2 * HD + HD + 4 * l);
+        const f4 ov = *(const f4*)(os + i * HD + 4 * (l ^ i));
+        const float inv = 1.0f / ml[w][1][i];
+        f4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = ov[j] * inv * sigmoidf_(gt[j]);
+        *(f4*)(out + (size_t)tt * ots + (size_t)hd * HD + 4 * l) = v;
+    }
 }
 
 hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                              int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st) {
     const int R = nt * (nh / nkv);
     const dim3 grid((R + BM - 1) / BM, nkv);
-    attn_flash_kernel<<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots);
+    attn_flash_kernel<<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, nullptr, 0, 1);
     return hipGetLastError();
+}
+
+int flash_split_chunk(int pos0, int nt, int nh, int nkv) {
+    const int R = nt * (nh / nkv);
+    const int wgs = (R + BM - 1) / BM * nkv;
+    const int keys = pos0 + nt;
+    if (wgs >= 128 || keys <= 4 * BN) return 0;
+    const int want = (256 + wgs - 1) / wgs;                       // splits to reach ~256 workgroups
+    int chunk = ((keys + want - 1) / want + BN - 1) / BN * BN;    // multiple of the 64-key tile
+    chunk = chunk < 2 * BN ? 2 * BN : chunk;
+    return chunk >= keys ? 0 : chunk;
+}
+
+hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
+                                   int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
+                                   hipStream_t st) {
+    const int R = nt * (nh / nkv);
+    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    const dim3 grid((R + BM - 1) / BM, nkv, smax);
+    attn_flash_kernel<<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, part, chunk, smax);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
 }
 
 }  // namespace it

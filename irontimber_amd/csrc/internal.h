@@ -10,13 +10,18 @@ hipError_t launch_kv_append(const float* k, const float* v, int sts, uint16_t* k
                             int kvd, int rtz, hipStream_t st);
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                                 int nh, int nkv, int nt, float scale, float* part, int chunk, hipStream_t st);
-hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nkv, int nt, int chunk,
+hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                float* out, int ots, hipStream_t st);
 hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                               int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
                               hipStream_t st);
 hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                              int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st);
+
+int flash_split_chunk(int pos0, int nt, int nh, int nkv);
+hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
+                                   int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
+                                   hipStream_t st);
 
 hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,
                            int K, hipStream_t st);

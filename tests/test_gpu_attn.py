@@ -100,6 +100,18 @@ def test_flash_shapes(dev, ctx, nt, nh, nkv):
     assert (argmax_projection(got) == argmax_projection(want)).all()
 
 
+@pytest.mark.parametrize("chunk", [0, 64, 128, 192, 640, 4096, 8192])
+def test_flash_key_splits(dev, chunk):
+    """BASELINE config 3's first case (a 64-token chunk after 4096 cached positions, seed 2) through
+    the flash kernel with its keys split (chunk 0 = the library's choice, 8192 = one pass): every
+    split size gives the oracle's result within 2e-3 and the same downstream argmax."""
+    got, want = run_case(dev, 2, 4096 + 64, 64, kernel=ops.KERNEL_FLASH, chunk=chunk)
+    err = np.abs(got - want).max()
+    print(f"flash split chunk={chunk} max_abs={err:.3g}")
+    assert np.isfinite(got).all() and err <= TOL
+    assert (argmax_projection(got) == argmax_projection(want)).all()
+
+
 def test_flash_whole_prompt_8192(dev):
     """BASELINE config 3 at full size (seed 2): one 8192-token causal call. The oracle checks the
     first and last 16 tokens; the whole output equals 128 chunked 64-token calls (split-K path)
@@ -113,9 +125,10 @@ def test_flash_whole_prompt_8192(dev):
     for t0 in (0, T - 16):
         want = oracle.attn(q[t0:t0 + 16].reshape(16, -1), kb, vb, t0, 16, 2)
         assert np.abs(whole[t0:t0 + 16] - want).max() <= TOL
-    chunked = np.concatenate([host(ops.attn_f16(qd[c:c + 64].contiguous(), kc, vc, c, 16, 2, kernel=ops.KERNEL_SPLITK))
-                              for c in range(0, T, 64)])
-    assert np.abs(whole - chunked).max() <= TOL
+    for kernel in (ops.KERNEL_SPLITK, ops.KERNEL_AUTO):   # split-K partials; flash (key splits past ~2k)
+        chunked = np.concatenate([host(ops.attn_f16(qd[c:c + 64].contiguous(), kc, vc, c, 16, 2, kernel=kernel))
+                                  for c in range(0, T, 64)])
+        assert np.abs(whole - chunked).max() <= TOL
 
 
 def test_kv_append_rne_bits(dev):
