@@ -356,7 +356,7 @@ def main():
         "results": res,
         "roofline": {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "attn_partial_kernel<1, 8>", "kernel_us": round(part_us, 3),
+                     "kernel": "attn_decode_kernel<1>", "kernel_us": round(part_us, 3),
                      "bytes_per_launch": dbytes},
         "roofline_prefill": {"bound": "mfma", "achieved": prefill_tflops, "peak": F16_MFMA_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4)},
