@@ -55,6 +55,21 @@ __device__ __forceinline__ void tile_to_lds(const uint16_t* __restrict__ src, in
     }
 }
 
+// acc *= a for an MFMA accumulator tile held in AGPRs, element by element in place (read to a VGPR,
+// multiply, write back). Written out so the accumulators never need a VGPR home: with a plain
+// multiply in the (rare) rescale branch the register allocator keeps them in VGPRs at the branch
+// merge and the common path copies all of them to VGPRs and back on every tile.
+__device__ __forceinline__ void scale_acc(f16v& acc, float a) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float x = acc[i], t;
+        asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32_e32 %1, %2, %1\n\tv_accvgpr_write_b32 %0, %1"
+                     : "+a"(x), "=&v"(t)
+                     : "v"(a));
+        acc[i] = x;
+    }
+}
+
 // s_waitcnt immediates (gfx9 encoding): wait until at most N vector-memory ops are outstanding
 // (expcnt/lgkmcnt left unconstrained).
 #define IT_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
@@ -201,7 +216,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
             const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - mnew);
             l_run *= alpha;
 #pragma unroll
-            for (int db = 0; db < 8; ++db) o[db] *= alpha;
+            for (int db = 0; db < 8; ++db) scale_acc(o[db], alpha);
             m_run = mnew;
         }
         const float msub = (m_run == -INFINITY) ? 0.0f : m_run;
