@@ -42,16 +42,21 @@ __device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 
 
 // Issue the direct-to-LDS loads of one 64-row tile: wave w moves rows 16w..16w+15, two rows
 // (64 lanes x 16 bytes) per instruction, each lane fetching the logical chunk that belongs at its
-// physical slot.
-__device__ __forceinline__ void tile_to_lds(const uint16_t* __restrict__ src, int kvd, size_t head_off, int kb,
-                                            int kend, _Float16* lds, int w, int l) {
+// physical slot. Rows past kend-1 repeat row kend-1 (a tile issued past the end only refetches it).
+// Addresses are a uniform row base plus a 32-bit lane offset, so each instruction needs two VALU
+// ops; the chunk part of the offsets (cj, including the head's column) is computed once.
+__device__ __forceinline__ void tile_to_lds(const uint16_t* __restrict__ src, int kvd, int kb, int kend,
+                                            const int (&cj)[8], _Float16* lds, int w, int l) {
     typedef __attribute__((address_space(3))) void lds_void;
+    const int ts = min(kb, kend - 1);                      // first row of the tile, clamped
+    const char* base = (const char*)(src + (size_t)ts * kvd);
+    const int rmax = kend - 1 - ts;                        // >= 0
+    const unsigned rowb = 2u * (unsigned)kvd;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int r = 16 * w + 2 * i + (l >> 5);
-        const int j = (l & 31) ^ swz(r);
-        const uint16_t* g = src + (size_t)min(kb + r, kend - 1) * kvd + head_off + 8 * j;
-        __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds + (16 * w + 2 * i) * HD), 16, 0, 0);
+        const unsigned off = (unsigned)min(r, rmax) * rowb + (unsigned)cj[i];
+        __builtin_amdgcn_global_load_lds((const void*)(base + off), (lds_void*)(lds + (16 * w + 2 * i) * HD), 16, 0, 0);
     }
 }
 
@@ -109,6 +114,10 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     // 16 KB of the second K/V buffers, which the first tile does not use (rows XOR-swizzled by
     // 16-byte chunk so the operand reads of 32 rows hit distinct banks). The q loads go out before
     // the first tile's, so the prologue costs one memory round trip.
+    // byte offset of the logical chunk each lane's DMA slot holds, plus the KV head's column
+    int cj[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cj[i] = 2 * (int)head_off + 16 * ((l & 31) ^ swz(16 * w + 2 * i + (l >> 5)));
     h8 qb[16];
     {
         f4 qx[32];
@@ -118,8 +127,8 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
             const int rr = min(rw + i, R - 1);   // rows past R: any valid row, zeroed below
             qx[i] = ld_f4(q + (size_t)(rr / G) * qts + (size_t)(kh * G + rr % G) * 2 * HD + 4 * l);
         }
-        tile_to_lds(kc, kvd, head_off, kb0, kend, K0, w, l);
-        tile_to_lds(vc, kvd, head_off, kb0, kend, V0, w, l);
+        tile_to_lds(kc, kvd, kb0, kend, cj, K0, w, l);
+        tile_to_lds(vc, kvd, kb0, kend, cj, V0, w, l);
         _Float16* qs = (w < 2 ? K1 : V1) + (w & 1) * (32 * HD);
         const float sc = scale * LOG2E;
 #pragma unroll
@@ -166,10 +175,11 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         // done with the buffers that tile kb+BN goes into
         IT_WAIT_VMCNT(0);
         __syncthreads();
-        if (kb + BN < kend) {
-            tile_to_lds(kc, kvd, head_off, kb + BN, kend, Kn, w, l);
-            tile_to_lds(vc, kvd, head_off, kb + BN, kend, Vn, w, l);
-        }
+        // the next tile streams in while this one is computed; issued unconditionally (past the end
+        // it refetches row kend-1 into the idle buffers) so the loads stay in the same basic block
+        // as the S^T matrix ops and the scheduler can spread them between those
+        tile_to_lds(kc, kvd, kb + BN, kend, cj, Kn, w, l);
+        tile_to_lds(vc, kvd, kb + BN, kend, cj, Vn, w, l);
         // ---- S^T = K Q^T for two 32-key blocks. Logical chunk 2ks+hh of row rr sits at physical
         // chunk 16*(ks/8) + ((2*(ks%8) + hh) ^ swz(rr)): eight per-lane offsets plus immediates.
         f16v sc[2];
@@ -180,16 +190,18 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
 #pragma unroll
             for (int b = 0; b < 2; ++b)
                 sc[b] = mfma32x32x16(ld_h8(K + (32 * b) * HD + koff[ks & 7] + 128 * (ks >> 3)), qb[ks], sc[b]);
-        // keep four operand reads in flight ahead of the matrix cores
+        // eight operand reads in flight ahead of the matrix cores, and the next tile's 16 loads
+        // spread one per two matrix ops (each occupies the CU's load path for ~16 cycles per wave)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
-        for (int i = 0; i < 28; ++i) {
+        for (int i = 0; i < 24; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (i < 16) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         // ---- causal mask (only tiles that reach past the first row's diagonal)
         if (kb + BN > kfull) {
 #pragma unroll
@@ -244,16 +256,16 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
                 const h8 va = cat_h4(lds_tr4(v + voff[db & 3][0]), lds_tr4(v + voff[db & 3][1]));
                 o[db] = mfma32x32x16(va, pb[ks], o[db]);
             }
-        // two operands (four transpose reads) in flight ahead of the matrix cores
+        // four operands (eight transpose reads) in flight ahead of the matrix cores
 #pragma unroll
-        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
-        for (int i = 0; i < 30; ++i) {
+        for (int i = 0; i < 28; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     };
     for (int kb = kb0; kb < kend; kb += 2 * BN) {
         tile(kb, K0, V0, K1, V1);
@@ -262,6 +274,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     // ---- epilogue. Lane (c, hh) holds O^T of query c at dims 32db + 8*(i/4) + 4hh + (i&3); wave w
     // stages its 32 rows x 256 f32 in its own 32 KB of the tile buffers (16-byte chunk index XOR
     // row, conflict-free), then writes whole rows: one 1 KB row per store instruction.
+    IT_WAIT_VMCNT(0);  // the loads issued past the end land in the buffers staged below
     __syncthreads();   // every wave is done with the last tile
     float* os = (float*)(w == 0 ? K0 : w == 1 ? K1 : w == 2 ? V0 : V1);
 #pragma unroll
