@@ -75,6 +75,22 @@ __device__ __forceinline__ void scale_acc(f16v& acc, float a) {
     }
 }
 
+// max / sum over lanes l and l ^ 32 without going through LDS (a ds_bpermute would make the next
+// wait on LDS results also wait for every operand read in flight): v_permlane32_swap exchanges
+// the two lane halves between two registers, both holding v. Written out because the compiler
+// folds the builtin's two results when both inputs are the same value. The swap reads VGPRs just
+// written by VALU ops, which needs two wait states first.
+__device__ __forceinline__ float max_xor32(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+
 // s_waitcnt immediates (gfx9 encoding): wait until at most N vector-memory ops are outstanding
 // (expcnt/lgkmcnt left unconstrained).
 #define IT_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
@@ -221,12 +237,16 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[b][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = max_xor32(mx);
         const bool grow = mx > m_run + RESCALE_SLACK;
         if (__any(grow)) {
             const float mnew = grow ? mx : m_run;
             const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - mnew);
             l_run *= alpha;
+            // the previous tile's last P.V matrix ops may still be writing O: the reads below are
+            // inline assembly, which the compiler's hazard checks do not see into, so give them
+            // time to finish (> 18 wait states for a 16-pass op)
+            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");
 #pragma unroll
             for (int db = 0; db < 8; ++db) scale_acc(o[db], alpha);
             m_run = mnew;
@@ -244,8 +264,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
                     lsum += p;
                     pb[2 * b + kk][j] = (_Float16)p;
                 }
-        lsum += __shfl_xor(lsum, 32);
-        l_run += lsum;
+        l_run += lsum;   // this lane half's keys only; the halves are added after the loop
         // ---- O^T += V^T P^T: k-step ks covers keys 16ks + {4hh + 0..3, 8 + 4hh + 0..3}; the
         // transpose-read address is voff[db & 3][half] plus immediates
 #pragma unroll
@@ -285,6 +304,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
             *(f4*)(os + c * HD + 4 * (ch ^ c)) = f4{o[db][4 * i4], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
         }
     __shared__ float ml[4][2][32];   // per wave: running max and sum of its 32 queries
+    l_run = sum_xor32(l_run);
     if (hh == 0) { ml[w][0][c] = m_run; ml[w][1][c] = l_run; }
     const int rw = rt * BM + 32 * w;
     const int nrow = min(32, R - rw);
