@@ -27,6 +27,10 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the dominant decode kernel (attn_decode_kernel<1>, ctx 8192), from two
+# rocprofv3 --pmc runs of `bench.py --only decode` scaled by a 256 MiB copy's readings:
+# FETCH_SIZE 8,307.7 KiB x 2.0 + WRITE_SIZE 2,112 KiB x 1.0 (profiles/attn_decode_ctx8192.md).
+DECODE_TRAFFIC_BYTES = int((8307.7 * 2.0 + 2112.0 * 1.0) * 1024)
 F16_MFMA_PEAK_TFLOPS = 2500.0
 NH, NKV, HD = 16, 2, 256
 KVD = NKV * HD
@@ -83,6 +87,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-chunk", type=int, default=0, help="keys per split for decode (0 = library policy)")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "gdn"], default="all",
+                    help="run one section only (profiling runs); the JSON line then carries that section's figures")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain device copies of 256 MiB (reference reading for the FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
@@ -109,240 +115,248 @@ def main():
         return
     stream_of = lambda: torch.cuda.current_stream().cuda_stream
     res = {}
+    us_layer = value_gbs = part_gbs = part_us = prefill_tflops = None
+    chunk, NSETS, cpu = 64, 40, None
+    dbytes = decode_bytes(8192)
+    scale = 1.0 / 16
+    rnd = lambda v, n: None if v is None else round(v, n)
+    K, W = args.steps, args.warmup
 
     # ------------------------------------------------------------------ decode attention, ctx 8192
-    ctx = 8192
-    q_np, kb, vb = attn_inputs(1, ctx=ctx, nt=4)
-    q4 = torch.from_numpy(q_np.reshape(4, -1)).to(dev)
-    q1 = q4[3:4].contiguous()
-    NSETS = 40
-    kc0 = torch.from_numpy(kb.view(np.int16)).to(dev)
-    vc0 = torch.from_numpy(vb.view(np.int16)).to(dev)
-    kcs = [kc0.clone() for _ in range(NSETS)]
-    vcs = [vc0.clone() for _ in range(NSETS)]
-    out = torch.empty(4, NH * HD, device=dev)
-    # decode split: the library's automatic choice unless --decode-chunk overrides it
-    chunk = args.decode_chunk or 64
-    part_bytes = ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, chunk)
-    part = torch.empty(max(part_bytes, ops.attn_scratch_bytes(ctx - 4, 4, NH, NKV, HD, ops.KERNEL_SPLITK, 64),
-                           ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, 64)),
-                       dtype=torch.uint8, device=dev)
-    scale = 1.0 / 16
+    if args.only in ("all", "decode"):
+        ctx = 8192
+        q_np, kb, vb = attn_inputs(1, ctx=ctx, nt=4)
+        q4 = torch.from_numpy(q_np.reshape(4, -1)).to(dev)
+        q1 = q4[3:4].contiguous()
+        NSETS = 40
+        kc0 = torch.from_numpy(kb.view(np.int16)).to(dev)
+        vc0 = torch.from_numpy(vb.view(np.int16)).to(dev)
+        kcs = [kc0.clone() for _ in range(NSETS)]
+        vcs = [vc0.clone() for _ in range(NSETS)]
+        out = torch.empty(4, NH * HD, device=dev)
+        # decode split: the library's automatic choice unless --decode-chunk overrides it
+        chunk = args.decode_chunk or 64
+        part_bytes = ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, chunk)
+        part = torch.empty(max(part_bytes, ops.attn_scratch_bytes(ctx - 4, 4, NH, NKV, HD, ops.KERNEL_SPLITK, 64),
+                               ops.attn_scratch_bytes(ctx - 1, 1, NH, NKV, HD, ops.KERNEL_SPLITK, 64)),
+                           dtype=torch.uint8, device=dev)
+        scale = 1.0 / 16
 
-    def decode_step(i, q=q1, nt=1):
-        call("it_attn_f16_ex", q.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,
-             ctx - nt, HD, NH, NKV, nt, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(),
-             ops.KERNEL_AUTO if nt > 1 or not args.decode_chunk else ops.KERNEL_SPLITK, 0 if nt > 1 else args.decode_chunk,
-             stream_of())
+        def decode_step(i, q=q1, nt=1):
+            call("it_attn_f16_ex", q.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,
+                 ctx - nt, HD, NH, NKV, nt, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(),
+                 ops.KERNEL_AUTO if nt > 1 or not args.decode_chunk else ops.KERNEL_SPLITK, 0 if nt > 1 else args.decode_chunk,
+                 stream_of())
 
-    def decode_partials(i):
-        call("it_attn_partials", q1.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,
-             ctx - 1, HD, NH, NKV, 1, scale, part.data_ptr(), part.numel(), chunk, stream_of())
+        def decode_partials(i):
+            call("it_attn_partials", q1.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,
+                 ctx - 1, HD, NH, NKV, 1, scale, part.data_ptr(), part.numel(), chunk, stream_of())
 
-    # correctness guard on the benchmarked path (eager vs graph replays)
-    decode_step(0)
-    torch.cuda.synchronize()
-    ref_out = out[:1].clone()
+        # correctness guard on the benchmarked path (eager vs graph replays)
+        decode_step(0)
+        torch.cuda.synchronize()
+        ref_out = out[:1].clone()
 
-    # headline: exactly K steps in the timed region (warmup W untimed), graph of K steps
-    K, W = args.steps, args.warmup
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for i in range(W):
-            decode_step(i)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s):
-        for i in range(K):
-            decode_step(i)
-    g.replay()   # untimed replay (graph upload)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(s):
-        e0.record(s)
-        g.replay()
-        e1.record(s)
-    torch.cuda.synchronize()
-    total_ms = e0.elapsed_time(e1)
-    assert torch.equal(out[:1], ref_out), "graph replay changed the decode result"
-    us_layer = total_ms * 1000.0 / K
-    dbytes = decode_bytes(ctx)
-    value_gbs = dbytes / (us_layer * 1e-6) / 1e9
-    res["decode_ctx8192_us_per_layer"] = round(us_layer, 3)
-    res["decode_ctx8192_GBs"] = round(value_gbs, 1)
-    log(f"decode ctx8192: {us_layer:.2f} us/layer, {value_gbs:.0f} GB/s")
+        # headline: exactly K steps in the timed region (warmup W untimed), graph of K steps
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(W):
+                decode_step(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(K):
+                decode_step(i)
+        g.replay()   # untimed replay (graph upload)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        total_ms = e0.elapsed_time(e1)
+        assert torch.equal(out[:1], ref_out), "graph replay changed the decode result"
+        us_layer = total_ms * 1000.0 / K
+        dbytes = decode_bytes(ctx)
+        value_gbs = dbytes / (us_layer * 1e-6) / 1e9
+        res["decode_ctx8192_us_per_layer"] = round(us_layer, 3)
+        res["decode_ctx8192_GBs"] = round(value_gbs, 1)
+        log(f"decode ctx8192: {us_layer:.2f} us/layer, {value_gbs:.0f} GB/s")
 
-    # dominant kernel alone: the split-K partial kernel, K launches per graph
-    ms_part = graph_time_ms(torch, lambda: [decode_partials(i) for i in range(K)], reps=3)
-    part_us = ms_part * 1000.0 / K
-    part_gbs = dbytes / (part_us * 1e-6) / 1e9
-    log(f"decode partial kernel: {part_us:.2f} us, {part_gbs:.0f} GB/s")
+        # dominant kernel alone: the split-K partial kernel, K launches per graph
+        ms_part = graph_time_ms(torch, lambda: [decode_partials(i) for i in range(K)], reps=3)
+        part_us = ms_part * 1000.0 / K
+        part_gbs = dbytes / (part_us * 1e-6) / 1e9
+        log(f"decode partial kernel: {part_us:.2f} us, {part_gbs:.0f} GB/s")
 
-    # MTP verify: 4 query positions attending 8189..8192 keys
-    ms = graph_time_ms(torch, lambda: [decode_step(i, q4, 4) for i in range(K)], reps=3)
-    res["verify_nt4_us_per_layer"] = round(ms * 1000.0 / K, 3)
-    res["verify_nt4_GBs"] = round(decode_bytes(ctx, 4) / (ms * 1e-3 / K) / 1e9, 1)
+        # MTP verify: 4 query positions attending 8189..8192 keys
+        ms = graph_time_ms(torch, lambda: [decode_step(i, q4, 4) for i in range(K)], reps=3)
+        res["verify_nt4_us_per_layer"] = round(ms * 1000.0 / K, 3)
+        res["verify_nt4_GBs"] = round(decode_bytes(ctx, 4) / (ms * 1e-3 / K) / 1e9, 1)
 
-    # decode at ctx 512 (config 1, seed 0)
-    q5, kb5, vb5 = attn_inputs(0, ctx=512, nt=1)
-    q5 = torch.from_numpy(q5.reshape(1, -1)).to(dev)
-    k5 = [torch.from_numpy(kb5.view(np.int16)).to(dev) for _ in range(8)]
-    v5 = [torch.from_numpy(vb5.view(np.int16)).to(dev) for _ in range(8)]
+        # decode at ctx 512 (config 1, seed 0)
+        q5, kb5, vb5 = attn_inputs(0, ctx=512, nt=1)
+        q5 = torch.from_numpy(q5.reshape(1, -1)).to(dev)
+        k5 = [torch.from_numpy(kb5.view(np.int16)).to(dev) for _ in range(8)]
+        v5 = [torch.from_numpy(vb5.view(np.int16)).to(dev) for _ in range(8)]
 
-    def d512(i):
-        call("it_attn_f16_ex", q5.data_ptr(), NH * 2 * HD, k5[i % 8].data_ptr(), v5[i % 8].data_ptr(), KVD, 511, HD,
-             NH, NKV, 1, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(), ops.KERNEL_SPLITK, chunk,
-             stream_of())
-    ms = graph_time_ms(torch, lambda: [d512(i) for i in range(K)], reps=3)
-    res["decode_ctx512_us_per_layer"] = round(ms * 1000.0 / K, 3)
-    del kcs, vcs, k5, v5
+        def d512(i):
+            call("it_attn_f16_ex", q5.data_ptr(), NH * 2 * HD, k5[i % 8].data_ptr(), v5[i % 8].data_ptr(), KVD, 511, HD,
+                 NH, NKV, 1, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(), ops.KERNEL_SPLITK, chunk,
+                 stream_of())
+        ms = graph_time_ms(torch, lambda: [d512(i) for i in range(K)], reps=3)
+        res["decode_ctx512_us_per_layer"] = round(ms * 1000.0 / K, 3)
+        del kcs, vcs, k5, v5
 
     # ------------------------------------------------------------------ prefill attention (config 3)
-    T = 8192
-    qp_np, kbp, vbp = attn_inputs(2, ctx=T, nt=T)
-    qp = torch.from_numpy(qp_np.reshape(T, -1)).to(dev)
-    kp = torch.from_numpy(kbp.view(np.int16)).to(dev)
-    vp = torch.from_numpy(vbp.view(np.int16)).to(dev)
-    outp = torch.empty(T, NH * HD, device=dev)
-    sb = max(ops.attn_scratch_bytes(c * 64, 64, NH, NKV, HD) for c in range(128))
-    sb = max(sb, ops.attn_scratch_bytes(0, T, NH, NKV, HD))
-    scr = torch.empty(max(sb, 16), dtype=torch.uint8, device=dev)
+    if args.only in ("all", "prefill"):
+        T = 8192
+        qp_np, kbp, vbp = attn_inputs(2, ctx=T, nt=T)
+        qp = torch.from_numpy(qp_np.reshape(T, -1)).to(dev)
+        kp = torch.from_numpy(kbp.view(np.int16)).to(dev)
+        vp = torch.from_numpy(vbp.view(np.int16)).to(dev)
+        outp = torch.empty(T, NH * HD, device=dev)
+        sb = max(ops.attn_scratch_bytes(c * 64, 64, NH, NKV, HD) for c in range(128))
+        sb = max(sb, ops.attn_scratch_bytes(0, T, NH, NKV, HD))
+        scr = torch.empty(max(sb, 16), dtype=torch.uint8, device=dev)
 
-    def chunk_call(c):
-        call("it_attn_f16", qp[c * 64].data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, c * 64, HD, NH, NKV,
-             64, scale, outp[c * 64].data_ptr(), NH * HD, scr.data_ptr(), scr.numel(), stream_of())
+        def chunk_call(c):
+            call("it_attn_f16", qp[c * 64].data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, c * 64, HD, NH, NKV,
+                 64, scale, outp[c * 64].data_ptr(), NH * HD, scr.data_ptr(), scr.numel(), stream_of())
 
-    ms = graph_time_ms(torch, lambda: chunk_call(64), reps=5)
-    f = prefill_flops(4096, 64)
-    res["prefill_chunk64_at4096_us"] = round(ms * 1000, 2)
-    res["prefill_chunk64_at4096_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
-    ms = graph_time_ms(torch, lambda: [chunk_call(c) for c in range(128)], reps=3)
-    f = prefill_flops(0, T)
-    res["prefill_8192_as_128_chunks_ms"] = round(ms, 3)
-    res["prefill_8192_as_128_chunks_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
+        ms = graph_time_ms(torch, lambda: chunk_call(64), reps=5)
+        f = prefill_flops(4096, 64)
+        res["prefill_chunk64_at4096_us"] = round(ms * 1000, 2)
+        res["prefill_chunk64_at4096_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
+        ms = graph_time_ms(torch, lambda: [chunk_call(c) for c in range(128)], reps=3)
+        f = prefill_flops(0, T)
+        res["prefill_8192_as_128_chunks_ms"] = round(ms, 3)
+        res["prefill_8192_as_128_chunks_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
 
-    def whole():
-        call("it_attn_f16", qp.data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, 0, HD, NH, NKV, T, scale,
-             outp.data_ptr(), NH * HD, scr.data_ptr(), scr.numel(), stream_of())
-    ms = graph_time_ms(torch, whole, reps=3)
-    res["prefill_8192_single_call_ms"] = round(ms, 3)
-    res["prefill_8192_single_call_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
-    prefill_tflops = max(res["prefill_8192_single_call_TFLOPs"], res["prefill_8192_as_128_chunks_TFLOPs"])
-    log(f"prefill: chunk@4096 {res['prefill_chunk64_at4096_TFLOPs']} TF/s, 128 chunks "
-        f"{res['prefill_8192_as_128_chunks_TFLOPs']} TF/s, single call {res['prefill_8192_single_call_TFLOPs']} TF/s")
-    del qp, kp, vp, outp, scr
+        def whole():
+            call("it_attn_f16", qp.data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, 0, HD, NH, NKV, T, scale,
+                 outp.data_ptr(), NH * HD, scr.data_ptr(), scr.numel(), stream_of())
+        ms = graph_time_ms(torch, whole, reps=3)
+        res["prefill_8192_single_call_ms"] = round(ms, 3)
+        res["prefill_8192_single_call_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
+        prefill_tflops = max(res["prefill_8192_single_call_TFLOPs"], res["prefill_8192_as_128_chunks_TFLOPs"])
+        log(f"prefill: chunk@4096 {res['prefill_chunk64_at4096_TFLOPs']} TF/s, 128 chunks "
+            f"{res['prefill_8192_as_128_chunks_TFLOPs']} TF/s, single call {res['prefill_8192_single_call_TFLOPs']} TF/s")
+        del qp, kp, vp, outp, scr
 
     # ------------------------------------------------------------------ GDN decode step (config 4)
-    nv, nk, S = 32, 16, 128
-    d = gdn_inputs(3, nt=1, nv=nv, nk=nk)
-    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
-    NST = 160
-    states = [t(d["state"]) for _ in range(NST)]
-    x, w, cst = t(d["x"]), t(d["w"]), t(d["conv_state"])
-    br, ar, dtv, av = t(d["beta_raw"]), t(d["alpha_raw"]), t(d["dt"]), t(d["a"])
-    co = torch.empty(1, d["cd"], device=dev)
-    og = torch.empty(1, nv * S, device=dev)
+    if args.only in ("all", "gdn"):
+        nv, nk, S = 32, 16, 128
+        d = gdn_inputs(3, nt=1, nv=nv, nk=nk)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+        NST = 160
+        states = [t(d["state"]) for _ in range(NST)]
+        x, w, cst = t(d["x"]), t(d["w"]), t(d["conv_state"])
+        br, ar, dtv, av = t(d["beta_raw"]), t(d["alpha_raw"]), t(d["dt"]), t(d["a"])
+        co = torch.empty(1, d["cd"], device=dev)
+        og = torch.empty(1, nv * S, device=dev)
 
-    def gdn_layer(i):
-        call("it_gdn_conv", x.data_ptr(), d["cd"], w.data_ptr(), cst.data_ptr(), co.data_ptr(), d["cd"], d["cd"], 1, 4,
-             stream_of())
-        call("it_l2norm_heads", co.data_ptr(), d["cd"], 2 * nk, S, 1, 1e-6, stream_of())
-        call("it_gdn_step", co.data_ptr(), d["cd"], br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
-             states[i % NST].data_ptr(), og.data_ptr(), nv * S, 1, nv, nk, S, stream_of())
+        def gdn_layer(i):
+            call("it_gdn_conv", x.data_ptr(), d["cd"], w.data_ptr(), cst.data_ptr(), co.data_ptr(), d["cd"], d["cd"], 1, 4,
+                 stream_of())
+            call("it_l2norm_heads", co.data_ptr(), d["cd"], 2 * nk, S, 1, 1e-6, stream_of())
+            call("it_gdn_step", co.data_ptr(), d["cd"], br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
+                 states[i % NST].data_ptr(), og.data_ptr(), nv * S, 1, nv, nk, S, stream_of())
 
-    def gdn_only(i):
-        call("it_gdn_step", co.data_ptr(), d["cd"], br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
-             states[i % NST].data_ptr(), og.data_ptr(), nv * S, 1, nv, nk, S, stream_of())
-    ms = graph_time_ms(torch, lambda: [gdn_layer(i) for i in range(K)], reps=3)
-    res["gdn_decode_layer_us"] = round(ms * 1000 / K, 3)
-    ms = graph_time_ms(torch, lambda: [gdn_only(i) for i in range(K)], reps=3)
-    gst_us = ms * 1000 / K
-    gbytes = 2 * nv * S * S * 4
-    res["gdn_step_us"] = round(gst_us, 3)
-    res["gdn_step_state_GBs"] = round(gbytes / (gst_us * 1e-6) / 1e9, 1)
-    log(f"gdn: layer {res['gdn_decode_layer_us']} us, step {gst_us:.2f} us ({res['gdn_step_state_GBs']} GB/s state)")
-    del states
+        def gdn_only(i):
+            call("it_gdn_step", co.data_ptr(), d["cd"], br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
+                 states[i % NST].data_ptr(), og.data_ptr(), nv * S, 1, nv, nk, S, stream_of())
+        ms = graph_time_ms(torch, lambda: [gdn_layer(i) for i in range(K)], reps=3)
+        res["gdn_decode_layer_us"] = round(ms * 1000 / K, 3)
+        ms = graph_time_ms(torch, lambda: [gdn_only(i) for i in range(K)], reps=3)
+        gst_us = ms * 1000 / K
+        gbytes = 2 * nv * S * S * 4
+        res["gdn_step_us"] = round(gst_us, 3)
+        res["gdn_step_state_GBs"] = round(gbytes / (gst_us * 1e-6) / 1e9, 1)
+        log(f"gdn: layer {res['gdn_decode_layer_us']} us, step {gst_us:.2f} us ({res['gdn_step_state_GBs']} GB/s state)")
+        del states
 
-    # ------------------------------------------------------------------ GDN chunked prefill (config 5)
-    T5 = 8192
-    d5 = gdn_inputs(4, nt=T5, nv=nv, nk=nk)
-    x5, w5, cs5 = t(d5["x"]), t(d5["w"]), t(d5["conv_state"])
-    br5, ar5, dt5, a5 = t(d5["beta_raw"]), t(d5["alpha_raw"]), t(d5["dt"]), t(d5["a"])
-    st5 = t(d5["state"])
-    co5 = torch.empty(T5, d5["cd"], device=dev)
-    o5 = torch.empty(T5, nv * S, device=dev)
-    from irontimber_amd._lib import lib as _l
-    scr5 = torch.empty(_l().it_gdn_chunked_scratch_bytes(T5, nv, S), dtype=torch.uint8, device=dev)
+        # ------------------------------------------------------------------ GDN chunked prefill (config 5)
+        T5 = 8192
+        d5 = gdn_inputs(4, nt=T5, nv=nv, nk=nk)
+        x5, w5, cs5 = t(d5["x"]), t(d5["w"]), t(d5["conv_state"])
+        br5, ar5, dt5, a5 = t(d5["beta_raw"]), t(d5["alpha_raw"]), t(d5["dt"]), t(d5["a"])
+        st5 = t(d5["state"])
+        co5 = torch.empty(T5, d5["cd"], device=dev)
+        o5 = torch.empty(T5, nv * S, device=dev)
+        from irontimber_amd._lib import lib as _l
+        scr5 = torch.empty(_l().it_gdn_chunked_scratch_bytes(T5, nv, S), dtype=torch.uint8, device=dev)
 
-    def gdn_prefill():
-        call("it_gdn_conv", x5.data_ptr(), d5["cd"], w5.data_ptr(), cs5.data_ptr(), co5.data_ptr(), d5["cd"], d5["cd"],
-             T5, 4, stream_of())
-        call("it_l2norm_heads", co5.data_ptr(), d5["cd"], 2 * nk, S, T5, 1e-6, stream_of())
-        call("it_gdn_chunked", co5.data_ptr(), d5["cd"], br5.data_ptr(), ar5.data_ptr(), nv, dt5.data_ptr(),
-             a5.data_ptr(), st5.data_ptr(), o5.data_ptr(), nv * S, T5, nv, nk, S, scr5.data_ptr(), scr5.numel(),
-             stream_of())
+        def gdn_prefill():
+            call("it_gdn_conv", x5.data_ptr(), d5["cd"], w5.data_ptr(), cs5.data_ptr(), co5.data_ptr(), d5["cd"], d5["cd"],
+                 T5, 4, stream_of())
+            call("it_l2norm_heads", co5.data_ptr(), d5["cd"], 2 * nk, S, T5, 1e-6, stream_of())
+            call("it_gdn_chunked", co5.data_ptr(), d5["cd"], br5.data_ptr(), ar5.data_ptr(), nv, dt5.data_ptr(),
+                 a5.data_ptr(), st5.data_ptr(), o5.data_ptr(), nv * S, T5, nv, nk, S, scr5.data_ptr(), scr5.numel(),
+                 stream_of())
 
-    def gdn_scan_only():
-        call("it_gdn_chunked", co5.data_ptr(), d5["cd"], br5.data_ptr(), ar5.data_ptr(), nv, dt5.data_ptr(),
-             a5.data_ptr(), st5.data_ptr(), o5.data_ptr(), nv * S, T5, nv, nk, S, scr5.data_ptr(), scr5.numel(),
-             stream_of())
-    ms = graph_time_ms(torch, gdn_prefill, reps=3)
-    res["gdn_prefill_8192_layer_ms"] = round(ms, 4)
-    ms_s = graph_time_ms(torch, gdn_scan_only, reps=3)
-    gflop = 47.96e9   # chunked-form flops for 8192 tokens, 32 V heads, C=64
-    res["gdn_prefill_8192_scan_ms"] = round(ms_s, 4)
-    res["gdn_prefill_8192_scan_TFLOPs"] = round(gflop / (ms_s * 1e-3) / 1e12, 2)
-    io = T5 * (2 * nk + nv) * S * 4 + T5 * nv * S * 4 + 2 * 2 * nv * S * S * 4 + 2 * T5 * nv * 4
-    res["gdn_prefill_8192_scan_io_GBs"] = round(io / (ms_s * 1e-3) / 1e9, 1)
-    log(f"gdn prefill 8192: layer {ms:.3f} ms, scan {ms_s:.3f} ms ({res['gdn_prefill_8192_scan_TFLOPs']} TF/s chunked)")
+        def gdn_scan_only():
+            call("it_gdn_chunked", co5.data_ptr(), d5["cd"], br5.data_ptr(), ar5.data_ptr(), nv, dt5.data_ptr(),
+                 a5.data_ptr(), st5.data_ptr(), o5.data_ptr(), nv * S, T5, nv, nk, S, scr5.data_ptr(), scr5.numel(),
+                 stream_of())
+        ms = graph_time_ms(torch, gdn_prefill, reps=3)
+        res["gdn_prefill_8192_layer_ms"] = round(ms, 4)
+        ms_s = graph_time_ms(torch, gdn_scan_only, reps=3)
+        gflop = 47.96e9   # chunked-form flops for 8192 tokens, 32 V heads, C=64
+        res["gdn_prefill_8192_scan_ms"] = round(ms_s, 4)
+        res["gdn_prefill_8192_scan_TFLOPs"] = round(gflop / (ms_s * 1e-3) / 1e12, 2)
+        io = T5 * (2 * nk + nv) * S * 4 + T5 * nv * S * 4 + 2 * 2 * nv * S * S * 4 + 2 * T5 * nv * 4
+        res["gdn_prefill_8192_scan_io_GBs"] = round(io / (ms_s * 1e-3) / 1e9, 1)
+        log(f"gdn prefill 8192: layer {ms:.3f} ms, scan {ms_s:.3f} ms ({res['gdn_prefill_8192_scan_TFLOPs']} TF/s chunked)")
 
-    # hybrid stack (config 5): 3 GDN prefill layers then 1 attention prefill layer, 8192 tokens
-    T = 8192
-    qp_np, kbp, vbp = attn_inputs(2, ctx=T, nt=T)
-    qp = torch.from_numpy(qp_np.reshape(T, -1)).to(dev)
-    kp = torch.from_numpy(kbp.view(np.int16)).to(dev)
-    vp = torch.from_numpy(vbp.view(np.int16)).to(dev)
-    outp = torch.empty(T, NH * HD, device=dev)
+        # hybrid stack (config 5): 3 GDN prefill layers then 1 attention prefill layer, 8192 tokens
+        T = 8192
+        qp_np, kbp, vbp = attn_inputs(2, ctx=T, nt=T)
+        qp = torch.from_numpy(qp_np.reshape(T, -1)).to(dev)
+        kp = torch.from_numpy(kbp.view(np.int16)).to(dev)
+        vp = torch.from_numpy(vbp.view(np.int16)).to(dev)
+        outp = torch.empty(T, NH * HD, device=dev)
 
-    def hybrid():
-        for _ in range(3):
-            gdn_prefill()
-        call("it_attn_f16", qp.data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, 0, HD, NH, NKV, T, scale,
-             outp.data_ptr(), NH * HD, None, 0, stream_of())
-    ms = graph_time_ms(torch, hybrid, reps=2)
-    res["hybrid_3gdn_1attn_prefill_8192_ms"] = round(ms, 3)
-    del qp, kp, vp, outp, co5, o5, scr5
+        def hybrid():
+            for _ in range(3):
+                gdn_prefill()
+            call("it_attn_f16", qp.data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, 0, HD, NH, NKV, T, scale,
+                 outp.data_ptr(), NH * HD, None, 0, stream_of())
+        ms = graph_time_ms(torch, hybrid, reps=2)
+        res["hybrid_3gdn_1attn_prefill_8192_ms"] = round(ms, 3)
+        del qp, kp, vp, outp, co5, o5, scr5
 
     # ------------------------------------------------------------------ CPU baseline (oracle, host cores)
-    cpu = None
-    if not args.no_cpu:
-        import oracle
-        threads = min(16, oracle.hardware_threads())
-        q_c = q_np[3:4].reshape(1, -1)
-        n_runs, t0 = 0, time.perf_counter()
-        while True:
-            oracle.attn(q_c, kb, vb, ctx - 1, NH, NKV, threads=threads)
-            n_runs += 1
-            el = time.perf_counter() - t0
-            if el >= args.cpu_seconds or n_runs >= 2000:
-                break
-        cpu_us = el / n_runs * 1e6
-        cpu = {"value": round(dbytes / (cpu_us * 1e-6) / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-               "us_per_layer": round(cpu_us, 1),
-               "sample": f"{n_runs} decode-attention layers at ctx 8192 (config 2) through oracle/cpu_ref.cpp "
-                         f"(restatement of src/cpu.rs:260-272), {threads} threads, {el:.1f} s"}
-        log(f"cpu baseline: {cpu_us:.0f} us/layer on {threads} threads")
+    if args.only in ("all", "decode"):
+        if not args.no_cpu:
+            import oracle
+            threads = min(16, oracle.hardware_threads())
+            q_c = q_np[3:4].reshape(1, -1)
+            n_runs, t0 = 0, time.perf_counter()
+            while True:
+                oracle.attn(q_c, kb, vb, ctx - 1, NH, NKV, threads=threads)
+                n_runs += 1
+                el = time.perf_counter() - t0
+                if el >= args.cpu_seconds or n_runs >= 2000:
+                    break
+            cpu_us = el / n_runs * 1e6
+            cpu = {"value": round(dbytes / (cpu_us * 1e-6) / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                   "us_per_layer": round(cpu_us, 1),
+                   "sample": f"{n_runs} decode-attention layers at ctx 8192 (config 2) through oracle/cpu_ref.cpp "
+                             f"(restatement of src/cpu.rs:260-272), {threads} threads, {el:.1f} s"}
+            log(f"cpu baseline: {cpu_us:.0f} us/layer on {threads} threads")
 
     line = {
         "metric": "decode attn µs/layer + HBM GB/s @ctx 8192; prefill attn TFLOP/s @8192 tok",
-        "value": round(value_gbs, 1),
+        "value": rnd(value_gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": W,
-        "ms_per_step": round(us_layer / 1000.0, 6),
+        "ms_per_step": rnd(None if us_layer is None else us_layer / 1000.0, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -351,15 +365,16 @@ def main():
         "config": {"workload": "decode attention, 1 layer, batch 1, 16 q / 2 KV heads, head_dim 256, "
                                "f16 KV cache 8192 positions (config 2, seed 1)",
                    "kv_rotation_sets": NSETS, "split_keys": chunk, "timing": "hip graph replay, hip events"},
-        "decode_us_per_layer": round(us_layer, 3),
+        "decode_us_per_layer": rnd(us_layer, 3),
         "prefill_attn_TFLOPs": prefill_tflops,
         "results": res,
-        "roofline": {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "attn_decode_kernel<1>", "kernel_us": round(part_us, 3),
+        "roofline": {"bound": "hbm", "achieved": rnd(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": rnd(None if part_gbs is None else part_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": DECODE_TRAFFIC_BYTES, "traffic_unit": "bytes per launch",
+                     "kernel": "attn_decode_kernel<1>", "kernel_us": rnd(part_us, 3),
                      "bytes_per_launch": dbytes},
         "roofline_prefill": {"bound": "mfma", "achieved": prefill_tflops, "peak": F16_MFMA_PEAK_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4)},
+                             "unit": "TFLOP/s", "frac": rnd(None if prefill_tflops is None else prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
