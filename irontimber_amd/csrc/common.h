@@ -88,6 +88,22 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (a + b) + (c + d);
 }
 
+// max / sum over lanes l and l ^ 32 without going through LDS (a ds_bpermute would make the next
+// wait on LDS results also wait for every LDS operand read in flight): v_permlane32_swap exchanges
+// the two lane halves between two registers, both holding v. Written out because the compiler
+// folds the builtin's two results when both inputs are the same value. The swap reads VGPRs just
+// written by VALU ops, which needs two wait states first.
+__device__ __forceinline__ float max_xor32(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }

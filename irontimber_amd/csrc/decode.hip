@@ -247,29 +247,31 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
         }
     }
 
-    // ---- records {m (natural log units), l, 0, 0, o[256]}: sums of the per-wave running sums,
-    // P_hi and P_lo halves of O added across the two lane halves, stored straight from registers
+    // ---- records {m (natural log units), l, 0, 0, o[256]}: sums of the per-wave running sums;
+    // the P_hi and P_lo halves of O added across the two lane halves and staged in LDS (the V
+    // buffers are free once every wave is past the last tile), then written as whole 1 KB rows,
+    // one 16-byte store per lane
 #pragma unroll
     for (int b = 0; b < NB; ++b)
         if (g == 0 && c < 8) Mx[w][8 * b + c] = l_run[b];
+    float* Os = (float*)V0;   // [ROWS][256]
+    static_assert(ROWS * HD * 4 <= TK * HD * 2, "O fits in a V buffer");
     __syncthreads();
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int n = 0; n < 4; ++n)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[b][n][i] += __shfl_xor(acc[b][n][i], 32);
-        if (l < 32) {
-#pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int rr = r0 + 8 * b + 4 * g + i;
-                if (rr < R) {
-                    float* rec = part + ((size_t)((rr / G) * nh + kh * G + rr % G) * smax + s) * PART + 4 + 64 * w + c;
-#pragma unroll
-                    for (int n = 0; n < 4; ++n) rec[16 * n] = acc[b][n][i];
-                }
+                const float v = sum_xor32(acc[b][n][i]);
+                if (l < 32) Os[(8 * b + 4 * g + i) * HD + 64 * w + 16 * n + c] = v;
             }
-        }
+    __syncthreads();
+    for (int row = w; row < ROWS; row += 4) {
+        const int rr = r0 + row;
+        if (rr >= R) break;
+        float* rec = part + ((size_t)((rr / G) * nh + kh * G + rr % G) * smax + s) * PART;
+        *(f4*)(rec + 4 + 4 * l) = *(const f4*)(Os + row * HD + 4 * l);
     }
     if (w == 0 && l < ROWS) {
         const int rr = r0 + l;

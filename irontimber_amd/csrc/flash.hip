@@ -75,22 +75,6 @@ __device__ __forceinline__ void scale_acc(f16v& acc, float a) {
     }
 }
 
-// max / sum over lanes l and l ^ 32 without going through LDS (a ds_bpermute would make the next
-// wait on LDS results also wait for every operand read in flight): v_permlane32_swap exchanges
-// the two lane halves between two registers, both holding v. Written out because the compiler
-// folds the builtin's two results when both inputs are the same value. The swap reads VGPRs just
-// written by VALU ops, which needs two wait states first.
-__device__ __forceinline__ float max_xor32(float v) {
-    float a = v, b = v;
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return fmaxf(a, b);
-}
-__device__ __forceinline__ float sum_xor32(float v) {
-    float a = v, b = v;
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return a + b;
-}
-
 // s_waitcnt immediates (gfx9 encoding): wait until at most N vector-memory ops are outstanding
 // (expcnt/lgkmcnt left unconstrained).
 #define IT_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
@@ -114,7 +98,6 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     const int r = rt * BM + 32 * w + c;                 // this lane's query row
     const bool rvalid = r < R;
     const int t = rvalid ? r / G : 0;
-    const int head = kh * G + (rvalid ? r % G : 0);
     const int tmin = (rt * BM) / G, tmax = (min(R, rt * BM + BM) - 1) / G;
     const int split = blockIdx.z;
     const int kb0 = part ? split * chunk : 0;           // this workgroup's keys: [kb0, kend)
