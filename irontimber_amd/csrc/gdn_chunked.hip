@@ -37,6 +37,7 @@ constexpr size_t REC = (OFF_GC + 16 + 255) / 256 * 256;
 // 32-byte aligned, so the row pitch (288 B) is a multiple of 32 bytes
 constexpr int XS = SD + 16;
 }
+#define IT_SCAN_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
 
 size_t gdn_chunked_scratch_bytes(int nt, int nv, int S) {
     (void)S;
@@ -260,9 +261,54 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
 
 // ------------------------------------------------------------------------------------------------
 constexpr int NCB = SD / 32;   // 32-column blocks of the state per head
+
+// One chunk's operands for one column block, staged in LDS by the direct global->LDS path (no
+// registers hold data in flight, so the next chunk streams in during this one's products). Rows
+// are XOR-swizzled by 16-byte chunk so the operand reads of 16 consecutive rows hit distinct banks:
+// 256-byte rows (W, e^G Q) by row & 15, 128-byte rows (K^T, Q K^T) by (row >> 1) & 7 (two rows
+// share a 256-byte bank window). U holds only this block's 32 columns.
+struct ScanStage {
+    _Float16 W[C * SD];      // [token][dim]
+    _Float16 QG[C * SD];     // [token][dim]
+    _Float16 KT[SD * C];     // [dim][token]
+    _Float16 AQK[C * C];     // [token][token]
+    float U[C * 32];         // [token][column]
+};
+__device__ __forceinline__ int swz256(int r) { return r & 15; }
+// Workgroup barrier for LDS data written by the waves themselves (ds_write): waits for this wave's
+// LDS operations only. __syncthreads would also wait for the next chunk's loads into LDS, which
+// are still in flight by design (its release fence covers every outstanding LDS write).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ int swz128(int r) { return (r >> 1) & 7; }
+
+// Issue the loads of chunk record `rec` into stage B: 64 instructions of 64 lanes x 16 bytes, 16 per
+// wave (W 4, e^G Q 4, K^T 4, Q K^T 2, U 2); lane l lands at byte 16*l of its instruction's 1 KB.
+__device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, ScanStage& B, int n0, int w, int l) {
+    typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {   // W and e^G Q: 4 rows of 256 B per instruction
+        const int i = 4 * w + k, r = 4 * i + (l >> 4), j = (l & 15) ^ swz256(r);
+        __builtin_amdgcn_global_load_lds(rec + OFF_W + r * SD * 2 + 16 * j, (lds_void*)(B.W + 4 * i * SD), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(rec + OFF_QG + r * SD * 2 + 16 * j, (lds_void*)(B.QG + 4 * i * SD), 16, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {   // K^T: 8 rows of 128 B per instruction
+        const int i = 4 * w + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
+        __builtin_amdgcn_global_load_lds(rec + OFF_KT + r * C * 2 + 16 * j, (lds_void*)(B.KT + 8 * i * C), 16, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {   // Q K^T and this block's U columns: 8 rows of 128 B
+        const int i = 2 * w + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
+        __builtin_amdgcn_global_load_lds(rec + OFF_AQK + r * C * 2 + 16 * j, (lds_void*)(B.AQK + 8 * i * C), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(rec + OFF_U + (r * SD + n0) * 4 + 16 * (l & 7), (lds_void*)(B.U + 8 * i * 32), 16, 0, 0);
+    }
+}
+
 __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ scr, int nch, float* __restrict__ state,
                                                       float* __restrict__ out, int ots, int nt, int nv) {
     constexpr int SP = SD + 8, VP = C + 8;
+    __shared__ __align__(16) ScanStage B0;
+    __shared__ __align__(16) ScanStage B1;
     __shared__ __align__(16) _Float16 S0T[2][32][SP];   // [hi|lo][state column][key dim]
     __shared__ __align__(16) _Float16 VpT[2][32][VP];   // [hi|lo][state column][token]
 
@@ -276,6 +322,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
     const int n0 = 32 * cb;
     float* sh = state + (size_t)h * SD * SD;
     const float rs = 1.0f / sqrtf((float)SD);
+    const char* hrec = scr + (size_t)h * nch * REC;
+
+    scan_stage_loads(hrec, B0, n0, w, l);
+    float gc_next = *(const float*)(hrec + OFF_GC);
 
     // state slice in accumulator layout: st[mi][ni][i] = S[16(2w+mi) + 4g + i][n0 + 16ni + li]
     f4 st[2][2];
@@ -286,36 +336,15 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
 #pragma unroll
             for (int i = 0; i < 4; ++i) st[mi][ni][i] = sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li];
 
-    // Operands of one chunk as this lane reads them; the next chunk's are loaded into registers
-    // while the current chunk is computed.
-    struct ChunkOps { h8 w[4], qg[4], aqk[2], kt[2][2]; float u[2][4]; float gc; };
-    auto load_ops = [&](int c, ChunkOps& o) {
-        const char* rec = scr + ((size_t)h * nch + c) * REC;
-        const _Float16* W = (const _Float16*)(rec + OFF_W);
-        const _Float16* QG = (const _Float16*)(rec + OFF_QG);
-        const _Float16* KT = (const _Float16*)(rec + OFF_KT);
-        const _Float16* AQK = (const _Float16*)(rec + OFF_AQK);
-        const float* U = (const float*)(rec + OFF_U);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            o.w[ks] = ld_h8(W + (16 * w + li) * SD + 32 * ks + 8 * g);
-            o.qg[ks] = ld_h8(QG + (16 * w + li) * SD + 32 * ks + 8 * g);
+    // one chunk of the scan: its operands sit in stage B (landed), the next chunk's go into Bn
+    auto step = [&](int c, const ScanStage& B, ScanStage& Bn) {
+        IT_SCAN_WAIT_VMCNT(0);
+        __syncthreads();            // stage B complete for every wave; Bn, S0T and VpT free
+        const float gc = gc_next;
+        if (c + 1 < nch) {
+            scan_stage_loads(hrec + (size_t)(c + 1) * REC, Bn, n0, w, l);
+            gc_next = *(const float*)(hrec + (size_t)(c + 1) * REC + OFF_GC);
         }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            o.aqk[ks] = ld_h8(AQK + (16 * w + li) * C + 32 * ks + 8 * g);
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi) o.kt[ks][mi] = ld_h8(KT + (16 * (2 * w + mi) + li) * C + 32 * ks + 8 * g);
-        }
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o.u[ni][i] = U[(16 * w + 4 * g + i) * SD + n0 + 16 * ni + li];
-        o.gc = *(const float*)(rec + OFF_GC);
-    };
-    // one chunk of the scan with its operands already in registers
-    auto step = [&](int c, const ChunkOps& cur) {
-        const float gc = cur.gc;
         const int t0 = c * C, L = min(C, nt - t0);
 
         // ---- S0 -> LDS as hi/lo, transposed to [column][key dim]
@@ -331,12 +360,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
                     S0T[0][col][dk] = hi;
                     S0T[1][col][dk] = lo;
                 }
-        __syncthreads();
-        // ---- V' = U - W S0 for tokens 16w..16w+15
+        lds_barrier();
+        // ---- V' = U - W S0 for tokens 16w..16w+15 (W row 16w+li, dims 32ks+8g..)
+        const int rw = 16 * w + li;
         f4 vp[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const h8 a = cur.w[ks];
+            const h8 a = ld_h8(B.W + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
                 vp[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
@@ -348,17 +378,17 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = 16 * w + 4 * g + i, col = 16 * ni + li;
-                const float v = cur.u[ni][i] - vp[ni][i];
+                const float v = B.U[t * 32 + col] - vp[ni][i];
                 const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
                 VpT[0][col][t] = hi;
                 VpT[1][col][t] = lo;
             }
-        __syncthreads();
+        lds_barrier();
         // ---- O = (e^G Q S0 + Aqk V') / sqrt(128) for tokens 16w..16w+15
         f4 oa[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const h8 a = cur.qg[ks];
+            const h8 a = ld_h8(B.QG + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
                 oa[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
@@ -367,21 +397,31 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         }
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const h8 a = cur.aqk[ks];
+            const h8 a = ld_h8(B.AQK + rw * C + 8 * ((4 * ks + g) ^ swz128(rw)));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
                 oa[ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
                 oa[ni] = mfma16x16x32(a, ld_h8(&VpT[1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
             }
         }
+        // (stores guarded per token only in a partial last chunk: per-lane conditions split the
+        // code into small blocks)
+        float* orow = out + (size_t)t0 * ots + (size_t)h * SD + n0 + li;
+        if (L == C) {
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+            for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * w + 4 * g + i;
-                if (t < L) out[(size_t)(t0 + t) * ots + (size_t)h * SD + n0 + 16 * ni + li] = oa[ni][i] * rs;
-            }
-        // ---- S1 = e^{G_last} S0 + Ktilde^T V'
+                for (int i = 0; i < 4; ++i) orow[(size_t)(16 * w + 4 * g + i) * ots + 16 * ni] = oa[ni][i] * rs;
+        } else {
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * w + 4 * g + i;
+                    if (t < L) orow[(size_t)t * ots + 16 * ni] = oa[ni][i] * rs;
+                }
+        }
+        // ---- S1 = e^{G_last} S0 + Ktilde^T V' (K^T rows 16(2w+mi)+li, tokens 32ks+8g..)
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -390,28 +430,20 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi) {
-                const h8 a = cur.kt[ks][mi];
+                const int rk = 16 * (2 * w + mi) + li;
+                const h8 a = ld_h8(B.KT + rk * C + 8 * ((4 * ks + g) ^ swz128(rk)));
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni) {
                     st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
                     st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
                 }
             }
-        __syncthreads();
     };
-    // operands are loaded two chunks ahead (three register sets, loop unrolled by three)
-    ChunkOps o0, o1, o2;
-    load_ops(0, o0);
-    if (nch > 1) load_ops(1, o1);
-    for (int c = 0; c < nch; c += 3) {
-        if (c + 2 < nch) load_ops(c + 2, o2);
-        step(c, o0);
-        if (c + 1 >= nch) break;
-        if (c + 3 < nch) load_ops(c + 3, o0);
-        step(c + 1, o1);
-        if (c + 2 >= nch) break;
-        if (c + 4 < nch) load_ops(c + 4, o1);
-        step(c + 2, o2);
+    // two stages as distinct objects, so the compiler can tell the loads streaming into one never
+    // alias the reads of the other (no conservative waits); loop unrolled by two
+    for (int c = 0; c < nch; c += 2) {
+        step(c, B0, B1);
+        if (c + 1 < nch) step(c + 1, B1, B0);
     }
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
