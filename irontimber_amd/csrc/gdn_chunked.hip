@@ -260,19 +260,21 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
 }
 
 // ------------------------------------------------------------------------------------------------
-constexpr int NCB = SD / 32;   // 32-column blocks of the state per head
+constexpr int CW = 16;         // state columns per scan workgroup
+constexpr int NCB = SD / CW;   // column blocks of the state per head
+constexpr int NI = CW / 16;    // 16-column MFMA tiles per workgroup
 
 // One chunk's operands for one column block, staged in LDS by the direct global->LDS path (no
 // registers hold data in flight, so the next chunk streams in during this one's products). Rows
 // are XOR-swizzled by 16-byte chunk so the operand reads of 16 consecutive rows hit distinct banks:
 // 256-byte rows (W, e^G Q) by row & 15, 128-byte rows (K^T, Q K^T) by (row >> 1) & 7 (two rows
-// share a 256-byte bank window). U holds only this block's 32 columns.
+// share a 256-byte bank window). U holds only this block's CW columns.
 struct ScanStage {
     _Float16 W[C * SD];      // [token][dim]
     _Float16 QG[C * SD];     // [token][dim]
     _Float16 KT[SD * C];     // [dim][token]
     _Float16 AQK[C * C];     // [token][token]
-    float U[C * 32];         // [token][column]
+    float U[C * CW];         // [token][column]
 };
 __device__ __forceinline__ int swz256(int r) { return r & 15; }
 // Workgroup barrier for LDS data written by the waves themselves (ds_write): waits for this wave's
@@ -281,8 +283,8 @@ __device__ __forceinline__ int swz256(int r) { return r & 15; }
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ int swz128(int r) { return (r >> 1) & 7; }
 
-// Issue the loads of chunk record `rec` into stage B: 64 instructions of 64 lanes x 16 bytes, 16 per
-// wave (W 4, e^G Q 4, K^T 4, Q K^T 2, U 2); lane l lands at byte 16*l of its instruction's 1 KB.
+// Issue the loads of chunk record `rec` into stage B: instructions of 64 lanes x 16 bytes, per wave
+// W 4, e^G Q 4, K^T 4, Q K^T 2 and U CW/16; lane l lands at byte 16*l of its instruction's 1 KB.
 __device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, ScanStage& B, int n0, int w, int l) {
     typedef __attribute__((address_space(3))) void lds_void;
 #pragma unroll
@@ -297,10 +299,15 @@ __device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, S
         __builtin_amdgcn_global_load_lds(rec + OFF_KT + r * C * 2 + 16 * j, (lds_void*)(B.KT + 8 * i * C), 16, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {   // Q K^T and this block's U columns: 8 rows of 128 B
+    for (int k = 0; k < 2; ++k) {   // Q K^T: 8 rows of 128 B
         const int i = 2 * w + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
         __builtin_amdgcn_global_load_lds(rec + OFF_AQK + r * C * 2 + 16 * j, (lds_void*)(B.AQK + 8 * i * C), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(rec + OFF_U + (r * SD + n0) * 4 + 16 * (l & 7), (lds_void*)(B.U + 8 * i * 32), 16, 0, 0);
+    }
+    constexpr int UL = CW / 4;       // 16-byte lanes per U row (CW floats)
+#pragma unroll
+    for (int k = 0; k < CW / 16; ++k) {   // this block's U columns: 64/UL rows per instruction
+        const int i = (CW / 16) * w + k, r = (64 / UL) * i + l / UL;
+        __builtin_amdgcn_global_load_lds(rec + OFF_U + (r * SD + n0) * 4 + 16 * (l % UL), (lds_void*)(B.U + (64 / UL) * i * CW), 16, 0, 0);
     }
 }
 
@@ -309,17 +316,17 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
     constexpr int SP = SD + 8, VP = C + 8;
     __shared__ __align__(16) ScanStage B0;
     __shared__ __align__(16) ScanStage B1;
-    __shared__ __align__(16) _Float16 S0T[2][32][SP];   // [hi|lo][state column][key dim]
-    __shared__ __align__(16) _Float16 VpT[2][32][VP];   // [hi|lo][state column][token]
+    __shared__ __align__(16) _Float16 S0T[2][CW][SP];   // [hi|lo][state column][key dim]
+    __shared__ __align__(16) _Float16 VpT[2][CW][VP];   // [hi|lo][state column][token]
 
     // XCD-aware placement: workgroups are dealt to the 8 XCDs round-robin by linear id, so id L
-    // runs on XCD L % 8. All column blocks of one head go to the same XCD (head = xcd + 8*(slot/4))
+    // runs on XCD L % 8. All column blocks of one head go to the same XCD (head = xcd + 8*(slot/NCB))
     // and re-read that head's chunk records from the XCD's L2 instead of HBM.
     const int L_id = blockIdx.x, xcd = L_id & 7, slot = L_id >> 3;
     const int h = xcd + 8 * (slot / NCB), cb = slot % NCB;
     if (h >= nv) return;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
-    const int n0 = 32 * cb;
+    const int n0 = CW * cb;
     float* sh = state + (size_t)h * SD * SD;
     const float rs = 1.0f / sqrtf((float)SD);
     const char* hrec = scr + (size_t)h * nch * REC;
@@ -328,11 +335,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
     float gc_next = *(const float*)(hrec + OFF_GC);
 
     // state slice in accumulator layout: st[mi][ni][i] = S[16(2w+mi) + 4g + i][n0 + 16ni + li]
-    f4 st[2][2];
+    f4 st[2][NI];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
             for (int i = 0; i < 4; ++i) st[mi][ni][i] = sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li];
 
@@ -351,7 +358,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
+            for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float v = st[mi][ni][i];
@@ -363,34 +370,38 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         lds_barrier();
         // ---- V' = U - W S0 for tokens 16w..16w+15 (W row 16w+li, dims 32ks+8g..)
         const int rw = 16 * w + li;
-        f4 vp[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+        f4 vp[NI];
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) vp[ni] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const h8 a = ld_h8(B.W + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
+            for (int ni = 0; ni < NI; ++ni) {
                 vp[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
                 vp[ni] = mfma16x16x32(a, ld_h8(&S0T[1][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
             }
         }
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = 16 * w + 4 * g + i, col = 16 * ni + li;
-                const float v = B.U[t * 32 + col] - vp[ni][i];
+                const float v = B.U[t * CW + col] - vp[ni][i];
                 const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
                 VpT[0][col][t] = hi;
                 VpT[1][col][t] = lo;
             }
         lds_barrier();
         // ---- O = (e^G Q S0 + Aqk V') / sqrt(128) for tokens 16w..16w+15
-        f4 oa[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+        f4 oa[NI];
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) oa[ni] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const h8 a = ld_h8(B.QG + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
+            for (int ni = 0; ni < NI; ++ni) {
                 oa[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
                 oa[ni] = mfma16x16x32(a, ld_h8(&S0T[1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
             }
@@ -399,7 +410,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         for (int ks = 0; ks < 2; ++ks) {
             const h8 a = ld_h8(B.AQK + rw * C + 8 * ((4 * ks + g) ^ swz128(rw)));
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
+            for (int ni = 0; ni < NI; ++ni) {
                 oa[ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
                 oa[ni] = mfma16x16x32(a, ld_h8(&VpT[1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
             }
@@ -409,12 +420,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
         float* orow = out + (size_t)t0 * ots + (size_t)h * SD + n0 + li;
         if (L == C) {
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
+            for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) orow[(size_t)(16 * w + 4 * g + i) * ots + 16 * ni] = oa[ni][i] * rs;
         } else {
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
+            for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = 16 * w + 4 * g + i;
@@ -425,7 +436,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) st[mi][ni] *= gc;
+            for (int ni = 0; ni < NI; ++ni) st[mi][ni] *= gc;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -433,7 +444,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
                 const int rk = 16 * (2 * w + mi) + li;
                 const h8 a = ld_h8(B.KT + rk * C + 8 * ((4 * ks + g) ^ swz128(rk)));
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni) {
+                for (int ni = 0; ni < NI; ++ni) {
                     st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
                     st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
                 }
@@ -448,7 +459,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
             for (int i = 0; i < 4; ++i) sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li] = st[mi][ni][i];
 }
