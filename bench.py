@@ -260,9 +260,8 @@ def main():
         og = torch.empty(1, nv * S, device=dev)
 
         def gdn_layer(i):
-            call("it_gdn_conv", x.data_ptr(), d["cd"], w.data_ptr(), cst.data_ptr(), co.data_ptr(), d["cd"], d["cd"], 1, 4,
-                 stream_of())
-            call("it_l2norm_heads", co.data_ptr(), d["cd"], 2 * nk, S, 1, 1e-6, stream_of())
+            call("it_gdn_conv_l2norm", x.data_ptr(), d["cd"], w.data_ptr(), cst.data_ptr(), co.data_ptr(), d["cd"],
+                 d["cd"], 1, 4, 2 * nk, 1e-6, stream_of())
             call("it_gdn_step", co.data_ptr(), d["cd"], br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
                  states[i % NST].data_ptr(), og.data_ptr(), nv * S, 1, nv, nk, S, stream_of())
 
@@ -291,9 +290,8 @@ def main():
         scr5 = torch.empty(_l().it_gdn_chunked_scratch_bytes(T5, nv, S), dtype=torch.uint8, device=dev)
 
         def gdn_prefill():
-            call("it_gdn_conv", x5.data_ptr(), d5["cd"], w5.data_ptr(), cs5.data_ptr(), co5.data_ptr(), d5["cd"], d5["cd"],
-                 T5, 4, stream_of())
-            call("it_l2norm_heads", co5.data_ptr(), d5["cd"], 2 * nk, S, T5, 1e-6, stream_of())
+            call("it_gdn_conv_l2norm", x5.data_ptr(), d5["cd"], w5.data_ptr(), cs5.data_ptr(), co5.data_ptr(), d5["cd"],
+                 d5["cd"], T5, 4, 2 * nk, 1e-6, stream_of())
             call("it_gdn_chunked", co5.data_ptr(), d5["cd"], br5.data_ptr(), ar5.data_ptr(), nv, dt5.data_ptr(),
                  a5.data_ptr(), st5.data_ptr(), o5.data_ptr(), nv * S, T5, nv, nk, S, scr5.data_ptr(), scr5.numel(),
                  stream_of())

@@ -114,6 +114,14 @@ int it_gdn_conv(const float* x, int x_tok_stride, const float* w, float* state, 
  * cpu.rs:214). */
 int it_l2norm_heads(float* x, int tok_stride, int nheads, int d, int nt, float eps, void* stream);
 
+/* it_gdn_conv followed by it_l2norm_heads(out, ..., nnorm, 128, ...) in one pass: channels
+ * [0, nnorm*128) (the q and k heads, nnorm = 2*nk) are L2-normalised per 128-channel head and token
+ * after the conv + SiLU, the rest (v) are written as the conv gives them. Same buffers and state
+ * rules as it_gdn_conv; cd must be a multiple of 128.
+ * Replaces the conv and rmsnorm mode 2 dispatch pair, src/vk/mod.rs:803-804 (cpu.rs:201-214). */
+int it_gdn_conv_l2norm(const float* x, int x_tok_stride, const float* w, float* state, float* out,
+                       int out_tok_stride, int cd, int nt, int K, int nnorm, float eps, void* stream);
+
 /* Gated-delta recurrence, token by token, for nt tokens (decode: nt=1).
  *   co    : f32 normalised conv output, token t at co[t*co_tok_stride]: q heads [0, nk*S),
  *           k heads [nk*S, 2*nk*S), v heads [2*nk*S, 2*nk*S + nv*S). V head h uses q/k head h % nk.

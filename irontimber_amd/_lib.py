@@ -26,6 +26,7 @@ SIGNATURES = {
     "it_attn_combine": (c_int, [P, c_int, P, c_int, c_int, c_int, c_int, c_int, P, c_int, P]),
     "it_gdn_conv": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
     "it_l2norm_heads": (c_int, [P, c_int, c_int, c_int, c_int, c_float, P]),
+    "it_gdn_conv_l2norm": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "it_gdn_step": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "it_gdn_chunked_scratch_bytes": (c_size_t, [c_int, c_int, c_int]),
     "it_gdn_chunked": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_size_t, P]),

@@ -177,6 +177,18 @@ int it_gdn_conv(const float* x, int xts, const float* w, float* state, float* ou
     return check(it::launch_gdn_conv(x, xts, w, state, out, ots, cd, nt, K, (hipStream_t)stream), "it_gdn_conv");
 }
 
+int it_gdn_conv_l2norm(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt, int K,
+                       int nnorm, float eps, void* stream) {
+    if (K < 2 || K > 4) return fail("it_gdn_conv_l2norm: kernel size %d unsupported (2..4)", K);
+    if (cd <= 0 || cd % 128 != 0 || nt < 0) return fail("it_gdn_conv_l2norm: bad geometry cd=%d nt=%d (cd a multiple of 128)", cd, nt);
+    if (nnorm < 0 || nnorm * 128 > cd) return fail("it_gdn_conv_l2norm: %d normalised heads exceed cd=%d", nnorm, cd);
+    if (nt > 1 && (xts < cd || ots < cd)) return fail("it_gdn_conv_l2norm: token strides smaller than cd");
+    if (!x || !w || !state || !out) return fail("it_gdn_conv_l2norm: null buffer");
+    if (nt == 0) { g_err.clear(); return 0; }
+    return check(it::launch_gdn_conv_l2(x, xts, w, state, out, ots, cd, nt, K, nnorm, eps, (hipStream_t)stream),
+                 "it_gdn_conv_l2norm");
+}
+
 int it_l2norm_heads(float* x, int ts, int nheads, int d, int nt, float eps, void* stream) {
     if (d != 128 && d != 256) return fail("it_l2norm_heads: row length %d unsupported (128 or 256)", d);
     if (nheads <= 0 || nt < 0) return fail("it_l2norm_heads: bad geometry");

@@ -60,6 +60,65 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __rest
 }
 
 // ------------------------------------------------------------------------------------------------
+// Conv + SiLU with the per-head L2 norm fused (one pass over the activations instead of two).
+// Wave = (128-channel head block hb, run of TT tokens); lane l holds channels 128hb + l and
+// 128hb + 64 + l, so a token's head vector is the whole wave and its sum of squares one DPP
+// reduction. Head blocks hb < nnorm (the q and k heads) are normalised, x / max(||x||, eps); the
+// rest (v) pass through. State handling as in gdn_conv_kernel.
+template <int K>
+__global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restrict__ x, int xts,
+                                                          const float* __restrict__ w, float* __restrict__ state,
+                                                          float* __restrict__ out, int ots, int cd, int nt, int TT,
+                                                          int nnorm, float eps) {
+    const int hb = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (hb >= cd / 128) return;   // whole waves
+    const bool norm = hb < nnorm;
+    const int t0 = blockIdx.y * TT, t1 = min(nt, t0 + TT);
+    int ch[2] = {128 * hb + l, 128 * hb + 64 + l};
+    float wt[2][K], win[2][K - 1];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int i = 0; i < K; ++i) wt[c][i] = w[(size_t)ch[c] * K + i];
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i) {
+            const int tt = t0 - (K - 1) + i;
+            win[c][i] = tt >= 0 ? x[(size_t)tt * xts + ch[c]] : state[(size_t)(tt + K - 1) * cd + ch[c]];
+        }
+    }
+    for (int t = t0; t < t1; ++t) {
+        float y[2], xv[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            xv[c] = x[(size_t)t * xts + ch[c]];
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < K - 1; ++i) s += win[c][i] * wt[c][i];
+            s += xv[c] * wt[c][K - 1];
+            y[c] = siluf_(s);
+        }
+        if (norm) {
+            const float sc = 1.0f / fmaxf(sqrtf(wave_sum(y[0] * y[0] + y[1] * y[1])), eps);
+            y[0] *= sc;
+            y[1] *= sc;
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            out[(size_t)t * ots + ch[c]] = y[c];
+#pragma unroll
+            for (int i = 0; i + 1 < K - 1; ++i) win[c][i] = win[c][i + 1];
+            win[c][K - 2] = xv[c];
+        }
+    }
+    if (gridDim.y == 1) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int i = 0; i < K - 1; ++i) state[(size_t)i * cd + ch[c]] = win[c][i];
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // L2 norm of rows of D floats, one wave per row, in place: x / max(||x||, eps).
 template <int D>
 __global__ __launch_bounds__(256) void l2norm_kernel(float* __restrict__ x, int ts, int nheads, int nt, float eps) {
@@ -146,6 +205,22 @@ hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state
         default: IT_CONV(4) break;
     }
 #undef IT_CONV
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd,
+                              int nt, int K, int nnorm, float eps, hipStream_t st) {
+    const int TT = nt <= 16 ? nt : 16;
+    const dim3 grid((cd / 128 + 3) / 4, (nt + TT - 1) / TT);
+#define IT_CONVL2(KK)                                                                                          \
+    gdn_conv_l2_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps);         \
+    if (grid.y > 1) gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, cd, nt);
+    switch (K) {
+        case 2: IT_CONVL2(2) break;
+        case 3: IT_CONVL2(3) break;
+        default: IT_CONVL2(4) break;
+    }
+#undef IT_CONVL2
     return hipGetLastError();
 }
 

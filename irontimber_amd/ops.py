@@ -86,6 +86,19 @@ def gdn_conv(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor, out: torch.T
     return out
 
 
+def gdn_conv_l2norm(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor, nnorm: int, eps: float = 1e-6,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """gdn_conv then l2norm_heads(out, nnorm, 128, eps) in one pass (x [nt, cd], cd % 128 == 0)."""
+    _need(x, torch.float32, "x"); _need(w, torch.float32, "w"); _need(state, torch.float32, "state")
+    nt, cd = x.shape
+    K = w.shape[1]
+    if out is None:
+        out = torch.empty_like(x)
+    call("it_gdn_conv_l2norm", x.data_ptr(), cd, w.data_ptr(), state.data_ptr(), out.data_ptr(), cd, cd, nt, K,
+         nnorm, float(eps), _stream())
+    return out
+
+
 def l2norm_heads(x: torch.Tensor, nheads: int, d: int, eps: float = 1e-6) -> torch.Tensor:
     """In place on the first nheads*d columns of each row of x [nt, C]."""
     _need(x, torch.float32, "x")

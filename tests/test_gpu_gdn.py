@@ -27,6 +27,28 @@ def test_conv(dev, nt, K):
     np.testing.assert_array_equal(host(st), wst)
 
 
+@pytest.mark.parametrize("nt,K,nv,nk", [(1, 4, 32, 16), (3, 4, 8, 4), (16, 4, 8, 4), (17, 3, 8, 4), (100, 4, 32, 16),
+                                         (1000, 2, 4, 2)])
+def test_conv_l2norm_fused(dev, nt, K, nv, nk):
+    """The fused conv + L2 entry equals the conv then L2 dispatch pair (the oracle's two passes, and
+    the GPU's two kernels), including the carried state."""
+    announce(f"conv+l2 nt={nt} K={K} nv={nv} nk={nk}")
+    d = gdn_inputs(5, nt=nt, nv=nv, nk=nk)
+    w = d["w"][:, :K].copy()
+    st0 = d["conv_state"][:K - 1].copy()
+    want, wst = oracle.gdn_conv(d["x"], w, st0)
+    want = oracle.l2norm_heads(want, 2 * nk, 128)
+    st = dev_f32(st0, dev)
+    got = host(ops.gdn_conv_l2norm(dev_f32(d["x"], dev), dev_f32(w, dev), st, 2 * nk))
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(host(st), wst)
+    st2 = dev_f32(st0, dev)
+    two = ops.gdn_conv(dev_f32(d["x"], dev), dev_f32(w, dev), st2)
+    ops.l2norm_heads(two, 2 * nk, 128)
+    np.testing.assert_allclose(got, host(two), rtol=2e-6, atol=1e-7)
+    np.testing.assert_array_equal(host(st2), wst)
+
+
 @pytest.mark.parametrize("d", [128, 256])
 def test_l2norm(dev, d):
     x = np.random.default_rng(2).standard_normal((7, 40 * d)).astype(np.float32)
