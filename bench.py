@@ -51,6 +51,12 @@ def prefill_flops(pos0: int, nt: int) -> int:
     return 4 * HD * NH * sum(pos0 + t + 1 for t in range(nt))
 
 
+def prep_bytes(nt: int) -> int:
+    """Algorithmic HBM bytes of the attention pre-pass: q read and rewritten (f32, query halves only),
+    k and v read (f32), K and V rows written (f16)."""
+    return nt * (NH * HD * 4 * 2 + 2 * KVD * 4 + 2 * KVD * 2)
+
+
 def graph_time_ms(torch, fn, reps: int, warm: int = 3) -> float:
     """Capture `fn` (which enqueues work on the current stream) into a graph, replay `warm` times,
     then time one more replay with events on the capture stream. Returns ms per replay."""
@@ -87,7 +93,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-chunk", type=int, default=0, help="keys per split for decode (0 = library policy)")
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "gdn"], default="all",
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "gdn", "prep"], default="all",
                     help="run one section only (profiling runs); the JSON line then carries that section's figures")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain device copies of 256 MiB (reference reading for the FETCH_SIZE / "
@@ -101,7 +107,7 @@ def main():
     import torch
     from irontimber_amd import ops
     from irontimber_amd._lib import call
-    from irontimber_amd.synth import attn_inputs, gdn_inputs
+    from irontimber_amd.synth import attn_inputs, gdn_inputs, prep_inputs
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -246,6 +252,29 @@ def main():
         log(f"prefill: chunk@4096 {res['prefill_chunk64_at4096_TFLOPs']} TF/s, 128 chunks "
             f"{res['prefill_8192_as_128_chunks_TFLOPs']} TF/s, single call {res['prefill_8192_single_call_TFLOPs']} TF/s")
         del qp, kp, vp, outp, scr
+
+    # ------------------------------------------------------------------ attention pre-pass (norm, rope, KV append)
+    if args.only in ("all", "prep"):
+        T = 8192
+        dp = prep_inputs(7, T)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+        pq, pk, pv, pqn, pkn = t(dp["q"]), t(dp["k"]), t(dp["v"]), t(dp["q_norm"]), t(dp["k_norm"])
+        pkc = torch.empty(T, KVD, dtype=torch.int16, device=dev)
+        pvc = torch.empty_like(pkc)
+
+        def prep(nt, pos0):
+            ops.attn_prep_f16(pq[:nt], pk[:nt], pv[:nt], pkc, pvc, pos0, NH, NKV, pqn, pkn)
+        ms = graph_time_ms(torch, lambda: [prep(1, T - 1) for _ in range(K)], reps=3)
+        res["prep_decode_us"] = round(ms * 1000 / K, 3)
+        ms = graph_time_ms(torch, lambda: [prep(64, 4096) for _ in range(100)], reps=3)
+        res["prep_chunk64_us"] = round(ms * 10, 3)
+        ms = graph_time_ms(torch, lambda: [prep(T, 0) for _ in range(10)], reps=3)
+        ms /= 10
+        res["prep_8192_us"] = round(ms * 1000, 2)
+        res["prep_8192_GBs"] = round(prep_bytes(T) / (ms * 1e-3) / 1e9, 1)
+        log(f"prep: decode {res['prep_decode_us']} us, chunk64 {res['prep_chunk64_us']} us, 8192 tokens "
+            f"{res['prep_8192_us']} us ({res['prep_8192_GBs']} GB/s)")
+        del pq, pk, pv, pkc, pvc
 
     # ------------------------------------------------------------------ GDN decode step (config 4)
     if args.only in ("all", "gdn"):

@@ -42,6 +42,25 @@ int it_abi_version(void);
 int it_kv_append_f16(const float* k, const float* v, int src_tok_stride, uint16_t* kc, uint16_t* vc,
                      int pos0, int nt, int kvd, int round_mode, void* stream);
 
+/* The whole pre-attention pass in one launch: per-head RMSNorm of q and k, neox-style (I)MRoPE on
+ * the first n_rot dims of each q and k head at positions pos0+t, and the f16 append of K and V.
+ *   q      : f32 [t*q_tok_stride + h*2*hd + d]; d < hd (the query) is rewritten in place with
+ *            rope(rmsnorm(q) * q_norm); d in [hd, 2hd) (the gate) is left as it is.
+ *   k, v   : f32 [t*kv_tok_stride + kh*hd + d], the k and v projections (read only).
+ *   kc, vc : f16 cache rows pos0+t receive f16(rope(rmsnorm(k) * k_norm)) and f16(v).
+ *   q_norm, k_norm: f32 [hd] weights, or NULL for unit weight. eps: the RMSNorm epsilon.
+ *   n_rot  : rotated dims per head (even, <= hd, a multiple of hd/32); theta_scale the f32
+ *            base^(-2/n_rot) the reference pushes (src/vk/mod.rs:824); sec0..sec3 the rope
+ *            sections (a frequency outside the text sections keeps angle 0, cpu.rs:152-155).
+ *   round_mode as for it_kv_append_f16. hd is 128 or 256.
+ * The angles p*theta_scale^i are formed in f64, so they are exact to f32 rounding at any position.
+ * Replaces the six dispatches of src/vk/mod.rs:822-838 (two rmsnorm mode 0, two rope, two kv_pack;
+ * kernels/src/lib.rs:207-229, 233-250, 743-750) and cpu.rs:249-258. */
+int it_attn_prep_f16(float* q, int q_tok_stride, const float* k, const float* v, int kv_tok_stride,
+                     const float* q_norm, const float* k_norm, float eps, uint16_t* kc, uint16_t* vc, int kvd,
+                     int pos0, int hd, int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1,
+                     int sec2, int sec3, int round_mode, void* stream);
+
 /* Bytes of scratch it_attn_f16 needs for this call geometry (0 if the chosen kernel needs none). */
 size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv);
 

@@ -8,6 +8,9 @@ namespace it {
 
 hipError_t launch_kv_append(const float* k, const float* v, int sts, uint16_t* kc, uint16_t* vc, int pos0, int nt,
                             int kvd, int rtz, hipStream_t st);
+hipError_t launch_attn_prep(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
+                            const float* kw, float eps, uint16_t* kc, uint16_t* vc, int pos0, int hd, int nh, int nkv,
+                            int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st);
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                                 int nh, int nkv, int nt, float scale, float* part, int chunk, hipStream_t st);
 hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,

@@ -43,6 +43,36 @@ def kv_append_f16(k: torch.Tensor, v: torch.Tensor, kc: torch.Tensor, vc: torch.
          round_mode, _stream())
 
 
+def attn_prep_f16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int,
+                  nh: int, nkv: int, q_norm: torch.Tensor | None = None, k_norm: torch.Tensor | None = None,
+                  eps: float = 1e-6, n_rot: int = 64, theta_scale: float | None = None, rope_base: float = 1e7,
+                  sections=(11, 11, 10, 0), round_mode: int = 0) -> None:
+    """Norm + rope of q (in place, q [nt, nh*2*hd]) and k [nt, nkv*hd], then the f16 append of k and
+    v to kc/vc at rows pos0.. (it_attn_prep_f16). theta_scale defaults to rope_base^(-2/n_rot) in f32."""
+    _need(q, torch.float32, "q"); _need(k, torch.float32, "k"); _need(v, torch.float32, "v")
+    nt, kvd = k.shape
+    hd = kvd // nkv
+    if q.shape != (nt, nh * 2 * hd) or v.shape != k.shape:
+        raise ValueError("q must be [nt, nh*2*hd] and v the shape of k [nt, nkv*hd]")
+    for c in (kc, vc):
+        if c.dtype not in (torch.float16, torch.int16) or not c.is_contiguous() or c.shape[-1] != kvd:
+            raise ValueError("kc/vc must be contiguous [ctx, kvd] f16")
+        if c.shape[0] < pos0 + nt:
+            raise ValueError("cache too short")
+    for w, n in ((q_norm, "q_norm"), (k_norm, "k_norm")):
+        if w is not None:
+            _need(w, torch.float32, n)
+            if w.numel() != hd:
+                raise ValueError(f"{n} must hold head_dim floats")
+    if theta_scale is None:
+        from .synth import rope_theta_scale
+        theta_scale = rope_theta_scale(rope_base, n_rot)
+    s = list(sections) + [0] * (4 - len(sections))
+    call("it_attn_prep_f16", q.data_ptr(), q.shape[1], k.data_ptr(), v.data_ptr(), kvd, _ptr(q_norm), _ptr(k_norm),
+         float(eps), kc.data_ptr(), vc.data_ptr(), kvd, pos0, hd, nh, nkv, nt, n_rot, float(theta_scale), *s[:4],
+         round_mode, _stream())
+
+
 def attn_scratch_bytes(pos0: int, nt: int, nh: int, nkv: int, hd: int = 256, kernel: int = KERNEL_AUTO,
                        chunk: int = 0) -> int:
     return lib().it_attn_scratch_bytes_ex(pos0, nt, hd, nh, nkv, kernel, chunk)

@@ -115,3 +115,26 @@ def gdn_step_inputs(seed: int, nt: int, nv: int = 32, nk: int = 16, S: int = 128
     a = (-np.exp(a_log)).astype(np.float32)
     dt = np.zeros(nv, np.float32)
     return dict(state=state, co=co.reshape(nt, -1), beta_raw=beta_raw, alpha_raw=alpha_raw, a=a, dt=dt)
+
+
+# Qwen3.5 rope geometry (the reference's kparity push constants, src/vk/kparity.rs:33): 64 rotated
+# dims per head, base 1e7, sections [11, 11, 10, 0].
+ROPE_N_ROT, ROPE_BASE, ROPE_SECTIONS = 64, 1e7, (11, 11, 10, 0)
+
+
+def rope_theta_scale(base: float, n_rot: int) -> float:
+    """base^(-2/n_rot) rounded to f32 (the theta_scale the reference computes and pushes)."""
+    return float(np.float32(np.float32(base) ** np.float32(-2.0 / n_rot)))
+
+
+def prep_inputs(seed: int, nt: int, nh: int = 16, nkv: int = 2, hd: int = 256):
+    """Attention pre-pass inputs (the q/k/v projections before norm and rope). Draw order:
+    q+gate [nt, nh*2*hd] ~ N(0, 2^2); k [nt, nkv*hd] ~ N(0, 2^2); v [nt, nkv*hd] ~ N(0,1);
+    q_norm, k_norm [hd] ~ 1 + N(0, 0.1^2)."""
+    r = Rng(seed)
+    q = r.normal(nt * nh * 2 * hd, std=2.0).reshape(nt, nh * 2 * hd)
+    k = r.normal(nt * nkv * hd, std=2.0).reshape(nt, nkv * hd)
+    v = r.normal(nt * nkv * hd).reshape(nt, nkv * hd)
+    q_norm = (1.0 + r.normal(hd, std=0.1)).astype(np.float32)
+    k_norm = (1.0 + r.normal(hd, std=0.1)).astype(np.float32)
+    return dict(q=q, k=k, v=v, q_norm=q_norm, k_norm=k_norm)

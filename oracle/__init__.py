@@ -4,7 +4,7 @@ Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import 
 only as the checker (or the timed CPU baseline). The product path never routes through it.
 
 - `cpu_ref.cpp` (built to liboracle.so by oracle/Makefile): restatement of the reference's CPU
-  forward pass, src/cpu.rs:14-22, 164, 194-274, in f32 with the reference's loop order.
+  forward pass, src/cpu.rs:14-22, 145-164, 194-274, in f32 with the reference's loop order.
 - `ref_np.py`: float64 references used to pin that restatement (the r012 known-answer softmax of
   src/vk/r012_parity.rs:22-28, a brute-force float64 gated-delta recurrence) and the numpy
   statement of the chunk-64 WY/UT scan (a new algorithm, pinned only by equality with the
@@ -30,6 +30,9 @@ _SIG = {
     "it_ref_f16_to_f32": (_f, [ctypes.c_uint16]),
     "it_ref_rmsnorm": (None, [_P, _P, _i, _f, _P]),
     "it_ref_l2norm": (None, [_P, _i, _f]),
+    "it_ref_rope_theta_scale": (_f, [_f, _i]),
+    "it_ref_rope": (None, [_P, _i, _i, _i, _i, _f, _P]),
+    "it_ref_attn_prep": (None, [_P, _i, _P, _i, _P, _P, _f, _P, _i, _i, _i, _i, _i, _i, _f, _P]),
     "it_ref_attn": (None, [_P, _i, _P, _P, _i, _i, _i, _i, _i, _i, _f, _P, _i, _i]),
     "it_ref_gdn_conv": (None, [_P, _i, _P, _P, _P, _i, _i, _i, _i]),
     "it_ref_gdn_step": (None, [_P, _i, _P, _P, _i, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i]),
@@ -110,3 +113,38 @@ def gdn_step(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, threads: i
     lib().it_ref_gdn_step(_p(co), co.shape[1], _p(br), _p(ar), br.shape[1], _p(dt), _p(a), _p(st), _p(out), nv * S,
                           nt, nv, nk, S, threads or hardware_threads())
     return out, st
+
+
+def _sections(sections) -> np.ndarray:
+    s = np.zeros(4, np.int32)
+    s[:len(sections)] = sections
+    return s
+
+
+def rope_theta_scale(base: float, n_rot: int) -> float:
+    """cpu.rs:147: base^(-2/n_rot) in f32."""
+    return float(lib().it_ref_rope_theta_scale(base, n_rot))
+
+
+def rope(x: np.ndarray, pos: int, n_rot: int, base: float, sections=(0, 0, 0, 0)) -> np.ndarray:
+    """cpu.rs:145-162 on every row of x [..., head_dim]; returns a copy."""
+    y = np.ascontiguousarray(x, np.float32).copy()
+    hd = y.shape[-1]
+    lib().it_ref_rope(_p(y), y.size // hd, hd, n_rot, pos, base, _p(_sections(sections)))
+    return y
+
+
+def attn_prep(q: np.ndarray, k: np.ndarray, q_norm, k_norm, eps: float, pos0: int, nh: int, nkv: int, hd: int,
+              n_rot: int, base: float, sections=(0, 0, 0, 0)):
+    """cpu.rs:249-257 for nt tokens. q [nt, nh*2*hd], k [nt, nkv*hd] f32; q_norm/k_norm [hd] or None.
+    Returns (q with its query halves normed and roped, k normed and roped), both f32."""
+    q = np.ascontiguousarray(q, np.float32).reshape(q.shape[0], -1).copy()
+    k = np.ascontiguousarray(k, np.float32).reshape(k.shape[0], -1)
+    nt = q.shape[0]
+    ko = np.zeros((nt, nkv * hd), np.float32)
+    qn = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+    kn = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
+    lib().it_ref_attn_prep(_p(q), q.shape[1], _p(k), k.shape[1], None if qn is None else _p(qn),
+                           None if kn is None else _p(kn), eps, _p(ko), pos0, hd, nh, nkv, nt, n_rot, base,
+                           _p(_sections(sections)))
+    return q, ko

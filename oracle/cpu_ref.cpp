@@ -15,6 +15,10 @@
 //                        (single key, equal scores), torch SDPA, split/chunk invariance.
 //   it_ref_gdn_*      -- brute-force float64 recurrence, closed forms (beta=0, g -> -inf),
 //                        conv over T tokens == T single-token calls.
+//   it_ref_rope, it_ref_attn_prep -- pos 0 = identity, a single pair = the 2-D rotation by pos,
+//                        the sector rule's fixed dims, pair norms, relative-position invariance of
+//                        q.k, and an f64 statement with exact angles (error bounded by the f32
+//                        angle recurrence); it_ref_rmsnorm -- unit RMS, constant rows.
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -83,6 +87,59 @@ void it_ref_rmsnorm(const float* x, const float* w, int n, float eps, float* y) 
     ss = ss / (float)n;
     float s = 1.0f / std::sqrt(ss + eps);
     for (int i = 0; i < n; ++i) y[i] = x[i] * s * (w ? w[i] : 1.0f);
+}
+
+// cpu.rs:147 theta_scale = base^(-2 / n_rot), f32 (the value the reference pushes, vk/mod.rs:824).
+float it_ref_rope_theta_scale(float base, int n_rot) { return std::pow(base, -2.0f / (float)n_rot); }
+
+// cpu.rs:145-162 neox-style (I)MRoPE in place on nheads rows of head_dim floats at position pos:
+// the angle of frequency i is the f32 recurrence theta_0 = pos, theta_{i+1} = theta_i * theta_scale,
+// replaced by 0 for a frequency whose sector lies outside the text sections.
+void it_ref_rope(float* x, int nheads, int head_dim, int n_rot, int pos, float base, const int* sections) {
+    const int half = n_rot / 2;
+    const float theta_scale = it_ref_rope_theta_scale(base, n_rot);
+    const int sect = sections[0] + sections[1] + sections[2] + sections[3];
+    for (int h = 0; h < nheads; ++h) {
+        float* r = x + (size_t)h * head_dim;
+        float theta = (float)pos;
+        for (int i = 0; i < half; ++i) {
+            const int sector = sect > 0 ? i % sect : 0;
+            const bool use_e = sect > 0 && !((sector % 3 == 1 && sector < 3 * sections[1]) ||
+                                             (sector % 3 == 2 && sector < 3 * sections[2]) ||
+                                             (sector % 3 == 0 && sector < 3 * sections[0]));
+            const float th = use_e ? 0.0f : theta;
+            const float sn = std::sin(th), c = std::cos(th);
+            const float x0 = r[i], x1 = r[i + half];
+            r[i] = x0 * c - x1 * sn;
+            r[i + half] = x0 * sn + x1 * c;
+            theta *= theta_scale;
+        }
+    }
+}
+
+// cpu.rs:249-257 for nt tokens at positions pos0+t: q heads (the first hd of each [q | gate]
+// block of 2*hd) and k heads RMS-normed with their weights (nullptr = unit), then roped; q is
+// rewritten in place, k_out receives the normed and roped k rows (f32, before the f16 cast of
+// cpu.rs:258 which the caller applies).
+//   q     : f32 q[t*q_tok_stride + h*2*hd + d]
+//   k     : f32 k[t*kv_tok_stride + kh*hd + d]; k_out [t*nkv*hd + kh*hd + d]
+void it_ref_attn_prep(float* q, int q_tok_stride, const float* k, int kv_tok_stride, const float* q_norm,
+                      const float* k_norm, float eps, float* k_out, int pos0, int hd, int nh, int nkv, int nt,
+                      int n_rot, float base, const int* sections) {
+    std::vector<float> row(hd);
+    for (int t = 0; t < nt; ++t) {
+        for (int h = 0; h < nh; ++h) {
+            float* qh = q + (size_t)t * q_tok_stride + (size_t)h * 2 * hd;
+            it_ref_rmsnorm(qh, q_norm, hd, eps, row.data());
+            it_ref_rope(row.data(), 1, hd, n_rot, pos0 + t, base, sections);
+            std::memcpy(qh, row.data(), hd * sizeof(float));
+        }
+        for (int h = 0; h < nkv; ++h) {
+            float* ko = k_out + ((size_t)t * nkv + h) * hd;
+            it_ref_rmsnorm(k + (size_t)t * kv_tok_stride + (size_t)h * hd, k_norm, hd, eps, ko);
+            it_ref_rope(ko, 1, hd, n_rot, pos0 + t, base, sections);
+        }
+    }
 }
 
 // cpu.rs:164 l2norm, in place.

@@ -105,3 +105,31 @@ def gdn_chunked_f64(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, C: 
             S0 = np.exp(G[-1]) * S0 + (np.exp(G[-1] - G)[:, None] * K).T @ U
         st[h] = S0
     return out.reshape(nt, nv * S), st
+
+
+def rope_f64(x: np.ndarray, pos: int, n_rot: int, theta_scale: float, sections=(0, 0, 0, 0)) -> np.ndarray:
+    """Neox-style (I)MRoPE in float64 with exact angles pos * theta_scale**i (theta_scale the f32
+    value, cpu.rs:147), the sector rule of cpu.rs:152-155; x [..., head_dim] -> float64 copy.
+    Differs from cpu.rs:145-162 only by that function's f32 angle recurrence."""
+    y = np.array(x, np.float64)
+    half = n_rot // 2
+    s0, s1, s2, s3 = (list(sections) + [0, 0, 0, 0])[:4]
+    sect = s0 + s1 + s2 + s3
+    i = np.arange(half)
+    sector = i % sect if sect > 0 else np.zeros_like(i)
+    keep = ((sector % 3 == 1) & (sector < 3 * s1)) | ((sector % 3 == 2) & (sector < 3 * s2)) | \
+           ((sector % 3 == 0) & (sector < 3 * s0))
+    use_e = (sect > 0) & ~keep
+    th = np.where(use_e, 0.0, float(pos) * np.float64(theta_scale) ** i)
+    c, s = np.cos(th), np.sin(th)
+    x0, x1 = y[..., :half].copy(), y[..., half:n_rot].copy()
+    y[..., :half] = x0 * c - x1 * s
+    y[..., half:n_rot] = x0 * s + x1 * c
+    return y
+
+
+def rmsnorm_f64(x: np.ndarray, w=None, eps: float = 1e-6) -> np.ndarray:
+    """x / sqrt(mean(x^2) + eps) * w over the last axis, float64 (cpu.rs:14-18)."""
+    x = np.asarray(x, np.float64)
+    y = x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    return y if w is None else y * np.asarray(w, np.float64)
