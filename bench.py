@@ -305,6 +305,29 @@ def main():
         res["gdn_step_us"] = round(gst_us, 3)
         res["gdn_step_state_GBs"] = round(gbytes / (gst_us * 1e-6) / 1e9, 1)
         log(f"gdn: layer {res['gdn_decode_layer_us']} us, step {gst_us:.2f} us ({res['gdn_step_state_GBs']} GB/s state)")
+
+        # MTP verify of [x, draft]: one nt = 2 layer call with the conv and SSM checkpoints after token 0
+        d2 = gdn_inputs(3, nt=2, nv=nv, nk=nk)
+        x2, br2, ar2 = t(d2["x"]), t(d2["beta_raw"]), t(d2["alpha_raw"])
+        co2, og2 = torch.empty(2, d["cd"], device=dev), torch.empty(2, nv * S, device=dev)
+        ck_conv, ck_ssm = torch.empty_like(cst), torch.empty_like(states[0])
+
+        def gdn_verify(i):
+            call("it_gdn_conv_l2norm_ckpt", x2.data_ptr(), d["cd"], w.data_ptr(), cst.data_ptr(), co2.data_ptr(),
+                 d["cd"], d["cd"], 2, 4, 2 * nk, 1e-6, ck_conv.data_ptr(), 0, stream_of())
+            call("it_gdn_step_ckpt", co2.data_ptr(), d["cd"], br2.data_ptr(), ar2.data_ptr(), nv, dtv.data_ptr(),
+                 av.data_ptr(), states[i % NST].data_ptr(), og2.data_ptr(), nv * S, 2, nv, nk, S, ck_ssm.data_ptr(), 0,
+                 stream_of())
+        ms = graph_time_ms(torch, lambda: [gdn_verify(i) for i in range(K)], reps=3)
+        res["gdn_verify_nt2_layer_us"] = round(ms * 1000 / K, 3)
+
+        def gdn_reject(i):
+            call("it_gdn_rollback", ck_conv.data_ptr(), cst.data_ptr(), cst.numel(), ck_ssm.data_ptr(),
+                 states[i % NST].data_ptr(), ck_ssm.numel(), stream_of())
+        ms = graph_time_ms(torch, lambda: [gdn_reject(i) for i in range(K)], reps=3)
+        res["gdn_rollback_us"] = round(ms * 1000 / K, 3)
+        log(f"gdn verify nt=2 layer (with checkpoints) {res['gdn_verify_nt2_layer_us']} us, "
+            f"rollback {res['gdn_rollback_us']} us")
         del states
 
         # ------------------------------------------------------------------ GDN chunked prefill (config 5)

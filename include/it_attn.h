@@ -157,6 +157,36 @@ int it_gdn_step(const float* co, int co_tok_stride, const float* beta_raw, const
                 int ba_tok_stride, const float* dt, const float* a, float* state, float* out,
                 int out_tok_stride, int nt, int nv, int nk, int S, void* stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * MTP verify checkpoint and rollback of the recurrent state.
+ * The reference runs a verify batch (the accepted token x and the draft d) one token at a time and
+ * copies the conv and SSM states after token 0 into checkpoint buffers (src/vk/mod.rs:790-801); a
+ * rejected draft copies them back (mtp_reject, src/vk/mod.rs:1018-1025; CPU: mtp.rs:227-234).
+ * Here the kernels that already hold the state for the whole token run write the checkpoint from
+ * registers after token ck_after (0 <= ck_after < nt), without a second pass over the state.
+ * ck_state has the layout of the state it snapshots and must not overlap it.
+ * ---------------------------------------------------------------------------------------------- */
+
+/* it_gdn_conv, plus ck_state[i*cd + ch] = the conv state after token ck_after. */
+int it_gdn_conv_ckpt(const float* x, int x_tok_stride, const float* w, float* state, float* out,
+                     int out_tok_stride, int cd, int nt, int K, float* ck_state, int ck_after, void* stream);
+
+/* it_gdn_conv_l2norm, plus the conv-state checkpoint after token ck_after. */
+int it_gdn_conv_l2norm_ckpt(const float* x, int x_tok_stride, const float* w, float* state, float* out,
+                            int out_tok_stride, int cd, int nt, int K, int nnorm, float eps, float* ck_state,
+                            int ck_after, void* stream);
+
+/* it_gdn_step, plus ck_state[h][i][j] = the SSM state after token ck_after (16-byte aligned). */
+int it_gdn_step_ckpt(const float* co, int co_tok_stride, const float* beta_raw, const float* alpha_raw,
+                     int ba_tok_stride, const float* dt, const float* a, float* state, float* out,
+                     int out_tok_stride, int nt, int nv, int nk, int S, float* ck_state, int ck_after,
+                     void* stream);
+
+/* Rollback after a rejected draft: conv_state <- ck_conv (conv_words floats) and ssm <- ck_ssm
+ * (ssm_words floats), two device copies on the stream (either count may be 0). */
+int it_gdn_rollback(const float* ck_conv, float* conv_state, size_t conv_words, const float* ck_ssm, float* ssm,
+                    size_t ssm_words, void* stream);
+
 /* Same contract and result as it_gdn_step over nt tokens, computed with the chunk-64 WY/UT form of
  * the gated delta rule on f16 MFMA with f32 state and accumulation (a new algorithm: the reference
  * runs the recurrence token-sequentially, kernels/src/lib.rs:285-331). Scratch as returned by

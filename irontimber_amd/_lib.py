@@ -30,6 +30,10 @@ SIGNATURES = {
     "it_l2norm_heads": (c_int, [P, c_int, c_int, c_int, c_int, c_float, P]),
     "it_gdn_conv_l2norm": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "it_gdn_step": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
+    "it_gdn_conv_ckpt": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P, c_int, P]),
+    "it_gdn_conv_l2norm_ckpt": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P]),
+    "it_gdn_step_ckpt": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_int, P]),
+    "it_gdn_rollback": (c_int, [P, P, c_size_t, P, P, c_size_t, P]),
     "it_gdn_chunked_scratch_bytes": (c_size_t, [c_int, c_int, c_int]),
     "it_gdn_chunked": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_size_t, P]),
     "it_attention_scratch_words": (c_size_t, [c_size_t, c_size_t]),

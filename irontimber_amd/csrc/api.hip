@@ -203,7 +203,27 @@ int it_gdn_conv(const float* x, int xts, const float* w, float* state, float* ou
     if (nt > 1 && (xts < cd || ots < cd)) return fail("it_gdn_conv: token strides smaller than cd");
     if (!x || !w || !state || !out) return fail("it_gdn_conv: null buffer");
     if (nt == 0) { g_err.clear(); return 0; }
-    return check(it::launch_gdn_conv(x, xts, w, state, out, ots, cd, nt, K, (hipStream_t)stream), "it_gdn_conv");
+    return check(it::launch_gdn_conv(x, xts, w, state, out, ots, cd, nt, K, nullptr, 0, (hipStream_t)stream),
+                 "it_gdn_conv");
+}
+
+// The checkpoint buffer must not overlap the live state (it is written while the state is read).
+static int validate_ckpt(const char* who, const float* ck, const float* state, size_t words, int ck_after, int nt) {
+    if (!ck) return fail("%s: null checkpoint buffer", who);
+    if (ck_after < 0 || ck_after >= nt) return fail("%s: checkpoint token %d outside [0, %d)", who, ck_after, nt);
+    if (ck < state + words && state < ck + words) return fail("%s: checkpoint buffer overlaps the state", who);
+    return 0;
+}
+
+int it_gdn_conv_ckpt(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt, int K,
+                     float* ck_state, int ck_after, void* stream) {
+    if (K < 2 || K > 4) return fail("it_gdn_conv_ckpt: kernel size %d unsupported (2..4)", K);
+    if (cd <= 0 || nt <= 0) return fail("it_gdn_conv_ckpt: bad geometry cd=%d nt=%d", cd, nt);
+    if (nt > 1 && (xts < cd || ots < cd)) return fail("it_gdn_conv_ckpt: token strides smaller than cd");
+    if (!x || !w || !state || !out) return fail("it_gdn_conv_ckpt: null buffer");
+    if (validate_ckpt("it_gdn_conv_ckpt", ck_state, state, (size_t)(K - 1) * cd, ck_after, nt)) return -1;
+    return check(it::launch_gdn_conv(x, xts, w, state, out, ots, cd, nt, K, ck_state, ck_after, (hipStream_t)stream),
+                 "it_gdn_conv_ckpt");
 }
 
 int it_gdn_conv_l2norm(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt, int K,
@@ -214,8 +234,23 @@ int it_gdn_conv_l2norm(const float* x, int xts, const float* w, float* state, fl
     if (nt > 1 && (xts < cd || ots < cd)) return fail("it_gdn_conv_l2norm: token strides smaller than cd");
     if (!x || !w || !state || !out) return fail("it_gdn_conv_l2norm: null buffer");
     if (nt == 0) { g_err.clear(); return 0; }
-    return check(it::launch_gdn_conv_l2(x, xts, w, state, out, ots, cd, nt, K, nnorm, eps, (hipStream_t)stream),
+    return check(it::launch_gdn_conv_l2(x, xts, w, state, out, ots, cd, nt, K, nnorm, eps, nullptr, 0,
+                                        (hipStream_t)stream),
                  "it_gdn_conv_l2norm");
+}
+
+int it_gdn_conv_l2norm_ckpt(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,
+                            int K, int nnorm, float eps, float* ck_state, int ck_after, void* stream) {
+    const char* who = "it_gdn_conv_l2norm_ckpt";
+    if (K < 2 || K > 4) return fail("%s: kernel size %d unsupported (2..4)", who, K);
+    if (cd <= 0 || cd % 128 != 0 || nt <= 0) return fail("%s: bad geometry cd=%d nt=%d (cd a multiple of 128)", who, cd, nt);
+    if (nnorm < 0 || nnorm * 128 > cd) return fail("%s: %d normalised heads exceed cd=%d", who, nnorm, cd);
+    if (nt > 1 && (xts < cd || ots < cd)) return fail("%s: token strides smaller than cd", who);
+    if (!x || !w || !state || !out) return fail("%s: null buffer", who);
+    if (validate_ckpt(who, ck_state, state, (size_t)(K - 1) * cd, ck_after, nt)) return -1;
+    return check(it::launch_gdn_conv_l2(x, xts, w, state, out, ots, cd, nt, K, nnorm, eps, ck_state, ck_after,
+                                        (hipStream_t)stream),
+                 who);
 }
 
 int it_l2norm_heads(float* x, int ts, int nheads, int d, int nt, float eps, void* stream) {
@@ -244,8 +279,35 @@ int it_gdn_step(const float* co, int cts, const float* br, const float* ar, int 
                 float* state, float* out, int ots, int nt, int nv, int nk, int S, void* stream) {
     if (validate_gdn("it_gdn_step", co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, S)) return -1;
     if (nt == 0) { g_err.clear(); return 0; }
-    return check(it::launch_gdn_step(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, (hipStream_t)stream),
+    return check(it::launch_gdn_step(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, nullptr, 0,
+                                     (hipStream_t)stream),
                  "it_gdn_step");
+}
+
+int it_gdn_step_ckpt(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+                     const float* a, float* state, float* out, int ots, int nt, int nv, int nk, int S, float* ck_state,
+                     int ck_after, void* stream) {
+    if (validate_gdn("it_gdn_step_ckpt", co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, S)) return -1;
+    if (validate_ckpt("it_gdn_step_ckpt", ck_state, state, (size_t)nv * S * S, ck_after, nt)) return -1;
+    if (!aligned16(ck_state)) return fail("it_gdn_step_ckpt: checkpoint buffer must be 16-byte aligned");
+    return check(it::launch_gdn_step(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, ck_state, ck_after,
+                                     (hipStream_t)stream),
+                 "it_gdn_step_ckpt");
+}
+
+int it_gdn_rollback(const float* ck_conv, float* conv_state, size_t conv_words, const float* ck_ssm, float* ssm,
+                    size_t ssm_words, void* stream) {
+    if ((conv_words && (!ck_conv || !conv_state)) || (ssm_words && (!ck_ssm || !ssm)))
+        return fail("it_gdn_rollback: null buffer");
+    hipStream_t st = (hipStream_t)stream;
+    if (conv_words) {
+        const hipError_t e = hipMemcpyAsync(conv_state, ck_conv, conv_words * sizeof(float), hipMemcpyDeviceToDevice, st);
+        if (e != hipSuccess) return check(e, "it_gdn_rollback");
+    }
+    if (ssm_words) return check(hipMemcpyAsync(ssm, ck_ssm, ssm_words * sizeof(float), hipMemcpyDeviceToDevice, st),
+                                "it_gdn_rollback");
+    g_err.clear();
+    return 0;
 }
 
 size_t it_gdn_chunked_scratch_bytes(int nt, int nv, int S) {

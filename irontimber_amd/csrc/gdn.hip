@@ -12,10 +12,13 @@ namespace it {
 // Conv: thread per (channel, run of TT tokens). The K-1 inputs before the run come from x or, for
 // tokens before 0, from the carried state (oldest first). With one run (grid.y == 1) the same
 // thread also writes the new state; otherwise gdn_conv_state_kernel does it after this kernel.
+// ck (optional): with one run, the state after token ck_after is written there from the window
+// (the MTP verify checkpoint); with several runs the host launches gdn_conv_state_kernel for it
+// before this kernel instead.
 template <int K>
 __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__ x, int xts, const float* __restrict__ w,
                                                        float* __restrict__ state, float* __restrict__ out, int ots,
-                                                       int cd, int nt, int TT) {
+                                                       int cd, int nt, int TT, float* __restrict__ ck, int ck_after) {
     const int ch = blockIdx.x * 256 + threadIdx.x;
     if (ch >= cd) return;
     const int t0 = blockIdx.y * TT, t1 = min(nt, t0 + TT);
@@ -37,6 +40,10 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__
 #pragma unroll
         for (int i = 0; i + 1 < K - 1; ++i) win[i] = win[i + 1];
         win[K - 2] = xv;
+        if (ck && t == ck_after && gridDim.y == 1) {
+#pragma unroll
+            for (int i = 0; i < K - 1; ++i) ck[(size_t)i * cd + ch] = win[i];
+        }
     }
     if (gridDim.y == 1) {
 #pragma unroll
@@ -44,9 +51,11 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__
     }
 }
 
+// The conv state after the first nt tokens, from the state before them and x, written to dst
+// (dst == state: the state update after a multi-run conv; dst != state: a checkpoint).
 template <int K>
-__global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __restrict__ x, int xts, float* __restrict__ state,
-                                                             int cd, int nt) {
+__global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __restrict__ x, int xts, const float* state,
+                                                             float* dst, int cd, int nt) {
     const int ch = blockIdx.x * 256 + threadIdx.x;
     if (ch >= cd) return;
     float nv[K - 1];
@@ -56,7 +65,7 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __rest
         nv[i] = tt >= 0 ? x[(size_t)tt * xts + ch] : state[(size_t)(tt + K - 1) * cd + ch];
     }
 #pragma unroll
-    for (int i = 0; i < K - 1; ++i) state[(size_t)i * cd + ch] = nv[i];
+    for (int i = 0; i < K - 1; ++i) dst[(size_t)i * cd + ch] = nv[i];
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -64,12 +73,12 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __rest
 // Wave = (128-channel head block hb, run of TT tokens); lane l holds channels 128hb + l and
 // 128hb + 64 + l, so a token's head vector is the whole wave and its sum of squares one DPP
 // reduction. Head blocks hb < nnorm (the q and k heads) are normalised, x / max(||x||, eps); the
-// rest (v) pass through. State handling as in gdn_conv_kernel.
+// rest (v) pass through. State and checkpoint handling as in gdn_conv_kernel.
 template <int K>
 __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restrict__ x, int xts,
                                                           const float* __restrict__ w, float* __restrict__ state,
                                                           float* __restrict__ out, int ots, int cd, int nt, int TT,
-                                                          int nnorm, float eps) {
+                                                          int nnorm, float eps, float* __restrict__ ck, int ck_after) {
     const int hb = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
     if (hb >= cd / 128) return;   // whole waves
     const bool norm = hb < nnorm;
@@ -109,6 +118,12 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restric
             for (int i = 0; i + 1 < K - 1; ++i) win[c][i] = win[c][i + 1];
             win[c][K - 2] = xv[c];
         }
+        if (ck && t == ck_after && gridDim.y == 1) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int i = 0; i < K - 1; ++i) ck[(size_t)i * cd + ch[c]] = win[c][i];
+        }
     }
     if (gridDim.y == 1) {
 #pragma unroll
@@ -143,10 +158,13 @@ __global__ __launch_bounds__(256) void l2norm_kernel(float* __restrict__ x, int 
 // Workgroup = (16-column block cb, V head h); thread = (column quad cg = tid & 3, row pair
 // rp = tid >> 2): it holds S[2rp..2rp+1][16cb+4cg .. +3]. Column sums over the 128 rows reduce
 // across lanes (xor 4..32) and then across the 4 waves through LDS.
+// ck (optional): the state after token ck_after is also written there, straight from the
+// registers (the MTP verify checkpoint; no second pass over the state).
 __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__ co, int cts, const float* __restrict__ br,
                                                        const float* __restrict__ ar, int bts, const float* __restrict__ dt,
                                                        const float* __restrict__ A, float* __restrict__ state,
-                                                       float* __restrict__ out, int ots, int nt, int nv, int nk) {
+                                                       float* __restrict__ out, int ots, int nt, int nv, int nk,
+                                                       float* __restrict__ ck, int ck_after) {
     constexpr int S = 128;
     __shared__ f4 red1[4][4], red2[4][4];
     const int cb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
@@ -186,6 +204,11 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
             const f4 ot = (red2[0][cg] + red2[1][cg] + red2[2][cg] + red2[3][cg]) * scale;
             *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = ot;
         }
+        if (ck && t == ck_after) {
+            float* cb_ = ck + (size_t)h * S * S;
+            *(f4*)(cb_ + (size_t)i0 * S + j0) = s0;
+            *(f4*)(cb_ + (size_t)(i0 + 1) * S + j0) = s1;
+        }
     }
     *(f4*)(sb + (size_t)i0 * S + j0) = s0;
     *(f4*)(sb + (size_t)(i0 + 1) * S + j0) = s1;
@@ -193,12 +216,14 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
 
 // ------------------------------------------------------------------------------------------------
 hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,
-                           int K, hipStream_t st) {
+                           int K, float* ck, int ck_after, hipStream_t st) {
     const int TT = nt <= 16 ? nt : 16;
     const dim3 grid((cd + 255) / 256, (nt + TT - 1) / TT);
-#define IT_CONV(KK)                                                                              \
-    gdn_conv_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT);           \
-    if (grid.y > 1) gdn_conv_state_kernel<KK><<<grid.x, 256, 0, st>>>(x, xts, state, cd, nt);
+#define IT_CONV(KK)                                                                                           \
+    if (ck && grid.y > 1)                                                                                     \
+        gdn_conv_state_kernel<KK><<<grid.x, 256, 0, st>>>(x, xts, state, ck, cd, ck_after + 1);              \
+    gdn_conv_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, ck, ck_after);          \
+    if (grid.y > 1) gdn_conv_state_kernel<KK><<<grid.x, 256, 0, st>>>(x, xts, state, state, cd, nt);
     switch (K) {
         case 2: IT_CONV(2) break;
         case 3: IT_CONV(3) break;
@@ -209,12 +234,14 @@ hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state
 }
 
 hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd,
-                              int nt, int K, int nnorm, float eps, hipStream_t st) {
+                              int nt, int K, int nnorm, float eps, float* ck, int ck_after, hipStream_t st) {
     const int TT = nt <= 16 ? nt : 16;
     const dim3 grid((cd / 128 + 3) / 4, (nt + TT - 1) / TT);
-#define IT_CONVL2(KK)                                                                                          \
-    gdn_conv_l2_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps);         \
-    if (grid.y > 1) gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, cd, nt);
+#define IT_CONVL2(KK)                                                                                               \
+    if (ck && grid.y > 1)                                                                                           \
+        gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, ck, cd, ck_after + 1);          \
+    gdn_conv_l2_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck, ck_after); \
+    if (grid.y > 1) gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, state, cd, nt);
     switch (K) {
         case 2: IT_CONVL2(2) break;
         case 3: IT_CONVL2(3) break;
@@ -233,8 +260,9 @@ hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps,
 }
 
 hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
-                           const float* a, float* state, float* out, int ots, int nt, int nv, int nk, hipStream_t st) {
-    gdn_step_kernel<<<dim3(8, nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk);
+                           const float* a, float* state, float* out, int ots, int nt, int nv, int nk, float* ck,
+                           int ck_after, hipStream_t st) {
+    gdn_step_kernel<<<dim3(8, nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, ck, ck_after);
     return hipGetLastError();
 }
 

@@ -26,13 +26,15 @@ hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, 
                                    int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
                                    hipStream_t st);
 
+// ck / ck_after: optional checkpoint of the state after token ck_after (null = none).
 hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,
-                           int K, hipStream_t st);
+                           int K, float* ck, int ck_after, hipStream_t st);
 hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd,
-                              int nt, int K, int nnorm, float eps, hipStream_t st);
+                              int nt, int K, int nnorm, float eps, float* ck, int ck_after, hipStream_t st);
 hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps, hipStream_t st);
 hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
-                           const float* a, float* state, float* out, int ots, int nt, int nv, int nk, hipStream_t st);
+                           const float* a, float* state, float* out, int ots, int nt, int nv, int nk, float* ck,
+                           int ck_after, hipStream_t st);
 size_t gdn_chunked_scratch_bytes(int nt, int nv, int S);
 hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,

@@ -105,27 +105,48 @@ def attn_f16(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int, nh:
     return out
 
 
-def gdn_conv(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """x [nt, cd] f32, w [cd, K], state [K-1, cd] (updated in place) -> silu(conv) [nt, cd]."""
+def _ckpt(ckpt, like: torch.Tensor):
+    if ckpt is not None:
+        _need(ckpt, torch.float32, "ckpt")
+        if ckpt.numel() != like.numel():
+            raise ValueError("ckpt must have the shape of the state it snapshots")
+
+
+def gdn_conv(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor, out: torch.Tensor | None = None,
+             ckpt: torch.Tensor | None = None, ckpt_after: int = 0) -> torch.Tensor:
+    """x [nt, cd] f32, w [cd, K], state [K-1, cd] (updated in place) -> silu(conv) [nt, cd].
+    ckpt (optional, shape of state) receives the state after token ckpt_after."""
     _need(x, torch.float32, "x"); _need(w, torch.float32, "w"); _need(state, torch.float32, "state")
+    _ckpt(ckpt, state)
     nt, cd = x.shape
     K = w.shape[1]
     if out is None:
         out = torch.empty_like(x)
-    call("it_gdn_conv", x.data_ptr(), cd, w.data_ptr(), state.data_ptr(), out.data_ptr(), cd, cd, nt, K, _stream())
+    if ckpt is None:
+        call("it_gdn_conv", x.data_ptr(), cd, w.data_ptr(), state.data_ptr(), out.data_ptr(), cd, cd, nt, K, _stream())
+    else:
+        call("it_gdn_conv_ckpt", x.data_ptr(), cd, w.data_ptr(), state.data_ptr(), out.data_ptr(), cd, cd, nt, K,
+             ckpt.data_ptr(), ckpt_after, _stream())
     return out
 
 
 def gdn_conv_l2norm(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor, nnorm: int, eps: float = 1e-6,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
-    """gdn_conv then l2norm_heads(out, nnorm, 128, eps) in one pass (x [nt, cd], cd % 128 == 0)."""
+                    out: torch.Tensor | None = None, ckpt: torch.Tensor | None = None,
+                    ckpt_after: int = 0) -> torch.Tensor:
+    """gdn_conv then l2norm_heads(out, nnorm, 128, eps) in one pass (x [nt, cd], cd % 128 == 0);
+    ckpt as for gdn_conv."""
     _need(x, torch.float32, "x"); _need(w, torch.float32, "w"); _need(state, torch.float32, "state")
+    _ckpt(ckpt, state)
     nt, cd = x.shape
     K = w.shape[1]
     if out is None:
         out = torch.empty_like(x)
-    call("it_gdn_conv_l2norm", x.data_ptr(), cd, w.data_ptr(), state.data_ptr(), out.data_ptr(), cd, cd, nt, K,
-         nnorm, float(eps), _stream())
+    if ckpt is None:
+        call("it_gdn_conv_l2norm", x.data_ptr(), cd, w.data_ptr(), state.data_ptr(), out.data_ptr(), cd, cd, nt, K,
+             nnorm, float(eps), _stream())
+    else:
+        call("it_gdn_conv_l2norm_ckpt", x.data_ptr(), cd, w.data_ptr(), state.data_ptr(), out.data_ptr(), cd, cd, nt,
+             K, nnorm, float(eps), ckpt.data_ptr(), ckpt_after, _stream())
     return out
 
 
@@ -137,9 +158,13 @@ def l2norm_heads(x: torch.Tensor, nheads: int, d: int, eps: float = 1e-6) -> tor
 
 
 def gdn_step(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, out=None, chunked: bool = False,
-             scratch=None):
+             scratch=None, ckpt=None, ckpt_after: int = 0):
     """co [nt, (2nk+nv)S], beta_raw/alpha_raw [nt, nv], dt/a [nv], state [nv, S, S] (in place)
-    -> out [nt, nv*S]. chunked=True uses the chunk-64 scan (it_gdn_chunked)."""
+    -> out [nt, nv*S]. chunked=True uses the chunk-64 scan (it_gdn_chunked). ckpt (optional, shape
+    of state; token-sequential kernel only) receives the state after token ckpt_after."""
+    _ckpt(ckpt, state)
+    if ckpt is not None and chunked:
+        raise ValueError("the checkpoint is a feature of the token-sequential kernel")
     for t, n in ((co, "co"), (beta_raw, "beta_raw"), (alpha_raw, "alpha_raw"), (dt, "dt"), (a, "a"), (state, "state")):
         _need(t, torch.float32, n)
     nt = co.shape[0]
@@ -154,6 +179,19 @@ def gdn_step(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, out=None, 
             scratch = torch.empty(need, device=co.device, dtype=torch.uint8)
         nbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
         call("it_gdn_chunked", *args, _ptr(scratch), nbytes, _stream())
+    elif ckpt is not None:
+        call("it_gdn_step_ckpt", *args, ckpt.data_ptr(), ckpt_after, _stream())
     else:
         call("it_gdn_step", *args, _stream())
     return out
+
+
+def gdn_rollback(ck_conv: torch.Tensor | None, conv_state: torch.Tensor | None, ck_ssm: torch.Tensor | None,
+                 ssm: torch.Tensor | None) -> None:
+    """Restore the checkpointed conv and SSM states after a rejected draft (it_gdn_rollback)."""
+    cw = 0 if conv_state is None else conv_state.numel()
+    sw = 0 if ssm is None else ssm.numel()
+    for c, t in ((ck_conv, conv_state), (ck_ssm, ssm)):
+        if t is not None and (c is None or c.numel() != t.numel()):
+            raise ValueError("checkpoint and state sizes differ")
+    call("it_gdn_rollback", _ptr(ck_conv), _ptr(conv_state), cw, _ptr(ck_ssm), _ptr(ssm), sw, _stream())
