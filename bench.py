@@ -306,6 +306,38 @@ def main():
         res["gdn_step_state_GBs"] = round(gbytes / (gst_us * 1e-6) / 1e9, 1)
         log(f"gdn: layer {res['gdn_decode_layer_us']} us, step {gst_us:.2f} us ({res['gdn_step_state_GBs']} GB/s state)")
 
+        # the reference's whole GDN decode output: recurrence + gated RMSNorm (rmsnorm mode 1), as two
+        # kernels and as one (the per-head recurrence with the epilogue fused)
+        zg = torch.randn(1, nv * S, device=dev)
+        nwg = torch.ones(S, device=dev)
+        og2g = torch.empty(1, nv * S, device=dev)
+
+        def gdn_gated_two(i):
+            gdn_only(i)
+            call("it_gdn_gated_rmsnorm", og.data_ptr(), nv * S, zg.data_ptr(), nv * S, nwg.data_ptr(), 1e-6,
+                 og2g.data_ptr(), nv * S, nv, S, 1, stream_of())
+
+        def gdn_head(i, gated):
+            call("it_gdn_step_gated", co.data_ptr(), d["cd"], br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(),
+                 av.data_ptr(), states[i % NST].data_ptr(), og2g.data_ptr(), nv * S, 1, nv, nk, S,
+                 zg.data_ptr() if gated else None, nv * S, nwg.data_ptr(), 1e-6, None, 0, stream_of())
+        ms = graph_time_ms(torch, lambda: [gdn_gated_two(i) for i in range(K)], reps=3)
+        res["gdn_step_plus_gated_norm_two_kernels_us"] = round(ms * 1000 / K, 3)
+        ms = graph_time_ms(torch, lambda: [gdn_head(i, False) for i in range(K)], reps=3)
+        res["gdn_step_head_kernel_us"] = round(ms * 1000 / K, 3)
+        ms = graph_time_ms(torch, lambda: [gdn_head(i, True) for i in range(K)], reps=3)
+        res["gdn_step_gated_fused_us"] = round(ms * 1000 / K, 3)
+
+        def gdn_layer_gated(i):
+            call("it_gdn_conv_l2norm", x.data_ptr(), d["cd"], w.data_ptr(), cst.data_ptr(), co.data_ptr(), d["cd"],
+                 d["cd"], 1, 4, 2 * nk, 1e-6, stream_of())
+            gdn_head(i, True)
+        ms = graph_time_ms(torch, lambda: [gdn_layer_gated(i) for i in range(K)], reps=3)
+        res["gdn_decode_layer_gated_us"] = round(ms * 1000 / K, 3)
+        log(f"gdn: step + gated norm as two kernels {res['gdn_step_plus_gated_norm_two_kernels_us']} us, "
+            f"per-head step {res['gdn_step_head_kernel_us']} us, fused gated {res['gdn_step_gated_fused_us']} us; "
+            f"layer with the gated output {res['gdn_decode_layer_gated_us']} us")
+
         # MTP verify of [x, draft]: one nt = 2 layer call with the conv and SSM checkpoints after token 0
         d2 = gdn_inputs(3, nt=2, nv=nv, nk=nk)
         x2, br2, ar2 = t(d2["x"]), t(d2["beta_raw"]), t(d2["alpha_raw"])
@@ -361,6 +393,18 @@ def main():
         io = T5 * (2 * nk + nv) * S * 4 + T5 * nv * S * 4 + 2 * 2 * nv * S * S * 4 + 2 * T5 * nv * 4
         res["gdn_prefill_8192_scan_io_GBs"] = round(io / (ms_s * 1e-3) / 1e9, 1)
         log(f"gdn prefill 8192: layer {ms:.3f} ms, scan {ms_s:.3f} ms ({res['gdn_prefill_8192_scan_TFLOPs']} TF/s chunked)")
+        z5 = torch.randn(T5, nv * S, device=dev)
+        nw5 = torch.ones(S, device=dev)
+
+        def gated5():
+            call("it_gdn_gated_rmsnorm", o5.data_ptr(), nv * S, z5.data_ptr(), nv * S, nw5.data_ptr(), 1e-6,
+                 o5.data_ptr(), nv * S, nv, S, T5, stream_of())
+        ms_g = graph_time_ms(torch, lambda: [gated5() for _ in range(10)], reps=3) / 10
+        res["gdn_prefill_8192_gated_norm_us"] = round(ms_g * 1000, 2)
+        res["gdn_prefill_8192_gated_norm_GBs"] = round(3 * T5 * nv * S * 4 / (ms_g * 1e-3) / 1e9, 1)
+        log(f"gdn prefill gated norm: {res['gdn_prefill_8192_gated_norm_us']} us "
+            f"({res['gdn_prefill_8192_gated_norm_GBs']} GB/s)")
+        del z5
 
         # hybrid stack (config 5): 3 GDN prefill layers then 1 attention prefill layer, 8192 tokens
         T = 8192

@@ -157,6 +157,25 @@ int it_gdn_step(const float* co, int co_tok_stride, const float* beta_raw, const
                 int ba_tok_stride, const float* dt, const float* a, float* state, float* out,
                 int out_tok_stride, int nt, int nv, int nk, int S, void* stream);
 
+/* The GDN output's gated RMSNorm, per (token t, V head h) row of S = 128:
+ *   out[t*out_tok_stride + h*S + j] = o_j / sqrt(mean_j(o^2) + eps) * w[j] * silu(z[t*z_tok_stride + h*S + j])
+ * with o the row o[t*o_tok_stride + h*S ...] and w [S] (ssm_norm, shared by the heads). out may be
+ * o itself (in place, like the reference) or a buffer that does not overlap it.
+ * Replaces rmsnorm mode 1, src/vk/mod.rs:808 (kernels/src/lib.rs:207-229; cpu.rs:234-238). */
+int it_gdn_gated_rmsnorm(const float* o, int o_tok_stride, const float* z, int z_tok_stride, const float* w,
+                         float eps, float* out, int out_tok_stride, int nv, int S, int nt, void* stream);
+
+/* it_gdn_step with the gated RMSNorm fused into the output write: one workgroup per V head holds
+ * the head's whole state, so each token's output row is complete before it is stored.
+ *   z, norm_w, eps: as for it_gdn_gated_rmsnorm (z 16-byte aligned, z_tok_stride a multiple of 4);
+ *          z == NULL writes the plain recurrence output (same values as it_gdn_step).
+ *   ck_state, ck_after: the optional MTP verify checkpoint as in it_gdn_step_ckpt (NULL = none).
+ * Replaces the gdn dispatch plus rmsnorm mode 1, src/vk/mod.rs:805-808 (cpu.rs:216-238). */
+int it_gdn_step_gated(const float* co, int co_tok_stride, const float* beta_raw, const float* alpha_raw,
+                      int ba_tok_stride, const float* dt, const float* a, float* state, float* out,
+                      int out_tok_stride, int nt, int nv, int nk, int S, const float* z, int z_tok_stride,
+                      const float* norm_w, float eps, float* ck_state, int ck_after, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * MTP verify checkpoint and rollback of the recurrent state.
  * The reference runs a verify batch (the accepted token x and the draft d) one token at a time and

@@ -33,6 +33,9 @@ SIGNATURES = {
     "it_gdn_conv_ckpt": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P, c_int, P]),
     "it_gdn_conv_l2norm_ckpt": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P]),
     "it_gdn_step_ckpt": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_int, P]),
+    "it_gdn_step_gated": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_int, P,
+                                  c_float, P, c_int, P]),
+    "it_gdn_gated_rmsnorm": (c_int, [P, c_int, P, c_int, P, c_float, P, c_int, c_int, c_int, c_int, P]),
     "it_gdn_rollback": (c_int, [P, P, c_size_t, P, P, c_size_t, P]),
     "it_gdn_chunked_scratch_bytes": (c_size_t, [c_int, c_int, c_int]),
     "it_gdn_chunked": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_size_t, P]),

@@ -295,6 +295,41 @@ int it_gdn_step_ckpt(const float* co, int cts, const float* br, const float* ar,
                  "it_gdn_step_ckpt");
 }
 
+int it_gdn_step_gated(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+                      const float* a, float* state, float* out, int ots, int nt, int nv, int nk, int S, const float* z,
+                      int zts, const float* norm_w, float eps, float* ck_state, int ck_after, void* stream) {
+    const char* who = "it_gdn_step_gated";
+    if (validate_gdn(who, co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, S)) return -1;
+    if (z) {
+        if (!norm_w) return fail("%s: null norm weight", who);
+        if (!aligned16(z) || !aligned16(norm_w) || zts % 4 != 0) return fail("%s: z / norm_w must be 16-byte aligned", who);
+        if (nt > 1 && zts < nv * S) return fail("%s: z token stride overlaps rows", who);
+        if (!(eps >= 0.0f)) return fail("%s: eps must be >= 0", who);
+    }
+    if (ck_state) {
+        if (validate_ckpt(who, ck_state, state, (size_t)nv * S * S, ck_after, nt)) return -1;
+        if (!aligned16(ck_state)) return fail("%s: checkpoint buffer must be 16-byte aligned", who);
+    }
+    if (nt == 0) { g_err.clear(); return 0; }
+    return check(it::launch_gdn_step_head(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, z, zts, norm_w, eps,
+                                          ck_state, ck_state ? ck_after : 0, (hipStream_t)stream),
+                 who);
+}
+
+int it_gdn_gated_rmsnorm(const float* o, int ots, const float* z, int zts, const float* w, float eps, float* out,
+                         int outs, int nv, int S, int nt, void* stream) {
+    const char* who = "it_gdn_gated_rmsnorm";
+    if (S != 128) return fail("%s: head size %d unsupported (128)", who, S);
+    if (nv <= 0 || nt < 0) return fail("%s: bad geometry nv=%d nt=%d", who, nv, nt);
+    if (!o || !z || !w || !out) return fail("%s: null buffer", who);
+    if (nt > 1 && (ots < nv * S || zts < nv * S || outs < nv * S)) return fail("%s: token strides overlap rows", who);
+    if (out != o && out < o + (size_t)(nt ? nt - 1 : 0) * ots + (size_t)nv * S && o < out + (size_t)(nt ? nt - 1 : 0) * outs + (size_t)nv * S)
+        return fail("%s: out must be o itself or not overlap it", who);
+    if (!(eps >= 0.0f)) return fail("%s: eps must be >= 0", who);
+    if (nt == 0) { g_err.clear(); return 0; }
+    return check(it::launch_gdn_gated_norm(o, ots, z, zts, w, eps, out, outs, nv, nt, (hipStream_t)stream), who);
+}
+
 int it_gdn_rollback(const float* ck_conv, float* conv_state, size_t conv_words, const float* ck_ssm, float* ssm,
                     size_t ssm_words, void* stream) {
     if ((conv_words && (!ck_conv || !conv_state)) || (ssm_words && (!ck_ssm || !ssm)))

@@ -215,6 +215,111 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------------
+// Gated RMSNorm epilogue of the GDN output, per (token, V head) row of 128:
+//   out = o / sqrt(mean(o^2) + eps) * w * silu(z)
+// One wave per row, lane l holds elements l and l + 64. out may alias o.
+__global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const float* o, int ots, const float* __restrict__ z,
+                                                             int zts, const float* __restrict__ w, float eps,
+                                                             float* out, int outs, int nv, int nt) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (row >= nv * nt) return;   // whole waves
+    const int t = row / nv, h = row - t * nv;
+    const float* op = o + (size_t)t * ots + (size_t)h * 128;
+    const float* zp = z + (size_t)t * zts + (size_t)h * 128;
+    const float a = op[l], b = op[l + 64];
+    const float za = zp[l], zb = zp[l + 64], wa = w[l], wb = w[l + 64];
+    const float sc = 1.0f / sqrtf(wave_sum(a * a + b * b) * (1.0f / 128.0f) + eps);
+    float* dp = out + (size_t)t * outs + (size_t)h * 128;
+    dp[l] = (a * sc) * wa * siluf_(za);
+    dp[l + 64] = (b * sc) * wb * siluf_(zb);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Gated-delta recurrence with one workgroup per V head (all 128 columns), so the head's output row
+// is complete inside the workgroup and the gated RMSNorm epilogue can be applied before the store.
+// Thread = (column quad cq = tid & 31, row group rg = tid >> 5): it holds S[16rg .. 16rg+15][4cq ..
+// 4cq+3] (64 floats). Column sums: 16 rows in the thread, rows 16rg and 16(rg^1) by a lane^32
+// swap, then the 4 waves through LDS. z == nullptr: plain output (o = S^T q / sqrt(S)).
+__global__ __launch_bounds__(256) void gdn_step_head_kernel(
+    const float* __restrict__ co, int cts, const float* __restrict__ br, const float* __restrict__ ar, int bts,
+    const float* __restrict__ dt, const float* __restrict__ A, float* __restrict__ state, float* __restrict__ out,
+    int ots, int nt, int nk, const float* __restrict__ z, int zts, const float* __restrict__ nw, float eps,
+    float* __restrict__ ck, int ck_after) {
+    constexpr int S = 128, R = 16;
+    __shared__ f4 red1[4][32], red2[4][32];
+    const int h = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int cq = tid & 31, rg = tid >> 5;
+    const int kh = h % nk, qk = nk * S, j0 = 4 * cq, i0 = R * rg;
+    float* sb = state + (size_t)h * S * S;
+    f4 s[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) s[r] = ld_f4(sb + (size_t)(i0 + r) * S + j0);
+    const float scale = 1.0f / sqrtf((float)S);
+    const float dth = dt[h], ah = A[h];
+    // Unconditional loads from a valid address when there is no epilogue: a load under a branch
+    // makes the compiler wait for every load before it (here the whole state slice).
+    const float* zb = z ? z : co;
+    const int zstride = z ? zts : 0;
+    const f4 wv = ld_f4((z ? nw : co) + j0);
+    for (int t = 0; t < nt; ++t) {
+        const float* c = co + (size_t)t * cts;
+        f4 q[R / 4], k[R / 4];
+#pragma unroll
+        for (int r = 0; r < R / 4; ++r) {
+            q[r] = ld_f4(c + kh * S + i0 + 4 * r);
+            k[r] = ld_f4(c + qk + kh * S + i0 + 4 * r);
+        }
+        const f4 v = ld_f4(c + 2 * qk + h * S + j0);
+        const f4 zv = ld_f4(zb + (size_t)t * zstride + (z ? (size_t)h * S : 0) + j0);   // issued with the token's loads
+        const float beta = sigmoidf_(br[(size_t)t * bts + h]);
+        const float eg = expf(softplusf_(ar[(size_t)t * bts + h] + dth) * ah);
+        f4 p = {};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            s[r] *= eg;
+            p += s[r] * k[r / 4][r & 3];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = sum_xor32(p[j]);
+        if (l < 32) red1[w][cq] = p;
+        __syncthreads();
+        const f4 sk = red1[0][cq] + red1[1][cq] + red1[2][cq] + red1[3][cq];
+        const f4 delta = (v - sk) * beta;
+        f4 o = {};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            s[r] += k[r / 4][r & 3] * delta;
+            o += s[r] * q[r / 4][r & 3];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = sum_xor32(o[j]);
+        if (l < 32) red2[w][cq] = o;
+        __syncthreads();
+        if (w == 0) {
+            const f4 ot = (red2[0][cq] + red2[1][cq] + red2[2][cq] + red2[3][cq]) * scale;
+            f4 res = ot;
+            if (z) {
+                // lanes 32..63 repeat lanes 0..31: the wave sum counts every column twice
+                const float ss = wave_sum(ot[0] * ot[0] + ot[1] * ot[1] + ot[2] * ot[2] + ot[3] * ot[3]) * 0.5f;
+                const float sc = 1.0f / sqrtf(ss * (1.0f / S) + eps);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) res[j] = (ot[j] * sc) * wv[j] * siluf_(zv[j]);
+            }
+            if (l < 32) *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = res;
+        }
+        if (ck && t == ck_after) {
+            float* cb_ = ck + (size_t)h * S * S;
+#pragma unroll
+            for (int r = 0; r < R; ++r) *(f4*)(cb_ + (size_t)(i0 + r) * S + j0) = s[r];
+        }
+        // red1/red2 are rewritten by the next token only after its first barrier, which every
+        // wave reaches after finishing this token's reads.
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) *(f4*)(sb + (size_t)(i0 + r) * S + j0) = s[r];
+}
+
+// ------------------------------------------------------------------------------------------------
 hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,
                            int K, float* ck, int ck_after, hipStream_t st) {
     const int TT = nt <= 16 ? nt : 16;
@@ -263,6 +368,22 @@ hipError_t launch_gdn_step(const float* co, int cts, const float* br, const floa
                            const float* a, float* state, float* out, int ots, int nt, int nv, int nk, float* ck,
                            int ck_after, hipStream_t st) {
     gdn_step_kernel<<<dim3(8, nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, ck, ck_after);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_step_head(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+                                const float* a, float* state, float* out, int ots, int nt, int nv, int nk,
+                                const float* z, int zts, const float* nw, float eps, float* ck, int ck_after,
+                                hipStream_t st) {
+    gdn_step_head_kernel<<<dim3(nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nk, z, zts, nw,
+                                                   eps, ck, ck_after);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_gated_norm(const float* o, int ots, const float* z, int zts, const float* w, float eps,
+                                 float* out, int outs, int nv, int nt, hipStream_t st) {
+    const long rows = (long)nv * nt;
+    gdn_gated_norm_kernel<<<dim3((unsigned)((rows + 3) / 4)), 256, 0, st>>>(o, ots, z, zts, w, eps, out, outs, nv, nt);
     return hipGetLastError();
 }
 

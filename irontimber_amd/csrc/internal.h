@@ -35,6 +35,12 @@ hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps,
 hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                            const float* a, float* state, float* out, int ots, int nt, int nv, int nk, float* ck,
                            int ck_after, hipStream_t st);
+hipError_t launch_gdn_step_head(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+                                const float* a, float* state, float* out, int ots, int nt, int nv, int nk,
+                                const float* z, int zts, const float* nw, float eps, float* ck, int ck_after,
+                                hipStream_t st);
+hipError_t launch_gdn_gated_norm(const float* o, int ots, const float* z, int zts, const float* w, float eps,
+                                 float* out, int outs, int nv, int nt, hipStream_t st);
 size_t gdn_chunked_scratch_bytes(int nt, int nv, int S);
 hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,

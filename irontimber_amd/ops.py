@@ -186,6 +186,36 @@ def gdn_step(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, out=None, 
     return out
 
 
+def gdn_gated_rmsnorm(o: torch.Tensor, z: torch.Tensor, w: torch.Tensor, nv: int, eps: float = 1e-6,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """o, z [nt, nv*128], w [128] -> o / rms(o) * w * silu(z) per 128-wide head row (out may be o)."""
+    _need(o, torch.float32, "o"); _need(z, torch.float32, "z"); _need(w, torch.float32, "w")
+    if out is None:
+        out = torch.empty_like(o)
+    call("it_gdn_gated_rmsnorm", o.data_ptr(), o.shape[1], z.data_ptr(), z.shape[1], w.data_ptr(), float(eps),
+         out.data_ptr(), out.shape[1], nv, 128, o.shape[0], _stream())
+    return out
+
+
+def gdn_step_gated(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, z=None, norm_w=None, eps: float = 1e-6,
+                   out=None, ckpt=None, ckpt_after: int = 0):
+    """The recurrence with one workgroup per V head and, when z is given, the gated RMSNorm
+    (o / rms(o) * norm_w * silu(z)) fused into the output write (it_gdn_step_gated)."""
+    for t, n in ((co, "co"), (beta_raw, "beta_raw"), (alpha_raw, "alpha_raw"), (dt, "dt"), (a, "a"), (state, "state")):
+        _need(t, torch.float32, n)
+    if z is not None:
+        _need(z, torch.float32, "z"); _need(norm_w, torch.float32, "norm_w")
+    _ckpt(ckpt, state)
+    nt = co.shape[0]
+    S = state.shape[-1]
+    if out is None:
+        out = torch.empty(nt, nv * S, device=co.device, dtype=torch.float32)
+    call("it_gdn_step_gated", co.data_ptr(), co.shape[1], beta_raw.data_ptr(), alpha_raw.data_ptr(), beta_raw.shape[1],
+         dt.data_ptr(), a.data_ptr(), state.data_ptr(), out.data_ptr(), out.shape[1], nt, nv, nk, S, _ptr(z),
+         0 if z is None else z.shape[1], _ptr(norm_w), float(eps), _ptr(ckpt), ckpt_after, _stream())
+    return out
+
+
 def gdn_rollback(ck_conv: torch.Tensor | None, conv_state: torch.Tensor | None, ck_ssm: torch.Tensor | None,
                  ssm: torch.Tensor | None) -> None:
     """Restore the checkpointed conv and SSM states after a rejected draft (it_gdn_rollback)."""

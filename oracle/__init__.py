@@ -30,6 +30,7 @@ _SIG = {
     "it_ref_f16_to_f32": (_f, [ctypes.c_uint16]),
     "it_ref_rmsnorm": (None, [_P, _P, _i, _f, _P]),
     "it_ref_l2norm": (None, [_P, _i, _f]),
+    "it_ref_gdn_gated_norm": (None, [_P, _P, _P, _i, _i, _i, _i, _f, _P]),
     "it_ref_rope_theta_scale": (_f, [_f, _i]),
     "it_ref_rope": (None, [_P, _i, _i, _i, _i, _f, _P]),
     "it_ref_attn_prep": (None, [_P, _i, _P, _i, _P, _P, _f, _P, _i, _i, _i, _i, _i, _i, _f, _P]),
@@ -148,3 +149,13 @@ def attn_prep(q: np.ndarray, k: np.ndarray, q_norm, k_norm, eps: float, pos0: in
                            None if kn is None else _p(kn), eps, _p(ko), pos0, hd, nh, nkv, nt, n_rot, base,
                            _p(_sections(sections)))
     return q, ko
+
+
+def gdn_gated_norm(o: np.ndarray, z: np.ndarray, w: np.ndarray, nv: int, eps: float = 1e-6) -> np.ndarray:
+    """cpu.rs:234-238: per hv-wide head row, rmsnorm(o) * w * silu(z). o, z [nt, nv*hv]."""
+    o = np.ascontiguousarray(o, np.float32); z = np.ascontiguousarray(z, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    nt = o.shape[0]; hv = w.shape[0]
+    out = np.zeros_like(o)
+    lib().it_ref_gdn_gated_norm(_p(o), _p(z), _p(w), nv, hv, nt, o.shape[1], eps, _p(out))
+    return out

@@ -19,6 +19,8 @@
 //                        the sector rule's fixed dims, pair norms, relative-position invariance of
 //                        q.k, and an f64 statement with exact angles (error bounded by the f32
 //                        angle recurrence); it_ref_rmsnorm -- unit RMS, constant rows.
+//   it_ref_gdn_gated_norm -- z = 0 gives 0, large z gives rmsnorm(o)*w*z, constant rows, an f64
+//                        statement.
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -140,6 +142,19 @@ void it_ref_attn_prep(float* q, int q_tok_stride, const float* k, int kv_tok_str
             it_ref_rope(ko, 1, hd, n_rot, pos0 + t, base, sections);
         }
     }
+}
+
+// cpu.rs:234-238 gated RMSNorm of the GDN output, per V head row of hv floats for nt tokens:
+// out = rmsnorm(o_h, w, eps) * silu(z_h), rows at o[t*tok_stride + h*hv], z and out alike.
+void it_ref_gdn_gated_norm(const float* o, const float* z, const float* w, int nv, int hv, int nt, int tok_stride,
+                           float eps, float* out) {
+    std::vector<float> n(hv);
+    for (int t = 0; t < nt; ++t)
+        for (int h = 0; h < nv; ++h) {
+            const size_t b = (size_t)t * tok_stride + (size_t)h * hv;
+            it_ref_rmsnorm(o + b, w, hv, eps, n.data());
+            for (int j = 0; j < hv; ++j) out[b + j] = n[j] * silu(z[b + j]);
+        }
 }
 
 // cpu.rs:164 l2norm, in place.

@@ -166,3 +166,88 @@ def test_chunked_prefill_config5(dev):
     st2 = dev_f32(d["state"], dev)
     seq = host(ops.gdn_step(co, *args, st2, nv, nk))
     assert np.abs(seq - out).max() <= OUT_TOL and np.abs(host(st2) - gst).max() <= STATE_TOL
+
+
+def _z_and_w(seed, nt, nv, S=128):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((nt, nv * S)).astype(np.float32),
+            (1 + 0.1 * rng.standard_normal(S)).astype(np.float32))
+
+
+@pytest.mark.parametrize("nt,nv", [(1, 32), (5, 32), (300, 8)])
+def test_gated_rmsnorm(dev, nt, nv):
+    """it_gdn_gated_rmsnorm (rmsnorm mode 1, vk/mod.rs:808) against cpu.rs:234-238, in place and
+    into a separate buffer."""
+    announce(f"gated rmsnorm nt={nt} nv={nv}")
+    o = np.random.default_rng(nt).standard_normal((nt, nv * 128)).astype(np.float32)
+    z, w = _z_and_w(7, nt, nv)
+    want = oracle.gdn_gated_norm(o, z, w, nv)
+    od, zd, wd = dev_f32(o, dev), dev_f32(z, dev), dev_f32(w, dev)
+    got = host(ops.gdn_gated_rmsnorm(od, zd, wd, nv))
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    ops.gdn_gated_rmsnorm(od, zd, wd, nv, out=od)
+    np.testing.assert_array_equal(host(od), got)
+
+
+@pytest.mark.parametrize("nt,nv,nk", [(1, 32, 16), (4, 32, 16), (2, 4, 2), (17, 8, 8)])
+def test_step_head_kernel_plain(dev, nt, nv, nk):
+    """The one-workgroup-per-head recurrence without the epilogue (z = NULL) equals the oracle like
+    it_gdn_step does (1e-5), and it_gdn_step within the same bound."""
+    announce(f"gdn_step_gated plain nt={nt} nv={nv}")
+    d = gdn_step_inputs(3, nt, nv=nv, nk=nk)
+    want, wst = oracle.gdn_step(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
+    args = [dev_f32(d[k], dev) for k in ("co", "beta_raw", "alpha_raw", "dt", "a")]
+    st = dev_f32(d["state"], dev)
+    got = host(ops.gdn_step_gated(*args, st, nv, nk))
+    assert np.abs(got - want).max() <= 1e-5 and np.abs(host(st) - wst).max() <= 1e-5
+    st2 = dev_f32(d["state"], dev)
+    other = host(ops.gdn_step(*args, st2, nv, nk))
+    assert np.abs(got - other).max() <= 1e-5
+
+
+@pytest.mark.parametrize("nt,nv,nk,ck_after", [(1, 32, 16, -1), (4, 32, 16, 0), (2, 32, 16, 0), (9, 8, 4, 5)])
+def test_step_gated(dev, nt, nv, nk, ck_after):
+    """The recurrence with the gated RMSNorm fused into its output write equals cpu.rs:216-238
+    (recurrence then rmsnorm(o)*w*silu(z)); the optional checkpoint is the prefix state."""
+    announce(f"gdn_step_gated nt={nt} nv={nv} ck={ck_after}")
+    d = gdn_step_inputs(8, nt, nv=nv, nk=nk)
+    z, w = _z_and_w(9, nt, nv)
+    o_ref, wst = oracle.gdn_step(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
+    want = oracle.gdn_gated_norm(o_ref, z, w, nv)
+    args = [dev_f32(d[k], dev) for k in ("co", "beta_raw", "alpha_raw", "dt", "a")]
+    st = dev_f32(d["state"], dev)
+    ck = torch.full_like(st, float("nan")) if ck_after >= 0 else None
+    got = host(ops.gdn_step_gated(*args, st, nv, nk, z=dev_f32(z, dev), norm_w=dev_f32(w, dev), ckpt=ck,
+                                  ckpt_after=max(ck_after, 0)))
+    e = np.abs(got - want).max()
+    print(f"gated out max_abs={e:.3g}")
+    assert e <= 1e-4 and np.abs(host(st) - wst).max() <= 1e-5
+    if ck is not None:
+        st_pre = dev_f32(d["state"], dev)
+        n = ck_after + 1
+        ops.gdn_step_gated(*[x[:n].contiguous() for x in args[:3]], *args[3:], st_pre, nv, nk)
+        np.testing.assert_array_equal(host(ck), host(st_pre))
+
+
+def test_gated_layer_config4(dev):
+    """BASELINE config 4 (seed 3) as the reference's whole GDN decode layer up to the output
+    projection: conv + L2 (fused), the recurrence with the fused gated RMSNorm, against cpu.rs
+    (layer pass, then the gated norm of cpu.rs:234-238); argmax of a fixed projection agrees."""
+    nv, nk, S = 32, 16, 128
+    d = gdn_inputs(3, nt=1, nv=nv, nk=nk)
+    z, w = _z_and_w(10, 1, nv)
+    co_ref = np.zeros((1, d["cd"]), np.float32)
+    cst, sst = d["conv_state"].copy(), d["state"].copy()
+    out_ref = np.zeros((1, nv * S), np.float32)
+    P = lambda a: a.ctypes.data
+    oracle.lib().it_ref_gdn_layer(P(d["x"]), d["cd"], P(d["w"]), P(cst), 4, P(d["beta_raw"]), P(d["alpha_raw"]), nv,
+                                  P(d["dt"]), P(d["a"]), P(sst), P(out_ref), nv * S, P(co_ref), 1, nv, nk, S, 1e-6, 8)
+    want = oracle.gdn_gated_norm(out_ref, z, w, nv)
+    cs, st = dev_f32(d["conv_state"], dev), dev_f32(d["state"], dev)
+    co = ops.gdn_conv_l2norm(dev_f32(d["x"], dev), dev_f32(d["w"], dev), cs, 2 * nk)
+    out = host(ops.gdn_step_gated(co, dev_f32(d["beta_raw"], dev), dev_f32(d["alpha_raw"], dev), dev_f32(d["dt"], dev),
+                                  dev_f32(d["a"], dev), st, nv, nk, z=dev_f32(z, dev), norm_w=dev_f32(w, dev)))
+    assert np.abs(out - want).max() <= OUT_TOL
+    assert np.abs(host(st) - sst).max() <= STATE_TOL
+    np.testing.assert_array_equal(host(cs), cst)
+    assert_argmax_agrees(out, want)

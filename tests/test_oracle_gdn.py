@@ -102,3 +102,24 @@ def test_layer_matches_pieces():
     o64, s64 = gdn_seq_f64(co, d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
     np.testing.assert_allclose(o1, o64, atol=2e-6)
     np.testing.assert_allclose(s1, s64, atol=2e-6)
+
+
+def test_gated_norm_closed_forms():
+    """cpu.rs:234-238 gated RMSNorm: z = 0 gives 0; large z gives rmsnorm(o)*w*z; a constant row c
+    gives c/sqrt(c^2+eps)*w*silu(z); random rows against a float64 statement."""
+    rng = np.random.default_rng(5)
+    nv, hv, nt = 4, 128, 3
+    o = rng.standard_normal((nt, nv * hv)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(hv)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.gdn_gated_norm(o, np.zeros_like(o), w, nv), np.zeros_like(o))
+    big = np.full_like(o, 40.0)
+    o64 = o.reshape(nt, nv, hv).astype(np.float64)
+    rn = o64 / np.sqrt((o64 ** 2).mean(-1, keepdims=True) + 1e-6) * w
+    np.testing.assert_allclose(oracle.gdn_gated_norm(o, big, w, nv).reshape(nt, nv, hv), rn * 40.0, rtol=2e-6, atol=1e-6)
+    c = np.full_like(o, -2.5)
+    z = rng.standard_normal(o.shape).astype(np.float32)
+    silu = z / (1 + np.exp(-z.astype(np.float64)))
+    want = (-2.5 / np.sqrt(6.25 + 1e-6)) * np.tile(w, nv)[None, :] * silu
+    np.testing.assert_allclose(oracle.gdn_gated_norm(c, z, w, nv), want, rtol=2e-6, atol=1e-7)
+    want = (rn * silu.reshape(nt, nv, hv)).reshape(nt, -1)
+    np.testing.assert_allclose(oracle.gdn_gated_norm(o, z, w, nv), want, rtol=1e-5, atol=1e-6)
