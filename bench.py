@@ -93,7 +93,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-chunk", type=int, default=0, help="keys per split for decode (0 = library policy)")
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "gdn", "prep"], default="all",
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "gdn", "prep", "mtp"], default="all",
                     help="run one section only (profiling runs); the JSON line then carries that section's figures")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain device copies of 256 MiB (reference reading for the FETCH_SIZE / "
@@ -275,6 +275,36 @@ def main():
         log(f"prep: decode {res['prep_decode_us']} us, chunk64 {res['prep_chunk64_us']} us, 8192 tokens "
             f"{res['prep_8192_us']} us ({res['prep_8192_GBs']} GB/s)")
         del pq, pk, pv, pkc, pvc
+
+    # ------------------------------------------------------------------ MTP head: f32-KV attention
+    if args.only in ("all", "mtp"):
+        S8 = 8192
+        NMT = 12   # 12 f32 caches of 32 MiB: 384 MiB rotated, beyond the 256 MB MALL
+        g = torch.Generator(device=dev).manual_seed(5)
+        kf = [torch.randn(S8, KVD, device=dev, generator=g) for _ in range(NMT)]
+        vf = [torch.randn(S8, KVD, device=dev, generator=g) for _ in range(NMT)]
+        qm = torch.randn(64, NH * 2 * HD, device=dev, generator=g)
+        om = torch.empty(64, NH * HD, device=dev)
+        from irontimber_amd._lib import lib as _lm
+        scm = torch.empty(max(_lm().it_attn_f32kv_scratch_bytes(S8 - 64, 64, HD, NH, NKV),
+                              _lm().it_attn_f32kv_scratch_bytes(S8 - 2, 2, HD, NH, NKV)), dtype=torch.uint8, device=dev)
+
+        def mtp_attn(i, nt, pos0):
+            call("it_attn_f32kv", qm.data_ptr(), NH * 2 * HD, kf[i % NMT].data_ptr(), vf[i % NMT].data_ptr(), KVD, pos0,
+                 HD, NH, NKV, nt, scale, om.data_ptr(), NH * HD, scm.data_ptr(), scm.numel(), stream_of())
+        ms = graph_time_ms(torch, lambda: [mtp_attn(i, 1, S8 - 1) for i in range(K)], reps=3)
+        us = ms * 1000 / K
+        fb = 2 * S8 * KVD * 4 + NH * 2 * HD * 4 + NH * HD * 4
+        res["mtp_f32kv_decode_8192_us"] = round(us, 3)
+        res["mtp_f32kv_decode_8192_GBs"] = round(fb / (us * 1e-6) / 1e9, 1)
+        ms = graph_time_ms(torch, lambda: [mtp_attn(i, 2, S8 - 2) for i in range(K)], reps=3)
+        res["mtp_f32kv_nt2_8192_us"] = round(ms * 1000 / K, 3)
+        ms = graph_time_ms(torch, lambda: [mtp_attn(i, 64, 4096) for i in range(20)], reps=3)
+        res["mtp_f32kv_catchup64_at4096_us"] = round(ms * 1000 / 20, 2)
+        log(f"mtp f32-KV attention: decode 8192 slots {res['mtp_f32kv_decode_8192_us']} us "
+            f"({res['mtp_f32kv_decode_8192_GBs']} GB/s), nt=2 {res['mtp_f32kv_nt2_8192_us']} us, "
+            f"64-token catch-up at 4096 {res['mtp_f32kv_catchup64_at4096_us']} us")
+        del kf, vf, scm
 
     # ------------------------------------------------------------------ GDN decode step (config 4)
     if args.only in ("all", "gdn"):

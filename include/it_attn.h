@@ -113,6 +113,33 @@ int it_attn_combine(const float* q, int q_tok_stride, const float* part, int pos
                     float* out, int out_tok_stride, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * The MTP head's attention over its own f32 KV cache (src/mtp.rs:96-130; src/vk/mod.rs:917-942).
+ * Slot p of that cache holds position p + 1 (mtp.rs:120, vk/mod.rs:932).
+ * ---------------------------------------------------------------------------------------------- */
+
+/* it_attn_prep_f16 for an f32 cache: token t is roped at position pos0 + t and its normed, roped K
+ * row and its V row are stored as f32 at cache row row0 + t (for the MTP head row0 = pos0 - 1).
+ * Replaces the MTP pass's rmsnorm mode 0 (q_norm, k_norm) and rope dispatches, src/vk/mod.rs:933-938
+ * (its k/v matvecs write the cache rows directly; here they write k, v and this call stores them). */
+int it_attn_prep_f32kv(float* q, int q_tok_stride, const float* k, const float* v, int kv_tok_stride,
+                       const float* q_norm, const float* k_norm, float eps, float* kc, float* vc, int kvd,
+                       int pos0, int row0, int hd, int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0,
+                       int sec1, int sec2, int sec3, void* stream);
+
+/* Bytes of scratch it_attn_f32kv needs (split-K partial records, same 260-float layout). */
+size_t it_attn_f32kv_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv);
+
+/* Causal GQA attention with sigmoid gate over an f32 KV cache: it_attn_f16's semantics and
+ * buffers with kc, vc as f32 [row][kvd]. Query t sees cache rows 0..pos0+t (for the MTP head pass
+ * pos0 is the first query's slot, position - 1). hd == 256, at most 16 q heads per KV head; the
+ * scratch (it_attn_f32kv_scratch_bytes) is required.
+ * Replaces VkEngine::attention(..., f16 = false) for the MTP head, src/vk/mod.rs:707-709 and 942
+ * (attn_s + attn_comb, kernels/src/lib.rs:682-740; CPU src/mtp.rs:122-130). */
+int it_attn_f32kv(const float* q, int q_tok_stride, const float* kc, const float* vc, int kvd, int pos0, int hd,
+                  int nh, int nkv, int nt, float scale, float* out, int out_tok_stride, void* scratch,
+                  size_t scratch_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Gated DeltaNet: short causal conv, q/k L2 norm, gated-delta recurrence.
  * ---------------------------------------------------------------------------------------------- */
 

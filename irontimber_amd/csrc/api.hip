@@ -91,11 +91,10 @@ int it_kv_append_f16(const float* k, const float* v, int src_tok_stride, uint16_
                  "it_kv_append_f16");
 }
 
-int it_attn_prep_f16(float* q, int qts, const float* k, const float* v, int kts, const float* q_norm,
-                     const float* k_norm, float eps, uint16_t* kc, uint16_t* vc, int kvd, int pos0, int hd, int nh,
-                     int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1, int sec2, int sec3,
-                     int round_mode, void* stream) {
-    const char* who = "it_attn_prep_f16";
+static int validate_prep(const char* who, const float* q, int qts, const float* k, const float* v, int kts,
+                         const float* q_norm, const float* k_norm, float eps, const void* kc, const void* vc, int kvd,
+                         int pos0, int hd, int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1,
+                         int sec2, int sec3) {
     if (hd != 128 && hd != 256) return fail("%s: head_dim %d unsupported (128 or 256)", who, hd);
     if (nh <= 0 || nkv <= 0 || nh % nkv != 0) return fail("%s: n_head %d / n_head_kv %d invalid", who, nh, nkv);
     if (kvd != nkv * hd) return fail("%s: kvd %d != n_head_kv*head_dim %d", who, kvd, nkv * hd);
@@ -106,17 +105,73 @@ int it_attn_prep_f16(float* q, int qts, const float* k, const float* v, int kts,
     if (sec0 < 0 || sec1 < 0 || sec2 < 0 || sec3 < 0) return fail("%s: rope sections must be >= 0", who);
     if (!(theta_scale > 0.0f) || !(theta_scale <= 1.0f)) return fail("%s: theta_scale %g must be in (0, 1]", who, theta_scale);
     if (!(eps >= 0.0f)) return fail("%s: eps must be >= 0", who);
-    if (round_mode != 0 && round_mode != 1) return fail("%s: round_mode must be 0 (RNE) or 1 (RTZ)", who);
     if (!q || !k || !v || !kc || !vc) return fail("%s: null buffer", who);
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(kc) || !aligned16(vc) ||
         (q_norm && !aligned16(q_norm)) || (k_norm && !aligned16(k_norm)))
         return fail("%s: buffers must be 16-byte aligned", who);
     if (qts % 4 != 0 || kts % 4 != 0) return fail("%s: token strides must be multiples of 4", who);
     if (nt > 1 && (qts < 2 * nh * hd || kts < kvd)) return fail("%s: token strides overlap rows", who);
+    return 0;
+}
+
+int it_attn_prep_f16(float* q, int qts, const float* k, const float* v, int kts, const float* q_norm,
+                     const float* k_norm, float eps, uint16_t* kc, uint16_t* vc, int kvd, int pos0, int hd, int nh,
+                     int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1, int sec2, int sec3,
+                     int round_mode, void* stream) {
+    const char* who = "it_attn_prep_f16";
+    if (validate_prep(who, q, qts, k, v, kts, q_norm, k_norm, eps, kc, vc, kvd, pos0, hd, nh, nkv, nt, n_rot,
+                      theta_scale, sec0, sec1, sec2, sec3))
+        return -1;
+    if (round_mode != 0 && round_mode != 1) return fail("%s: round_mode must be 0 (RNE) or 1 (RTZ)", who);
     if (nt == 0) { g_err.clear(); return 0; }
     const int sec[4] = {sec0, sec1, sec2, sec3};
     return check(it::launch_attn_prep(q, qts, k, v, kts, q_norm, k_norm, eps, kc, vc, pos0, hd, nh, nkv, nt, n_rot,
                                       theta_scale, sec, round_mode, (hipStream_t)stream),
+                 who);
+}
+
+int it_attn_prep_f32kv(float* q, int qts, const float* k, const float* v, int kts, const float* q_norm,
+                       const float* k_norm, float eps, float* kc, float* vc, int kvd, int pos0, int row0, int hd,
+                       int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1, int sec2, int sec3,
+                       void* stream) {
+    const char* who = "it_attn_prep_f32kv";
+    if (validate_prep(who, q, qts, k, v, kts, q_norm, k_norm, eps, kc, vc, kvd, pos0, hd, nh, nkv, nt, n_rot,
+                      theta_scale, sec0, sec1, sec2, sec3))
+        return -1;
+    if (row0 < 0) return fail("%s: cache row %d invalid", who, row0);
+    if (nt == 0) { g_err.clear(); return 0; }
+    const int sec[4] = {sec0, sec1, sec2, sec3};
+    return check(it::launch_attn_prep_f32kv(q, qts, k, v, kts, q_norm, k_norm, eps, kc, vc, pos0, row0, hd, nh, nkv, nt,
+                                            n_rot, theta_scale, sec, (hipStream_t)stream),
+                 who);
+}
+
+size_t it_attn_f32kv_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv) {
+    (void)hd;
+    if (nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv) return 0;
+    return splitk_scratch(pos0, nt, nh, auto_chunk(pos0, nt, nh, nkv));
+}
+
+int it_attn_f32kv(const float* q, int qts, const float* kc, const float* vc, int kvd, int pos0, int hd, int nh,
+                  int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes,
+                  void* stream) {
+    const char* who = "it_attn_f32kv";
+    if (hd != HD) return fail("%s: head_dim %d unsupported (256)", who, hd);
+    if (nh <= 0 || nkv <= 0 || nh % nkv != 0 || nh / nkv > 16)
+        return fail("%s: n_head %d / n_head_kv %d invalid (at most 16 q heads per KV head)", who, nh, nkv);
+    if (kvd != nkv * hd) return fail("%s: kvd %d != n_head_kv*head_dim %d", who, kvd, nkv * hd);
+    if (nt <= 0 || pos0 < 0 || (long)pos0 + nt > (1L << 22)) return fail("%s: nt %d / pos0 %d invalid", who, nt, pos0);
+    if (!q || !kc || !vc || !out) return fail("%s: null buffer", who);
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out))
+        return fail("%s: q/kc/vc/out must be 16-byte aligned", who);
+    if (qts % 4 != 0 || ots % 4 != 0) return fail("%s: token strides must be multiples of 4", who);
+    if (nt > 1 && (qts < 2 * nh * hd || ots < nh * hd)) return fail("%s: token strides overlap rows", who);
+    const int chunk = auto_chunk(pos0, nt, nh, nkv);
+    const size_t need = splitk_scratch(pos0, nt, nh, chunk);
+    if (!scratch || scratch_bytes < need || !aligned16(scratch))
+        return fail("%s: scratch of %zu bytes needed (got %zu, 16-byte aligned)", who, need, scratch_bytes);
+    return check(it::launch_attn_f32kv(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, (float*)scratch, chunk,
+                                       (hipStream_t)stream),
                  who);
 }
 

@@ -11,6 +11,11 @@ hipError_t launch_kv_append(const float* k, const float* v, int sts, uint16_t* k
 hipError_t launch_attn_prep(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
                             const float* kw, float eps, uint16_t* kc, uint16_t* vc, int pos0, int hd, int nh, int nkv,
                             int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st);
+hipError_t launch_attn_prep_f32kv(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
+                                  const float* kw, float eps, float* kc, float* vc, int pos0, int row0, int hd, int nh,
+                                  int nkv, int nt, int n_rot, float tsc, const int* sec, hipStream_t st);
+hipError_t launch_attn_f32kv(const float* q, int qts, const float* kc, const float* vc, int kvd, int pos0, int nh,
+                             int nkv, int nt, float scale, float* out, int ots, float* part, int chunk, hipStream_t st);
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                                 int nh, int nkv, int nt, float scale, float* part, int chunk, hipStream_t st);
 hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,

@@ -46,13 +46,16 @@ __device__ __forceinline__ uint32_t pack_f16(float a, float b, int rtz) {
     return __builtin_bit_cast(uint32_t, x);
 }
 
-// One wave per head row, ceil((nh + 2 nkv) / 4) workgroups per token. Rows of token t: [0, nh) q heads, [nh, nh+nkv) k heads, then nkv v heads.
+// One wave per head row, ceil((nh + 2 nkv) / 4) workgroups per token. Token t is roped at position
+// pos0 + t and its K/V rows go to cache row row0 + t (row0 = pos0 for the model's f16 cache; the
+// MTP head's f32 cache keeps position p in slot p - 1, src/mtp.rs:120). KVT = uint16_t stores f16,
+// KVT = float stores the f32 values as they are. Rows of token t: [0, nh) q heads, [nh, nh+nkv) k heads, then nkv v heads.
 // Lane l holds elements E*l .. E*l+E-1 of the row (hd = 64*E).
-template <int E>
+template <int E, class KVT>
 __global__ __launch_bounds__(64 * PREP_WAVES) void attn_prep_kernel(
     float* __restrict__ q, int qts, const float* __restrict__ k, const float* __restrict__ v, int kts,
-    const float* __restrict__ qw, const float* __restrict__ kw, float eps, uint16_t* __restrict__ kc,
-    uint16_t* __restrict__ vc, int kvd, int pos0, int nh, int nkv, int n_rot, float tsc, int s0, int s1, int s2,
+    const float* __restrict__ qw, const float* __restrict__ kw, float eps, KVT* __restrict__ kc,
+    KVT* __restrict__ vc, int kvd, int pos0, int row0, int nh, int nkv, int n_rot, float tsc, int s0, int s1, int s2,
     int s3, int rtz) {
     typedef typename RowT<E>::T V;
     constexpr int HDK = 64 * E;
@@ -109,8 +112,10 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void attn_prep_kernel(
         *(V*)(q + (size_t)t * qts + (size_t)kh * 2 * HDK + E * l) = x;
         return;
     }
-    uint16_t* dst = (kind == 1 ? kc : vc) + (size_t)p * kvd + (size_t)kh * HDK + E * l;
-    if constexpr (E == 4) {
+    KVT* dst = (kind == 1 ? kc : vc) + (size_t)(row0 + t) * kvd + (size_t)kh * HDK + E * l;
+    if constexpr (sizeof(KVT) == 4) {
+        *(V*)dst = x;
+    } else if constexpr (E == 4) {
         uint32_t* d = (uint32_t*)dst;
         d[0] = pack_f16(x[0], x[1], rtz);
         d[1] = pack_f16(x[2], x[3], rtz);
@@ -119,19 +124,34 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void attn_prep_kernel(
     }
 }
 
-hipError_t launch_attn_prep(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
-                            const float* kw, float eps, uint16_t* kc, uint16_t* vc, int pos0, int hd, int nh, int nkv,
-                            int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st) {
+template <class KVT>
+static hipError_t launch_prep(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
+                              const float* kw, float eps, KVT* kc, KVT* vc, int pos0, int row0, int hd, int nh,
+                              int nkv, int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st) {
     const long groups = (nh + 2 * nkv + PREP_WAVES - 1) / PREP_WAVES;   // workgroups per token
     const dim3 grid((unsigned)(groups * nt)), block(64 * PREP_WAVES);
     const int kvd = nkv * hd;
     if (hd == 256)
-        attn_prep_kernel<4><<<grid, block, 0, st>>>(q, qts, k, v, kts, qw, kw, eps, kc, vc, kvd, pos0, nh, nkv, n_rot,
-                                                   tsc, sec[0], sec[1], sec[2], sec[3], rtz);
+        attn_prep_kernel<4, KVT><<<grid, block, 0, st>>>(q, qts, k, v, kts, qw, kw, eps, kc, vc, kvd, pos0, row0, nh,
+                                                        nkv, n_rot, tsc, sec[0], sec[1], sec[2], sec[3], rtz);
     else
-        attn_prep_kernel<2><<<grid, block, 0, st>>>(q, qts, k, v, kts, qw, kw, eps, kc, vc, kvd, pos0, nh, nkv, n_rot,
-                                                   tsc, sec[0], sec[1], sec[2], sec[3], rtz);
+        attn_prep_kernel<2, KVT><<<grid, block, 0, st>>>(q, qts, k, v, kts, qw, kw, eps, kc, vc, kvd, pos0, row0, nh,
+                                                        nkv, n_rot, tsc, sec[0], sec[1], sec[2], sec[3], rtz);
     return hipGetLastError();
+}
+
+hipError_t launch_attn_prep(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
+                            const float* kw, float eps, uint16_t* kc, uint16_t* vc, int pos0, int hd, int nh, int nkv,
+                            int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st) {
+    return launch_prep<uint16_t>(q, qts, k, v, kts, qw, kw, eps, kc, vc, pos0, pos0, hd, nh, nkv, nt, n_rot, tsc, sec,
+                                 rtz, st);
+}
+
+hipError_t launch_attn_prep_f32kv(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
+                                  const float* kw, float eps, float* kc, float* vc, int pos0, int row0, int hd, int nh,
+                                  int nkv, int nt, int n_rot, float tsc, const int* sec, hipStream_t st) {
+    return launch_prep<float>(q, qts, k, v, kts, qw, kw, eps, kc, vc, pos0, row0, hd, nh, nkv, nt, n_rot, tsc, sec, 0,
+                              st);
 }
 
 }  // namespace it

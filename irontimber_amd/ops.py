@@ -73,6 +73,54 @@ def attn_prep_f16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kc: torch.T
          round_mode, _stream())
 
 
+def attn_prep_f32kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int,
+                    row0: int, nh: int, nkv: int, q_norm: torch.Tensor | None = None,
+                    k_norm: torch.Tensor | None = None, eps: float = 1e-6, n_rot: int = 64,
+                    theta_scale: float | None = None, rope_base: float = 1e7, sections=(11, 11, 10, 0)) -> None:
+    """attn_prep_f16 for an f32 cache: rope at positions pos0.., K/V rows stored at cache rows row0..
+    (the MTP head stores position p in row p - 1)."""
+    _need(q, torch.float32, "q"); _need(k, torch.float32, "k"); _need(v, torch.float32, "v")
+    _need(kc, torch.float32, "kc"); _need(vc, torch.float32, "vc")
+    nt, kvd = k.shape
+    hd = kvd // nkv
+    if q.shape != (nt, nh * 2 * hd) or v.shape != k.shape:
+        raise ValueError("q must be [nt, nh*2*hd] and v the shape of k [nt, nkv*hd]")
+    for c in (kc, vc):
+        if c.shape[-1] != kvd or c.shape[0] < row0 + nt:
+            raise ValueError("kc/vc must be [rows >= row0 + nt, kvd] f32")
+    if theta_scale is None:
+        from .synth import rope_theta_scale
+        theta_scale = rope_theta_scale(rope_base, n_rot)
+    s = list(sections) + [0] * (4 - len(sections))
+    call("it_attn_prep_f32kv", q.data_ptr(), q.shape[1], k.data_ptr(), v.data_ptr(), kvd, _ptr(q_norm), _ptr(k_norm),
+         float(eps), kc.data_ptr(), vc.data_ptr(), kvd, pos0, row0, hd, nh, nkv, nt, n_rot, float(theta_scale), *s[:4],
+         _stream())
+
+
+def attn_f32kv(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int, nh: int, nkv: int,
+               scale: float | None = None, out: torch.Tensor | None = None,
+               scratch: torch.Tensor | None = None) -> torch.Tensor:
+    """q [nt, nh*2*hd] f32 (q | gate per head), kc/vc [rows, nkv*hd] f32 -> out [nt, nh*hd] f32;
+    query t sees rows 0..pos0+t."""
+    _need(q, torch.float32, "q"); _need(kc, torch.float32, "kc"); _need(vc, torch.float32, "vc")
+    nt = q.shape[0]
+    hd = q.shape[-1] // (2 * nh)
+    kvd = nkv * hd
+    for c in (kc, vc):
+        if c.shape[-1] != kvd or c.shape[0] < pos0 + nt:
+            raise ValueError("kc/vc must be [rows >= pos0 + nt, nkv*hd] f32")
+    if scale is None:
+        scale = 1.0 / hd ** 0.5
+    if out is None:
+        out = torch.empty(nt, nh * hd, device=q.device, dtype=torch.float32)
+    need = lib().it_attn_f32kv_scratch_bytes(pos0, nt, hd, nh, nkv)
+    if scratch is None:
+        scratch = torch.empty(max(need, 16), device=q.device, dtype=torch.uint8)
+    call("it_attn_f32kv", q.data_ptr(), nh * 2 * hd, kc.data_ptr(), vc.data_ptr(), kvd, pos0, hd, nh, nkv, nt,
+         float(scale), out.data_ptr(), nh * hd, scratch.data_ptr(), scratch.numel(), _stream())
+    return out
+
+
 def attn_scratch_bytes(pos0: int, nt: int, nh: int, nkv: int, hd: int = 256, kernel: int = KERNEL_AUTO,
                        chunk: int = 0) -> int:
     return lib().it_attn_scratch_bytes_ex(pos0, nt, hd, nh, nkv, kernel, chunk)

@@ -35,6 +35,7 @@ _SIG = {
     "it_ref_rope": (None, [_P, _i, _i, _i, _i, _f, _P]),
     "it_ref_attn_prep": (None, [_P, _i, _P, _i, _P, _P, _f, _P, _i, _i, _i, _i, _i, _i, _f, _P]),
     "it_ref_attn": (None, [_P, _i, _P, _P, _i, _i, _i, _i, _i, _i, _f, _P, _i, _i]),
+    "it_ref_attn_f32kv": (None, [_P, _i, _P, _P, _i, _i, _i, _i, _i, _i, _f, _P, _i, _i]),
     "it_ref_gdn_conv": (None, [_P, _i, _P, _P, _P, _i, _i, _i, _i]),
     "it_ref_gdn_step": (None, [_P, _i, _P, _P, _i, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i]),
     "it_ref_gdn_layer": (None, [_P, _i, _P, _P, _i, _P, _P, _i, _P, _P, _P, _P, _i, _P, _i, _i, _i, _i, _f, _i]),
@@ -79,6 +80,20 @@ def attn(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, pos0: int, nh: int, nkv:
         scale = 1.0 / np.sqrt(hd)
     lib().it_ref_attn(_p(q), q.shape[1], _p(kc), _p(vc), nkv * hd, pos0, hd, nh, nkv, nt, scale, _p(out), nh * hd,
                       threads or hardware_threads())
+    return out
+
+
+def attn_f32kv(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, pos0: int, nh: int, nkv: int, hd: int = 256,
+               scale: float | None = None, threads: int = 0) -> np.ndarray:
+    """src/mtp.rs:122-130 attention over an f32 cache. q [nt, nh*2*hd]; kc/vc [>=pos0+nt, nkv*hd] f32."""
+    q = np.ascontiguousarray(q, np.float32).reshape(q.shape[0], -1)
+    kc = np.ascontiguousarray(kc, np.float32); vc = np.ascontiguousarray(vc, np.float32)
+    nt = q.shape[0]
+    out = np.zeros((nt, nh * hd), np.float32)
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    lib().it_ref_attn_f32kv(_p(q), q.shape[1], _p(kc), _p(vc), nkv * hd, pos0, hd, nh, nkv, nt, scale, _p(out),
+                            nh * hd, threads or hardware_threads())
     return out
 
 

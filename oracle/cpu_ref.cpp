@@ -11,7 +11,7 @@
 // change the per-head summation order.
 //
 // Parity pins for every function are listed in the test files (tests/test_oracle_*.py):
-//   it_ref_attn       -- r012 f64 known-answer sweep (src/vk/r012_parity.rs:6-28), closed forms
+//   it_ref_attn, it_ref_attn_f32kv -- r012 f64 known-answer sweep (src/vk/r012_parity.rs:6-28), closed forms
 //                        (single key, equal scores), torch SDPA, split/chunk invariance.
 //   it_ref_gdn_*      -- brute-force float64 recurrence, closed forms (beta=0, g -> -inf),
 //                        conv over T tokens == T single-token calls.
@@ -172,9 +172,13 @@ void it_ref_l2norm(float* x, int n, float eps) {
 //   out  : f32 out[t*out_tok_stride + h*hd + j]
 // The reference keeps K/V as f32 holding f16-rounded values in Numerics::Ggml (cpu.rs:258); here
 // the cache is f16 and widened exactly, which is the same set of values.
-void it_ref_attn(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,
-                 int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
-                 int threads) {
+}  // extern "C"
+
+// The attention loop of cpu.rs:260-272 (and of the MTP head, src/mtp.rs:122-130), for either cache
+// element type: the loader widens one cache element to f32.
+template <class T, class Load>
+static void attn_rows(const float* q, int q_tok_stride, const T* kc, const T* vc, int kvd, int pos0, int hd, int nh,
+                      int nkv, int nt, float scale, float* out, int out_tok_stride, int threads, Load ld) {
     const int group = nh / nkv;
     par_for(nt * nh, threads, [&](int job) {
         const int t = job / nh, h = job % nh;
@@ -182,11 +186,11 @@ void it_ref_attn(const float* q, int q_tok_stride, const uint16_t* kc, const uin
         const int n = pos0 + t + 1;                                // cpu.rs:260
         const float* qh = q + (size_t)t * q_tok_stride + (size_t)h * 2 * hd;
         const float* gate = qh + hd;
-        std::vector<float> kp(hd), sc(n);
+        std::vector<float> sc(n);
         for (int p = 0; p < n; ++p) {                              // cpu.rs:267
-            const uint16_t* kr = kc + (size_t)p * kvd + (size_t)kh * hd;
+            const T* kr = kc + (size_t)p * kvd + (size_t)kh * hd;
             float s = 0.0f;
-            for (int i = 0; i < hd; ++i) s += qh[i] * h2f(kr[i]);
+            for (int i = 0; i < hd; ++i) s += qh[i] * ld(kr[i]);
             sc[p] = s * scale;
         }
         float mx = -INFINITY; for (int p = 0; p < n; ++p) mx = std::max(mx, sc[p]);   // cpu.rs:268
@@ -195,11 +199,29 @@ void it_ref_attn(const float* q, int q_tok_stride, const uint16_t* kc, const uin
         for (int j = 0; j < hd; ++j) oh[j] = 0.0f;
         for (int p = 0; p < n; ++p) {                              // cpu.rs:270
             const float w = sc[p] / sum;
-            const uint16_t* vr = vc + (size_t)p * kvd + (size_t)kh * hd;
-            for (int j = 0; j < hd; ++j) oh[j] += w * h2f(vr[j]);
+            const T* vr = vc + (size_t)p * kvd + (size_t)kh * hd;
+            for (int j = 0; j < hd; ++j) oh[j] += w * ld(vr[j]);
         }
         for (int j = 0; j < hd; ++j) oh[j] *= sigmoid(gate[j]);   // cpu.rs:272
     });
+}
+
+extern "C" {
+
+void it_ref_attn(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,
+                 int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
+                 int threads) {
+    attn_rows(q, q_tok_stride, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, out_tok_stride, threads,
+              [](uint16_t b) { return h2f(b); });
+}
+
+// The MTP head's attention over its f32 KV cache, src/mtp.rs:122-130: the same loop with f32 K/V.
+// Slot p of the head's cache holds position p + 1 (mtp.rs:120); the caller passes pos0 = the first
+// query's slot, so query t sees slots 0..pos0+t.
+void it_ref_attn_f32kv(const float* q, int q_tok_stride, const float* kc, const float* vc, int kvd, int pos0, int hd,
+                       int nh, int nkv, int nt, float scale, float* out, int out_tok_stride, int threads) {
+    attn_rows(q, q_tok_stride, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, out_tok_stride, threads,
+              [](float x) { return x; });
 }
 
 // Depthwise causal conv + SiLU with the rolling (K-1)-token state, oldest first, for nt tokens

@@ -100,3 +100,40 @@ def test_oracle_token_by_token_equals_block():
     for t in range(nt):
         one = oracle.attn(q[t].reshape(1, -1), kb, vb, pos0 + t, 16, 2)
         np.testing.assert_array_equal(one[0], block[t])
+
+
+@pytest.mark.parametrize("nh,nkv,hd", GEOMS)
+@pytest.mark.parametrize("pos0,nt", CASES)
+def test_oracle_f32kv_r012_known_answer(pos0, nt, nh, nkv, hd):
+    """The MTP head's f32-cache attention (src/mtp.rs:122-130) on the r012 closed-form arena with
+    the f32 K/V as they are (no f16 rounding), against the float64 softmax."""
+    q, k, v = arena(pos0, nt, nh, nkv, hd)
+    got = oracle.attn_f32kv(q, k, v, pos0, nh, nkv, hd, scale=1.0 / 16)
+    want = attn_f64(q, k.astype(np.float64), v.astype(np.float64), pos0, nh, nkv, hd, 1.0 / 16)
+    assert np.isfinite(got).all() and np.abs(got - want).max() < 2e-5
+
+
+def test_oracle_f32kv_closed_forms():
+    """Single key: output v * sigmoid(gate); zero query: the mean of V; and the f32 path equals the
+    f16 path on a cache whose values are exactly f16."""
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((1, 16 * 512)).astype(np.float32)
+    k = rng.standard_normal((1, 512)).astype(np.float32)
+    v = rng.standard_normal((1, 512)).astype(np.float32)
+    got = oracle.attn_f32kv(q, k, v, 0, 16, 2).reshape(16, 256)
+    gate = q.reshape(16, 512)[:, 256:].astype(np.float64)
+    want = np.stack([v.reshape(2, 256)[h // 8] / (1 + np.exp(-gate[h])) for h in range(16)])
+    np.testing.assert_allclose(got, want, rtol=2e-7, atol=1e-7)
+    q2 = q.copy().reshape(16, 512)
+    q2[:, :256] = 0.0
+    q2[:, 256:] = 40.0
+    k = rng.standard_normal((50, 512)).astype(np.float32)
+    v = rng.standard_normal((50, 512)).astype(np.float32)
+    got = oracle.attn_f32kv(q2.reshape(1, -1), k, v, 49, 16, 2).reshape(16, 256)
+    for h in range(16):
+        np.testing.assert_allclose(got[h], v.reshape(50, 2, 256).mean(0)[h // 8], atol=2e-6)
+    q3, kb, vb = attn_inputs(13, ctx=70, nt=3)
+    a = oracle.attn(q3.reshape(3, -1), kb, vb, 67, 16, 2)
+    b = oracle.attn_f32kv(q3.reshape(3, -1), f16_to_f64(kb).astype(np.float32), f16_to_f64(vb).astype(np.float32), 67,
+                          16, 2)
+    np.testing.assert_array_equal(a, b)
