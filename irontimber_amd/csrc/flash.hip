@@ -121,10 +121,16 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     {
         f4 qx[32];
         const int rw = rt * BM + 32 * w;
+        // row rr = token rr / G, q-head kh*G + rr % G: one division, then a walk over the 32 rows
+        // (a division per row costs ~40 instructions, ~10k cycles over the unrolled loop)
+        int tq = rw / G, gq = rw - tq * G;
+        const float* qlast = q + (size_t)((R - 1) / G) * qts + (size_t)(kh * G + (R - 1) % G) * 2 * HD + 4 * l;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            const int rr = min(rw + i, R - 1);   // rows past R: any valid row, zeroed below
-            qx[i] = ld_f4(q + (size_t)(rr / G) * qts + (size_t)(kh * G + rr % G) * 2 * HD + 4 * l);
+            // rows past R: any valid row (the last), zeroed below
+            const float* src = rw + i < R ? q + (size_t)tq * qts + (size_t)(kh * G + gq) * 2 * HD + 4 * l : qlast;
+            qx[i] = ld_f4(src);
+            if (++gq == G) { gq = 0; ++tq; }
         }
         tile_to_lds(kc, kvd, kb0, kend, cj, K0, w, l);
         tile_to_lds(vc, kvd, kb0, kend, cj, V0, w, l);
@@ -291,21 +297,23 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     if (hh == 0) { ml[w][0][c] = m_run; ml[w][1][c] = l_run; }
     const int rw = rt * BM + 32 * w;
     const int nrow = min(32, R - rw);
+    int tq = rw / G, gq = rw - tq * G;   // (token, q-head) of row rw + i, walked as in the prologue
     if (part) {
         // partial records of (token, head, split): m in natural-log units of the scaled score
 #pragma unroll 4
         for (int i = 0; i < nrow; ++i) {
-            const int rr = rw + i, tt = rr / G, hd = kh * G + rr % G;
-            float* rec = part + ((size_t)(tt * nh + hd) * smax + split) * 260;
+            float* rec = part + ((size_t)(tq * nh + kh * G + gq) * smax + split) * 260;
             if (l == 0) *(f4*)rec = f4{ml[w][0][i] * 0.6931471805599453f, ml[w][1][i], 0.f, 0.f};
             *(f4*)(rec + 4 + 4 * l) = *(const f4*)(os + i * HD + 4 * (l ^ i));
+            if (++gq == G) { gq = 0; ++tq; }
         }
         return;
     }
     // out = O / l * sigmoid(gate), gate rows read whole as well
 #pragma unroll 4
     for (int i = 0; i < nrow; ++i) {
-        const int rr = rw + i, tt = rr / G, hd = kh * G + rr % G;
+        const int tt = tq, hd = kh * G + gq;
+        if (++gq == G) { gq = 0; ++tq; }
         const f4 gt = ld_f4(q + (size_t)tt * qts + (size_t)hd * 2 * HD + HD + 4 * l);
         const f4 ov = *(const f4*)(os + i * HD + 4 * (l ^ i));
         const float inv = 1.0f / ml[w][1][i];
