@@ -21,8 +21,12 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__
                                                        int cd, int nt, int TT, float* __restrict__ ck, int ck_after) {
     const int ch = blockIdx.x * 256 + threadIdx.x;
     if (ch >= cd) return;
-    const int t0 = blockIdx.y * TT, t1 = min(nt, t0 + TT);
-    float wt[K], win[K - 1];
+    constexpr int TMAX = 16;   // tokens per run (the host passes TT <= TMAX)
+    const int t0 = blockIdx.y * TT, n = min(nt, t0 + TT) - t0;
+    // the run's inputs are all loaded before any is used: one memory round trip per run
+    float xs[TMAX], wt[K], win[K - 1];
+#pragma unroll
+    for (int j = 0; j < TMAX; ++j) xs[j] = x[(size_t)(t0 + min(j, n - 1)) * xts + ch];
 #pragma unroll
     for (int i = 0; i < K; ++i) wt[i] = w[(size_t)ch * K + i];
 #pragma unroll
@@ -30,8 +34,11 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__
         const int tt = t0 - (K - 1) + i;
         win[i] = tt >= 0 ? x[(size_t)tt * xts + ch] : state[(size_t)(tt + K - 1) * cd + ch];
     }
-    for (int t = t0; t < t1; ++t) {
-        const float xv = x[(size_t)t * xts + ch];
+#pragma unroll
+    for (int j = 0; j < TMAX; ++j) {
+        if (j >= n) continue;
+        const int t = t0 + j;
+        const float xv = xs[j];
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < K - 1; ++i) s += win[i] * wt[i];
@@ -79,12 +86,22 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restric
                                                           const float* __restrict__ w, float* __restrict__ state,
                                                           float* __restrict__ out, int ots, int cd, int nt, int TT,
                                                           int nnorm, float eps, float* __restrict__ ck, int ck_after) {
+    constexpr int TMAX = 16;   // tokens per run (the host passes TT <= TMAX)
     const int hb = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
     if (hb >= cd / 128) return;   // whole waves
     const bool norm = hb < nnorm;
-    const int t0 = blockIdx.y * TT, t1 = min(nt, t0 + TT);
+    const int t0 = blockIdx.y * TT, n = min(nt, t0 + TT) - t0;
     int ch[2] = {128 * hb + l, 128 * hb + 64 + l};
-    float wt[2][K], win[2][K - 1];
+    // Every input of the run is loaded before any is used (one memory round trip per run instead
+    // of one per token): the run's tokens (clamped to the last one), the K-1 inputs before it and
+    // the weights.
+    float xs[2][TMAX], wt[2][K], win[2][K - 1];
+#pragma unroll
+    for (int j = 0; j < TMAX; ++j) {
+        const size_t row = (size_t)(t0 + min(j, n - 1)) * xts;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) xs[c][j] = x[row + ch[c]];
+    }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -95,15 +112,16 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restric
             win[c][i] = tt >= 0 ? x[(size_t)tt * xts + ch[c]] : state[(size_t)(tt + K - 1) * cd + ch[c]];
         }
     }
-    for (int t = t0; t < t1; ++t) {
-        float y[2], xv[2];
+#pragma unroll
+    for (int j = 0; j < TMAX; ++j) {
+        if (j >= n) continue;   // wave-uniform; keeps the loop fully unrollable
+        float y[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            xv[c] = x[(size_t)t * xts + ch[c]];
             float s = 0.f;
 #pragma unroll
             for (int i = 0; i < K - 1; ++i) s += win[c][i] * wt[c][i];
-            s += xv[c] * wt[c][K - 1];
+            s += xs[c][j] * wt[c][K - 1];
             y[c] = siluf_(s);
         }
         if (norm) {
@@ -113,12 +131,12 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restric
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            out[(size_t)t * ots + ch[c]] = y[c];
+            out[(size_t)(t0 + j) * ots + ch[c]] = y[c];
 #pragma unroll
             for (int i = 0; i + 1 < K - 1; ++i) win[c][i] = win[c][i + 1];
-            win[c][K - 2] = xv[c];
+            win[c][K - 2] = xs[c][j];
         }
-        if (ck && t == ck_after && gridDim.y == 1) {
+        if (ck && t0 + j == ck_after && gridDim.y == 1) {
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
