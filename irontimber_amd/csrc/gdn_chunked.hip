@@ -61,8 +61,9 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
     __shared__ __align__(16) float Ap[C][C + 4];
     __shared__ float sG[C], sB[C];
     __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
-    __shared__ __align__(16) _Float16 Rs[2][16][XS];         // right-hand side of the current block
-    static_assert(KP == XS, "solve rows reuse the Q tile");
+    __shared__ __align__(16) _Float16 Rs[2][2][16][XS];      // right-hand sides of the current block (W, U)
+    __shared__ __align__(16) _Float16 XU[2][C][XS];          // solve rows of U, hi / lo
+    static_assert(KP == XS, "solve rows of W reuse the Q tile");
     _Float16(*Xs)[C][XS] = QX;
 
     const int c = blockIdx.x, h = blockIdx.y, nch = gridDim.x;
@@ -70,16 +71,30 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
     const int kh = h % nk, qk = nk * SD;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
     char* rec = scr + ((size_t)h * nch + c) * REC;
+    const int col = 16 * w + li;                 // this lane's column of the solve (W and U)
 
-    // ---- q/k rows (zero past the prompt) as hi/lo, beta and the cumulative log-decay
+    // V rows (f32, 512 B each) straight into the U solve buffer, idle until the solve: direct
+    // global->LDS loads, two rows per instruction, 4 per wave, nothing held in registers. Rows past
+    // the prompt repeat the last row and are zeroed through beta = 0.
+    float* const Vs = (float*)&XU[0][0][0];   // [C][SD] f32 (32 KB of the 36 KB buffer)
+    {
+        typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 8 * w + 2 * i + (l >> 5);
+            const float* src = co + (size_t)(t0 + min(r, L - 1)) * cts + 2 * qk + h * SD + 4 * (l & 31);
+            __builtin_amdgcn_global_load_lds(src, (lds_void*)(Vs + (8 * w + 2 * i) * SD), 16, 0, 0);
+        }
+    }
+
+    // ---- q/k rows (zero past the prompt) as hi/lo, beta and the cumulative log-decay; the loads
+    // are unconditional (clamped row, then masked) so no branch separates them from their use
     for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
         const int t = idx >> 4, d8 = 8 * (idx & 15);
-        f4 k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0, q0 = k0, q1 = k0;
-        if (t < L) {
-            const float* row = co + (size_t)(t0 + t) * cts;
-            q0 = ld_f4(row + kh * SD + d8); q1 = ld_f4(row + kh * SD + d8 + 4);
-            k0 = ld_f4(row + qk + kh * SD + d8); k1 = ld_f4(row + qk + kh * SD + d8 + 4);
-        }
+        const float* row = co + (size_t)(t0 + min(t, L - 1)) * cts;
+        const float m = t < L ? 1.f : 0.f;
+        const f4 q0 = ld_f4(row + kh * SD + d8) * m, q1 = ld_f4(row + kh * SD + d8 + 4) * m;
+        const f4 k0 = ld_f4(row + qk + kh * SD + d8) * m, k1 = ld_f4(row + qk + kh * SD + d8 + 4) * m;
         h8 hi, lo;
         split_hi_lo(k0, k1, hi, lo);
         *(h8*)&Kx[0][t][d8] = hi; *(h8*)&Kx[1][t][d8] = lo;
@@ -180,62 +195,73 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
 #pragma unroll
         for (int r = 0; r < 16; ++r) Td[kb][r][ci] = y[r];
     }
-    const int col = 16 * w + li;                 // this lane's column within the half
-    for (int hf = 0; hf < 2; ++hf) {
-        // right-hand sides of this lane's 16 (row, column) cells, V straight from global
-        float rhs[4][4];
+    // W and U are solved together: wave w owns column tile w of both (two independent chains per
+    // block row, one barrier pair per block row for the pair)
+    float rhs[2][4][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = 16 * i + 4 * g + e;
-                float b;
-                if (hf == 0) b = expf(sG[t]) * ((float)Kx[0][t][col] + (float)Kx[1][t][col]);
-                else b = t < L ? co[(size_t)(t0 + t) * cts + 2 * qk + h * SD + col] : 0.f;
-                rhs[i][e] = sB[t] * b;
-            }
-        for (int idx = tid; idx < 2 * C * XS / 8; idx += PREP_THREADS) ((u4*)&Xs[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
-        __syncthreads();
+        for (int e = 0; e < 4; ++e) {
+            const int t = 16 * i + 4 * g + e;
+            rhs[0][i][e] = sB[t] * (expf(sG[t]) * ((float)Kx[0][t][col] + (float)Kx[1][t][col]));
+            rhs[1][i][e] = sB[t] * Vs[t * SD + col];
+        }
+    __syncthreads();   // every wave has read its V cells: the U buffer can be cleared
+    for (int idx = tid; idx < 2 * C * XS / 8; idx += PREP_THREADS) {
+        ((u4*)&Xs[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
+        ((u4*)&XU[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    const int c0 = 16 * w;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // R = beta B_i - sum_{k<i} A'_ik X_k for this wave's 16-column tile
-            f4 acc;
+    for (int i = 0; i < 4; ++i) {
+        // R = beta B_i - sum_{k<i} A'_ik X_k for this wave's 16-column tile of W and of U
+        f4 acc[2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = rhs[i][e];
+        for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-            for (int ks = 0; ks < (i + 1) / 2; ++ks) {
-                // A operand: -A'[16i + li][32ks + 8g + j], zero at and past column 16i
-                const int s0 = 32 * ks + 8 * g;
-                const float* arow = &Ap[16 * i + li][s0];
-                const f4 a0 = s0 < 16 * i ? -*(const f4*)arow : f4{0.f, 0.f, 0.f, 0.f};
-                const f4 a1 = s0 + 4 < 16 * i ? -*(const f4*)(arow + 4) : f4{0.f, 0.f, 0.f, 0.f};
-                h8 ah, al;
-                split_hi_lo(a0, a1, ah, al);
-                const int c0 = 16 * w;
-                const _Float16* xh = &Xs[0][s0 + (li >> 2)][c0 + 4 * (li & 3)];
-                const _Float16* xl = &Xs[1][s0 + (li >> 2)][c0 + 4 * (li & 3)];
+            for (int e = 0; e < 4; ++e) acc[hf][e] = rhs[hf][i][e];
+#pragma unroll
+        for (int ks = 0; ks < (i + 1) / 2; ++ks) {
+            // A operand: -A'[16i + li][32ks + 8g + j], zero at and past column 16i
+            const int s0 = 32 * ks + 8 * g;
+            const float* arow = &Ap[16 * i + li][s0];
+            const f4 a0 = s0 < 16 * i ? -*(const f4*)arow : f4{0.f, 0.f, 0.f, 0.f};
+            const f4 a1 = s0 + 4 < 16 * i ? -*(const f4*)(arow + 4) : f4{0.f, 0.f, 0.f, 0.f};
+            h8 ah, al;
+            split_hi_lo(a0, a1, ah, al);
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                _Float16(*X)[C][XS] = hf ? XU : Xs;
+                const _Float16* xh = &X[0][s0 + (li >> 2)][c0 + 4 * (li & 3)];
+                const _Float16* xl = &X[1][s0 + (li >> 2)][c0 + 4 * (li & 3)];
                 const h8 bh = cat_h4(lds_tr4(xh), lds_tr4(xh + 4 * XS));
                 const h8 bl = cat_h4(lds_tr4(xl), lds_tr4(xl + 4 * XS));
-                acc = mfma16x16x32(ah, bh, acc);
-                acc = mfma16x16x32(ah, bl, acc);
-                acc = mfma16x16x32(al, bh, acc);
+                acc[hf] = mfma16x16x32(ah, bh, acc[hf]);
+                acc[hf] = mfma16x16x32(ah, bl, acc[hf]);
+                acc[hf] = mfma16x16x32(al, bh, acc[hf]);
             }
-            // R -> LDS (hi/lo) so it can be the B operand of T_i R
+        }
+        // R -> LDS (hi/lo) so it can be the B operand of T_i R
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float v = acc[e];
+                const float v = acc[hf][e];
                 const _Float16 hi = (_Float16)v;
-                Rs[0][4 * g + e][col] = hi;
-                Rs[1][4 * g + e][col] = (_Float16)(v - (float)hi);
+                Rs[hf][0][4 * g + e][col] = hi;
+                Rs[hf][1][4 * g + e][col] = (_Float16)(v - (float)hi);
             }
-            __syncthreads();
-            // X_i = T_i R: K = 16 (k-groups 2 and 3 are zero padding)
-            h8 th = {}, tl = {};
-            if (g < 2) split_hi_lo(*(const f4*)&Td[i][li][8 * g], *(const f4*)&Td[i][li][8 * g + 4], th, tl);
-            // transpose reads run with the whole wave active; k-groups 2 and 3 reread rows 0..7
-            const int gr = g & 1, c0 = 16 * w;
-            const _Float16* rh = &Rs[0][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
-            const _Float16* rl = &Rs[1][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
+        __syncthreads();
+        // X_i = T_i R: K = 16 (k-groups 2 and 3 are zero padding)
+        h8 th = {}, tl = {};
+        if (g < 2) split_hi_lo(*(const f4*)&Td[i][li][8 * g], *(const f4*)&Td[i][li][8 * g + 4], th, tl);
+        // transpose reads run with the whole wave active; k-groups 2 and 3 reread rows 0..7
+        const int gr = g & 1;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const _Float16* rh = &Rs[hf][0][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
+            const _Float16* rl = &Rs[hf][1][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
             h8 bh = cat_h4(lds_tr4(rh), lds_tr4(rh + 4 * XS));
             h8 bl = cat_h4(lds_tr4(rl), lds_tr4(rl + 4 * XS));
             if (g >= 2) { bh = h8{}; bl = h8{}; }
@@ -244,18 +270,19 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
             z = mfma16x16x32(th, bl, z);
             z = mfma16x16x32(tl, bh, z);
             // X_i -> scratch (W f16 / U f32) and -> LDS (hi/lo) for the later block rows
+            _Float16(*X)[C][XS] = hf ? XU : Xs;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = 16 * i + 4 * g + e;
                 const float v = z[e];
                 const _Float16 hi = (_Float16)v;
-                Xs[0][t][col] = hi;
-                Xs[1][t][col] = (_Float16)(v - (float)hi);
+                X[0][t][col] = hi;
+                X[1][t][col] = (_Float16)(v - (float)hi);
                 if (hf == 0) ((_Float16*)(rec + OFF_W))[t * SD + col] = hi;
                 else ((float*)(rec + OFF_U))[t * SD + col] = v;
             }
-            __syncthreads();
         }
+        __syncthreads();
     }
 }
 
