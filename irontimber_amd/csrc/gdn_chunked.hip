@@ -46,60 +46,48 @@ size_t gdn_chunked_scratch_bytes(int nt, int nv, int S) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// 8 waves. LDS: K and Q rows as f16 hi/lo pairs (split once), A', the diagonal-block inverses,
-// and the solve buffers, which reuse the Q rows' space once Q K^T and e^G q are out.
+// 8 waves, 69 KB of LDS (two workgroups per CU, so one's loads overlap the other's products): the
+// K rows as f16 hi/lo pairs, A', the diagonal-block inverses and the current block's right-hand
+// side; the solve rows X reuse the K tile once K is dead. Q never enters LDS: the Q K^T operands
+// and e^G q are read from global (the chunk's q rows stay in L2).
 constexpr int PREP_THREADS = 512;
-constexpr int KP = SD + 16;    // f16 row pitch of the K/Q tiles (288 B, 32-byte multiple)
+constexpr int KP = SD + 16;    // f16 row pitch of the K tile (288 B, 32-byte multiple)
 
-__global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __restrict__ co, int cts,
+__global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void gdn_chunk_prep(const float* __restrict__ co, int cts,
                                                                const float* __restrict__ br, const float* __restrict__ ar,
                                                                int bts, const float* __restrict__ dt,
                                                                const float* __restrict__ A, int nt, int nk,
                                                                char* __restrict__ scr) {
-    __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows, hi / lo
-    __shared__ __align__(16) _Float16 QX[2][C][KP];          // Q rows hi / lo, then the solve rows X
+    __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows hi / lo, then the solve rows X
     __shared__ __align__(16) float Ap[C][C + 4];
     __shared__ float sG[C], sB[C];
     __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
-    __shared__ __align__(16) _Float16 Rs[2][2][16][XS];      // right-hand sides of the current block (W, U)
-    __shared__ __align__(16) _Float16 XU[2][C][XS];          // solve rows of U, hi / lo
-    static_assert(KP == XS, "solve rows of W reuse the Q tile");
-    _Float16(*Xs)[C][XS] = QX;
+    __shared__ __align__(16) _Float16 Rs[2][16][XS];         // right-hand side of the current block
+    static_assert(KP == XS, "solve rows reuse the K tile");
+    _Float16(*Xs)[C][XS] = Kx;
 
     const int c = blockIdx.x, h = blockIdx.y, nch = gridDim.x;
     const int t0 = c * C, L = min(C, nt - t0);
     const int kh = h % nk, qk = nk * SD;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
     char* rec = scr + ((size_t)h * nch + c) * REC;
-    const int col = 16 * w + li;                 // this lane's column of the solve (W and U)
+    const int col = 16 * w + li;                 // this lane's column of the solve
 
-    // V rows (f32, 512 B each) straight into the U solve buffer, idle until the solve: direct
-    // global->LDS loads, two rows per instruction, 4 per wave, nothing held in registers. Rows past
-    // the prompt repeat the last row and are zeroed through beta = 0.
-    float* const Vs = (float*)&XU[0][0][0];   // [C][SD] f32 (32 KB of the 36 KB buffer)
-    {
-        typedef __attribute__((address_space(3))) void lds_void;
+    // q row of this lane in the Q K^T and e^G q products (global; rows past the prompt masked)
+    auto qrow = [&](int t) { return co + (size_t)(t0 + min(t, L - 1)) * cts + kh * SD; };
+
+    // ---- K rows (zero past the prompt) as hi/lo, beta and the cumulative log-decay; unconditional
+    // loads (clamped row, then masked) so no branch separates them from their use
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 8 * w + 2 * i + (l >> 5);
-            const float* src = co + (size_t)(t0 + min(r, L - 1)) * cts + 2 * qk + h * SD + 4 * (l & 31);
-            __builtin_amdgcn_global_load_lds(src, (lds_void*)(Vs + (8 * w + 2 * i) * SD), 16, 0, 0);
-        }
-    }
-
-    // ---- q/k rows (zero past the prompt) as hi/lo, beta and the cumulative log-decay; the loads
-    // are unconditional (clamped row, then masked) so no branch separates them from their use
-    for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
+    for (int it = 0; it < C * SD / 8 / PREP_THREADS; ++it) {
+        const int idx = tid + it * PREP_THREADS;
         const int t = idx >> 4, d8 = 8 * (idx & 15);
-        const float* row = co + (size_t)(t0 + min(t, L - 1)) * cts;
+        const float* row = co + (size_t)(t0 + min(t, L - 1)) * cts + qk + kh * SD + d8;
         const float m = t < L ? 1.f : 0.f;
-        const f4 q0 = ld_f4(row + kh * SD + d8) * m, q1 = ld_f4(row + kh * SD + d8 + 4) * m;
-        const f4 k0 = ld_f4(row + qk + kh * SD + d8) * m, k1 = ld_f4(row + qk + kh * SD + d8 + 4) * m;
+        const f4 k0 = ld_f4(row) * m, k1 = ld_f4(row + 4) * m;
         h8 hi, lo;
         split_hi_lo(k0, k1, hi, lo);
         *(h8*)&Kx[0][t][d8] = hi; *(h8*)&Kx[1][t][d8] = lo;
-        split_hi_lo(q0, q1, hi, lo);
-        *(h8*)&QX[0][t][d8] = hi; *(h8*)&QX[1][t][d8] = lo;
     }
     if (w == 0) {
         float gg = 0.f, b = 0.f;
@@ -117,18 +105,27 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
     }
     __syncthreads();
 
-    // ---- lower 16x16 tiles of K K^T (tiles 0..9) and Q K^T (tiles 10..19), hi+lo products
+    // ---- lower 16x16 tiles of K K^T (tiles 0..9) and Q K^T (tiles 10..19), hi+lo products; the
+    // Q operand comes from global and is split in registers
     for (int tile = w; tile < 20; tile += PREP_THREADS / 64) {
         const bool isq = tile >= 10;
         const int tt = isq ? tile - 10 : tile;
         const int mt = tt >= 6 ? 3 : tt >= 3 ? 2 : tt >= 1 ? 1 : 0;
         const int nt_ = tt - mt * (mt + 1) / 2;
-        const _Float16(*Ar)[C][KP] = isq ? QX : Kx;
+        const int ta = 16 * mt + li;              // A-operand row (a q row for Q K^T tiles)
+        const float* qr = qrow(ta);
+        const float qm = ta < L ? 1.f : 0.f;
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int d = 32 * ks + 8 * g;
-            const h8 ah = ld_h8(&Ar[0][16 * mt + li][d]), al = ld_h8(&Ar[1][16 * mt + li][d]);
+            h8 ah, al;
+            if (isq) {   // wave-uniform
+                split_hi_lo(ld_f4(qr + d) * qm, ld_f4(qr + d + 4) * qm, ah, al);
+            } else {
+                ah = ld_h8(&Kx[0][ta][d]);
+                al = ld_h8(&Kx[1][ta][d]);
+            }
             const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
             acc = mfma16x16x32(ah, bh, acc);
             acc = mfma16x16x32(ah, bl, acc);
@@ -151,19 +148,19 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
             if ((s8 >> 4) > (t >> 4)) aqk[idx] = u4{0u, 0u, 0u, 0u};
         }
     }
-    // ---- e^G q (token-major) and e^{G_last - G} k (dim-major), 8 halves per store
+    // ---- e^G q (token-major, from global) and e^{G_last - G} k (dim-major), 8 halves per store
     {
         u4* QG = (u4*)(rec + OFF_QG);
         u4* KT = (u4*)(rec + OFF_KT);
         const float glast = sG[C - 1];
-        for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
-            const int t = idx >> 4, d8 = 8 * (idx & 15);
-            const float e = expf(sG[t]);
-            const h8 hi = ld_h8(&QX[0][t][d8]), lo = ld_h8(&QX[1][t][d8]);
-            h8 r;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) r[j] = (_Float16)(e * ((float)hi[j] + (float)lo[j]));
-            QG[idx] = __builtin_bit_cast(u4, r);
+        for (int it = 0; it < C * SD / 8 / PREP_THREADS; ++it) {
+            const int idx = tid + it * PREP_THREADS;
+            const int t = idx >> 4, d8 = 8 * (idx & 15);
+            const float* qr = qrow(t) + d8;
+            const float e = t < L ? expf(sG[t]) : 0.f;
+            const f4 q0 = ld_f4(qr) * e, q1 = ld_f4(qr + 4) * e;
+            QG[idx] = __builtin_bit_cast(u4, to_h8(q0, q1));
         }
         for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
             const int d = idx >> 3, t8 = 8 * (idx & 7);
@@ -177,7 +174,7 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
         }
         if (tid == 0) *(float*)(rec + OFF_GC) = expf(glast);
     }
-    __syncthreads();   // Q tile dead from here on: its LDS becomes the solve rows
+    __syncthreads();   // A' complete
     // ---- (I + A') [W | U] = diag(beta) [e^G K | V], blocked by 16 rows:
     //   T_i = (I + A'_ii)^-1 (16x16, one wave, forward substitution per column)
     //   X_i = T_i (diag(beta) B_i - sum_{k<i} A'_ik X_k)          (MFMA, hi+lo products)
@@ -195,8 +192,16 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
 #pragma unroll
         for (int r = 0; r < 16; ++r) Td[kb][r][ci] = y[r];
     }
-    // W and U are solved together: wave w owns column tile w of both (two independent chains per
-    // block row, one barrier pair per block row for the pair)
+    // V rows, coalesced (thread: row tid >> 3, 16 columns); they reach their solve lanes through
+    // LDS once the K tile is dead. Rows past the prompt repeat the last row and are zeroed through
+    // beta = 0. (The other workgroup on the CU covers their latency.)
+    f4 vreg[4];
+    {
+        const float* src = co + (size_t)(t0 + min(tid >> 3, L - 1)) * cts + 2 * qk + h * SD + 16 * (tid & 7);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vreg[j] = ld_f4(src + 4 * j);
+    }
+    // right-hand sides of this lane's 16 (row, column) cells: W from the K tile, U from V
     float rhs[2][4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -204,64 +209,63 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
         for (int e = 0; e < 4; ++e) {
             const int t = 16 * i + 4 * g + e;
             rhs[0][i][e] = sB[t] * (expf(sG[t]) * ((float)Kx[0][t][col] + (float)Kx[1][t][col]));
+        }
+    __syncthreads();   // the K tile is dead: V passes through it to its solve lanes
+    float* const Vs = (float*)&Xs[0][0][0];   // [C][SD] f32, 32 KB of the 36 KB tile
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *(f4*)(Vs + (tid >> 3) * SD + 16 * (tid & 7) + 4 * j) = vreg[j];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = 16 * i + 4 * g + e;
             rhs[1][i][e] = sB[t] * Vs[t * SD + col];
         }
-    __syncthreads();   // every wave has read its V cells: the U buffer can be cleared
-    for (int idx = tid; idx < 2 * C * XS / 8; idx += PREP_THREADS) {
-        ((u4*)&Xs[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
-        ((u4*)&XU[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
-    }
-    __syncthreads();
-    const int c0 = 16 * w;
+    for (int hf = 0; hf < 2; ++hf) {
+        __syncthreads();   // every wave is done with the tile (V, or the previous half's X)
+        for (int idx = tid; idx < 2 * C * XS / 8; idx += PREP_THREADS) ((u4*)&Xs[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
+        __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // R = beta B_i - sum_{k<i} A'_ik X_k for this wave's 16-column tile of W and of U
-        f4 acc[2];
+        for (int i = 0; i < 4; ++i) {
+            // R = beta B_i - sum_{k<i} A'_ik X_k for this wave's 16-column tile
+            f4 acc;
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+            for (int e = 0; e < 4; ++e) acc[e] = rhs[hf][i][e];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[hf][e] = rhs[hf][i][e];
-#pragma unroll
-        for (int ks = 0; ks < (i + 1) / 2; ++ks) {
-            // A operand: -A'[16i + li][32ks + 8g + j], zero at and past column 16i
-            const int s0 = 32 * ks + 8 * g;
-            const float* arow = &Ap[16 * i + li][s0];
-            const f4 a0 = s0 < 16 * i ? -*(const f4*)arow : f4{0.f, 0.f, 0.f, 0.f};
-            const f4 a1 = s0 + 4 < 16 * i ? -*(const f4*)(arow + 4) : f4{0.f, 0.f, 0.f, 0.f};
-            h8 ah, al;
-            split_hi_lo(a0, a1, ah, al);
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                _Float16(*X)[C][XS] = hf ? XU : Xs;
-                const _Float16* xh = &X[0][s0 + (li >> 2)][c0 + 4 * (li & 3)];
-                const _Float16* xl = &X[1][s0 + (li >> 2)][c0 + 4 * (li & 3)];
+            for (int ks = 0; ks < (i + 1) / 2; ++ks) {
+                // A operand: -A'[16i + li][32ks + 8g + j], zero at and past column 16i
+                const int s0 = 32 * ks + 8 * g;
+                const float* arow = &Ap[16 * i + li][s0];
+                const f4 a0 = s0 < 16 * i ? -*(const f4*)arow : f4{0.f, 0.f, 0.f, 0.f};
+                const f4 a1 = s0 + 4 < 16 * i ? -*(const f4*)(arow + 4) : f4{0.f, 0.f, 0.f, 0.f};
+                h8 ah, al;
+                split_hi_lo(a0, a1, ah, al);
+                const int c0 = 16 * w;
+                const _Float16* xh = &Xs[0][s0 + (li >> 2)][c0 + 4 * (li & 3)];
+                const _Float16* xl = &Xs[1][s0 + (li >> 2)][c0 + 4 * (li & 3)];
                 const h8 bh = cat_h4(lds_tr4(xh), lds_tr4(xh + 4 * XS));
                 const h8 bl = cat_h4(lds_tr4(xl), lds_tr4(xl + 4 * XS));
-                acc[hf] = mfma16x16x32(ah, bh, acc[hf]);
-                acc[hf] = mfma16x16x32(ah, bl, acc[hf]);
-                acc[hf] = mfma16x16x32(al, bh, acc[hf]);
+                acc = mfma16x16x32(ah, bh, acc);
+                acc = mfma16x16x32(ah, bl, acc);
+                acc = mfma16x16x32(al, bh, acc);
             }
-        }
-        // R -> LDS (hi/lo) so it can be the B operand of T_i R
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+            // R -> LDS (hi/lo) so it can be the B operand of T_i R
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float v = acc[hf][e];
+                const float v = acc[e];
                 const _Float16 hi = (_Float16)v;
-                Rs[hf][0][4 * g + e][col] = hi;
-                Rs[hf][1][4 * g + e][col] = (_Float16)(v - (float)hi);
+                Rs[0][4 * g + e][col] = hi;
+                Rs[1][4 * g + e][col] = (_Float16)(v - (float)hi);
             }
-        __syncthreads();
-        // X_i = T_i R: K = 16 (k-groups 2 and 3 are zero padding)
-        h8 th = {}, tl = {};
-        if (g < 2) split_hi_lo(*(const f4*)&Td[i][li][8 * g], *(const f4*)&Td[i][li][8 * g + 4], th, tl);
-        // transpose reads run with the whole wave active; k-groups 2 and 3 reread rows 0..7
-        const int gr = g & 1;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const _Float16* rh = &Rs[hf][0][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
-            const _Float16* rl = &Rs[hf][1][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
+            __syncthreads();
+            // X_i = T_i R: K = 16 (k-groups 2 and 3 are zero padding)
+            h8 th = {}, tl = {};
+            if (g < 2) split_hi_lo(*(const f4*)&Td[i][li][8 * g], *(const f4*)&Td[i][li][8 * g + 4], th, tl);
+            // transpose reads run with the whole wave active; k-groups 2 and 3 reread rows 0..7
+            const int gr = g & 1, c0 = 16 * w;
+            const _Float16* rh = &Rs[0][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
+            const _Float16* rl = &Rs[1][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
             h8 bh = cat_h4(lds_tr4(rh), lds_tr4(rh + 4 * XS));
             h8 bl = cat_h4(lds_tr4(rl), lds_tr4(rl + 4 * XS));
             if (g >= 2) { bh = h8{}; bl = h8{}; }
@@ -270,19 +274,18 @@ __global__ __launch_bounds__(PREP_THREADS) void gdn_chunk_prep(const float* __re
             z = mfma16x16x32(th, bl, z);
             z = mfma16x16x32(tl, bh, z);
             // X_i -> scratch (W f16 / U f32) and -> LDS (hi/lo) for the later block rows
-            _Float16(*X)[C][XS] = hf ? XU : Xs;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = 16 * i + 4 * g + e;
                 const float v = z[e];
                 const _Float16 hi = (_Float16)v;
-                X[0][t][col] = hi;
-                X[1][t][col] = (_Float16)(v - (float)hi);
+                Xs[0][t][col] = hi;
+                Xs[1][t][col] = (_Float16)(v - (float)hi);
                 if (hf == 0) ((_Float16*)(rec + OFF_W))[t * SD + col] = hi;
                 else ((float*)(rec + OFF_U))[t * SD + col] = v;
             }
+            __syncthreads();
         }
-        __syncthreads();
     }
 }
 
