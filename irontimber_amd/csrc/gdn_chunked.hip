@@ -31,7 +31,7 @@ constexpr size_t OFF_QG = OFF_W + C * SD * 2;       // f16 [C][SD]   e^{G_t} q_t
 constexpr size_t OFF_KT = OFF_QG + C * SD * 2;      // f16 [SD][C]   e^{G_last - G_t} k_t, transposed
 constexpr size_t OFF_AQK = OFF_KT + SD * C * 2;     // f16 [C][C]    lower_incl(D * Q K^T)
 constexpr size_t OFF_U = OFF_AQK + C * C * 2;       // f32 [C][SD]   U
-constexpr size_t OFF_GC = OFF_U + C * SD * 4;       // f32           e^{G_last}
+constexpr size_t OFF_GC = OFF_U + C * SD * 4;       // f32 [4]       e^{G_last} (4 copies)
 constexpr size_t REC = (OFF_GC + 16 + 255) / 256 * 256;
 // f16 LDS row stride of the solve buffers; transpose reads need every 4-lane 32-byte segment
 // 32-byte aligned, so the row pitch (288 B) is a multiple of 32 bytes
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             }
             KT[idx] = __builtin_bit_cast(u4, r);
         }
-        if (tid == 0) *(float*)(rec + OFF_GC) = expf(glast);
+        if (tid < 4) ((float*)(rec + OFF_GC))[tid] = expf(glast);   // 4 copies: read per lane
     }
     __syncthreads();   // A' complete
     // ---- (I + A') [W | U] = diag(beta) [e^G K | V], blocked by 16 rows:
@@ -294,60 +294,73 @@ constexpr int CW = 16;         // state columns per scan workgroup
 constexpr int NCB = SD / CW;   // column blocks of the state per head
 constexpr int NI = CW / 16;    // 16-column MFMA tiles per workgroup
 
-// One chunk's operands for one column block, staged in LDS by the direct global->LDS path (no
-// registers hold data in flight, so the next chunk streams in during this one's products). Rows
+// Workgroup barrier for LDS data written by the waves themselves (ds_write): waits for this wave's
+// LDS operations only, not for the next chunk's operand loads, which are in flight by design.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One chunk's operands for one column block, staged in LDS by the direct global->LDS path. Rows
 // are XOR-swizzled by 16-byte chunk so the operand reads of 16 consecutive rows hit distinct banks:
 // 256-byte rows (W, e^G Q) by row & 15, 128-byte rows (K^T, Q K^T) by (row >> 1) & 7 (two rows
-// share a 256-byte bank window). U holds only this block's CW columns.
+// share a 256-byte bank window). U holds only this block's CW columns; GC the 4 copies of
+// e^{G_last} (lane l of its 4-byte load reads copy l & 3).
 struct ScanStage {
     _Float16 W[C * SD];      // [token][dim]
     _Float16 QG[C * SD];     // [token][dim]
     _Float16 KT[SD * C];     // [dim][token]
     _Float16 AQK[C * C];     // [token][token]
     float U[C * CW];         // [token][column]
+    float GC[64];
 };
 __device__ __forceinline__ int swz256(int r) { return r & 15; }
-// Workgroup barrier for LDS data written by the waves themselves (ds_write): waits for this wave's
-// LDS operations only. __syncthreads would also wait for the next chunk's loads into LDS, which
-// are still in flight by design (its release fence covers every outstanding LDS write).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ int swz128(int r) { return (r >> 1) & 7; }
 
-// Issue the loads of chunk record `rec` into stage B: instructions of 64 lanes x 16 bytes, per wave
-// W 4, e^G Q 4, K^T 4, Q K^T 2 and U CW/16; lane l lands at byte 16*l of its instruction's 1 KB.
-__device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, ScanStage& B, int n0, int w, int l) {
-    typedef __attribute__((address_space(3))) void lds_void;
+// Issue loads of chunk record `rec` into stage B as the share `part` (0 or 1) of two loader waves:
+// instructions of 64 lanes x 16 bytes, per wave W 8, e^G Q 8, K^T 8, Q K^T 4, U CW/8 (+1 for GC on
+// part 0); lane l lands at byte 16*l of its instruction's 1 KB.
+__device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, ScanStage& B, int n0, int part, int l) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {   // W and e^G Q: 4 rows of 256 B per instruction
-        const int i = 4 * w + k, r = 4 * i + (l >> 4), j = (l & 15) ^ swz256(r);
+    for (int k = 0; k < 8; ++k) {   // W and e^G Q: 4 rows of 256 B per instruction
+        const int i = 8 * part + k, r = 4 * i + (l >> 4), j = (l & 15) ^ swz256(r);
         __builtin_amdgcn_global_load_lds(rec + OFF_W + r * SD * 2 + 16 * j, (lds_void*)(B.W + 4 * i * SD), 16, 0, 0);
         __builtin_amdgcn_global_load_lds(rec + OFF_QG + r * SD * 2 + 16 * j, (lds_void*)(B.QG + 4 * i * SD), 16, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {   // K^T: 8 rows of 128 B per instruction
-        const int i = 4 * w + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
+    for (int k = 0; k < 8; ++k) {   // K^T: 8 rows of 128 B per instruction
+        const int i = 8 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
         __builtin_amdgcn_global_load_lds(rec + OFF_KT + r * C * 2 + 16 * j, (lds_void*)(B.KT + 8 * i * C), 16, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {   // Q K^T: 8 rows of 128 B
-        const int i = 2 * w + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
+    for (int k = 0; k < 4; ++k) {   // Q K^T: 8 rows of 128 B
+        const int i = 4 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
         __builtin_amdgcn_global_load_lds(rec + OFF_AQK + r * C * 2 + 16 * j, (lds_void*)(B.AQK + 8 * i * C), 16, 0, 0);
     }
     constexpr int UL = CW / 4;       // 16-byte lanes per U row (CW floats)
 #pragma unroll
-    for (int k = 0; k < CW / 16; ++k) {   // this block's U columns: 64/UL rows per instruction
-        const int i = (CW / 16) * w + k, r = (64 / UL) * i + l / UL;
+    for (int k = 0; k < CW / 8; ++k) {   // this block's U columns: 64/UL rows per instruction
+        const int i = (CW / 8) * part + k, r = (64 / UL) * i + l / UL;
         __builtin_amdgcn_global_load_lds(rec + OFF_U + (r * SD + n0) * 4 + 16 * (l % UL), (lds_void*)(B.U + (64 / UL) * i * CW), 16, 0, 0);
     }
+    if (part == 0) __builtin_amdgcn_global_load_lds(rec + OFF_GC + 4 * (l & 3), (lds_void*)B.GC, 4, 0, 0);
 }
 
-__global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ scr, int nch, float* __restrict__ state,
+// Scan workgroup: 8 compute waves + 2 loader waves. The dependency chain per chunk is
+// V' = U - W S0 and S1 = e^{G_last} S0 + K~^T V'; the output O = e^G Q S0 + Aqk V' hangs off it.
+// Waves 0-3 ("chain") run the chain for chunk c while waves 4-7 ("output") compute O of chunk c-1
+// from the previous chunk's S0 and V' (both double buffered in LDS). Waves 8-9 ("loaders") stage
+// chunk c+1's operands into the other LDS stage and touch chunk c+3's record lines so that the
+// staging hits L2; only they ever wait for global loads, so no compute wave stalls on load issue.
+constexpr int SCAN_THREADS = 640;
+
+__global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __restrict__ scr, int nch, float* __restrict__ state,
                                                       float* __restrict__ out, int ots, int nt, int nv) {
     constexpr int SP = SD + 8, VP = C + 8;
     __shared__ __align__(16) ScanStage B0;
     __shared__ __align__(16) ScanStage B1;
-    __shared__ __align__(16) _Float16 S0T[2][CW][SP];   // [hi|lo][state column][key dim]
-    __shared__ __align__(16) _Float16 VpT[2][CW][VP];   // [hi|lo][state column][token]
+    __shared__ __align__(16) _Float16 S0T[2][2][CW][SP];   // [chunk & 1][hi|lo][state column][key dim]
+    __shared__ __align__(16) _Float16 VpT[2][2][CW][VP];   // [chunk & 1][hi|lo][state column][token]
+    __shared__ uint32_t PfSink[64];                         // landing words of the L2 touches, never read
 
     // XCD-aware placement: workgroups are dealt to the 8 XCDs round-robin by linear id, so id L
     // runs on XCD L % 8. All column blocks of one head go to the same XCD (head = xcd + 8*(slot/NCB))
@@ -355,143 +368,174 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(const char* __restrict__ s
     const int L_id = blockIdx.x, xcd = L_id & 7, slot = L_id >> 3;
     const int h = xcd + 8 * (slot / NCB), cb = slot % NCB;
     if (h >= nv) return;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
+    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
     const int n0 = CW * cb;
-    float* sh = state + (size_t)h * SD * SD;
-    const float rs = 1.0f / sqrtf((float)SD);
     const char* hrec = scr + (size_t)h * nch * REC;
 
-    scan_stage_loads(hrec, B0, n0, w, l);
-    float gc_next = *(const float*)(hrec + OFF_GC);
-
-    // state slice in accumulator layout: st[mi][ni][i] = S[16(2w+mi) + 4g + i][n0 + 16ni + li]
-    f4 st[2][NI];
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) st[mi][ni][i] = sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li];
-
-    // one chunk of the scan: its operands sit in stage B (landed), the next chunk's go into Bn
-    auto step = [&](int c, const ScanStage& B, ScanStage& Bn) {
-        IT_SCAN_WAIT_VMCNT(0);
-        __syncthreads();            // stage B complete for every wave; Bn, S0T and VpT free
-        const float gc = gc_next;
-        if (c + 1 < nch) {
-            scan_stage_loads(hrec + (size_t)(c + 1) * REC, Bn, n0, w, l);
-            gc_next = *(const float*)(hrec + (size_t)(c + 1) * REC + OFF_GC);
+    // Barrier schedule: step c (0 <= c <= nch) holds barriers A_c and B_c. The chain writes S0T[c&1]
+    // before A_c, reads stage c&1 and writes VpT[c&1] between A_c and B_c, reads stage c&1 again
+    // after B_c. The output waves read S0T/VpT[(c-1)&1] and stage c&1 between A_c and B_c. The
+    // loaders fill stage (c+1)&1 after A_c and have it landed before A_{c+1}. Step nch only
+    // finishes the last chunk's output.
+    if (wv >= 8) {
+        const int part = wv - 8;
+        constexpr int LINES = (int)(REC / 128);
+        // this block's share of the 128-byte lines of chunk cc's record: 64 lines per loader wave
+        auto touch = [&](int cc) {
+            const int line = min((2 * cb + part) * 64 + l, LINES - 1);
+            __builtin_amdgcn_global_load_lds(hrec + (size_t)min(cc, nch - 1) * REC + 128 * line, (lds_void*)PfSink, 4, 0, 0);
+        };
+        scan_stage_loads(hrec, B0, n0, part, l);
+        touch(1);
+        touch(2);
+        IT_SCAN_WAIT_VMCNT(2);
+        for (int c = 0; c <= nch; ++c) {
+            lds_barrier();   // A_c
+            if (c + 1 < nch) scan_stage_loads(hrec + (size_t)(c + 1) * REC, (c & 1) ? B0 : B1, n0, part, l);
+            touch(c + 3);
+            lds_barrier();   // B_c
+            IT_SCAN_WAIT_VMCNT(1);   // stage (c+1)&1 landed; the newest touch may still be in flight
         }
-        const int t0 = c * C, L = min(C, nt - t0);
-
-        // ---- S0 -> LDS as hi/lo, transposed to [column][key dim]
+        return;
+    }
+    const int w = wv & 3;
+    if (wv < 4) {
+        float* sh = state + (size_t)h * SD * SD;
+        // state slice in accumulator layout: st[mi][ni][i] = S[16(2w+mi) + 4g + i][n0 + 16ni + li]
+        f4 st[2][NI];
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
             for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float v = st[mi][ni][i];
-                    const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
-                    const int col = 16 * ni + li, dk = 16 * (2 * w + mi) + 4 * g + i;
-                    S0T[0][col][dk] = hi;
-                    S0T[1][col][dk] = lo;
-                }
-        lds_barrier();
-        // ---- V' = U - W S0 for tokens 16w..16w+15 (W row 16w+li, dims 32ks+8g..)
+                for (int i = 0; i < 4; ++i) st[mi][ni][i] = sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li];
         const int rw = 16 * w + li;
-        f4 vp[NI];
+        for (int c = 0; c < nch; ++c) {
+            const int b = c & 1;
+            const ScanStage& B = b ? B1 : B0;
+            // ---- S0 -> LDS as hi/lo, transposed to [column][key dim]
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni) vp[ni] = f4{0.f, 0.f, 0.f, 0.f};
+            for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const h8 a = ld_h8(B.W + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
+                for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni) {
-                vp[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
-                vp[ni] = mfma16x16x32(a, ld_h8(&S0T[1][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
+                    for (int i = 0; i < 4; ++i) {
+                        const float v = st[mi][ni][i];
+                        const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+                        const int col = 16 * ni + li, dk = 16 * (2 * w + mi) + 4 * g + i;
+                        S0T[b][0][col][dk] = hi;
+                        S0T[b][1][col][dk] = lo;
+                    }
+            lds_barrier();   // A_c
+            // ---- V' = U - W S0 for tokens 16w..16w+15 (W row 16w+li, dims 32ks+8g..)
+            f4 vp[NI];
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni) vp[ni] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const h8 a = ld_h8(B.W + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni) {
+                    vp[ni] = mfma16x16x32(a, ld_h8(&S0T[b][0][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
+                    vp[ni] = mfma16x16x32(a, ld_h8(&S0T[b][1][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
+                }
             }
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * w + 4 * g + i, col = 16 * ni + li;
+                    const float v = B.U[t * CW + col] - vp[ni][i];
+                    const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+                    VpT[b][0][col][t] = hi;
+                    VpT[b][1][col][t] = lo;
+                }
+            lds_barrier();   // B_c
+            // ---- S1 = e^{G_last} S0 + Ktilde^T V' (K^T rows 16(2w+mi)+li, tokens 32ks+8g..)
+            const float gc = B.GC[0];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni) st[mi][ni] *= gc;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi) {
+                    const int rk = 16 * (2 * w + mi) + li;
+                    const h8 a = ld_h8(B.KT + rk * C + 8 * ((4 * ks + g) ^ swz128(rk)));
+#pragma unroll
+                    for (int ni = 0; ni < NI; ++ni) {
+                        st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[b][0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
+                        st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[b][1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
+                    }
+                }
         }
+        lds_barrier();   // A_nch
+        lds_barrier();   // B_nch
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni)
+        for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * w + 4 * g + i, col = 16 * ni + li;
-                const float v = B.U[t * CW + col] - vp[ni][i];
-                const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
-                VpT[0][col][t] = hi;
-                VpT[1][col][t] = lo;
-            }
-        lds_barrier();
-        // ---- O = (e^G Q S0 + Aqk V') / sqrt(128) for tokens 16w..16w+15
+            for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li] = st[mi][ni][i];
+        return;
+    }
+    // ---- output waves: O of chunk c-1 in step c, for tokens 16w..16w+15; the A operands of chunk
+    // c (e^G Q and Q K^T rows) are copied from stage c&1 into registers in step c, used in step c+1
+    const float rs = 1.0f / sqrtf((float)SD);
+    const int rw = 16 * w + li;
+    h8 qg[4], aqk[2];
+    for (int c = 0; c <= nch; ++c) {
+        lds_barrier();   // A_c
+        const int b = c & 1, pb = b ^ 1;
         f4 oa[NI];
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) oa[ni] = f4{0.f, 0.f, 0.f, 0.f};
+        if (c > 0) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const h8 a = ld_h8(B.QG + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni) {
-                oa[ni] = mfma16x16x32(a, ld_h8(&S0T[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-                oa[ni] = mfma16x16x32(a, ld_h8(&S0T[1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-            }
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const h8 a = ld_h8(B.AQK + rw * C + 8 * ((4 * ks + g) ^ swz128(rw)));
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni) {
-                oa[ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-                oa[ni] = mfma16x16x32(a, ld_h8(&VpT[1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-            }
-        }
-        // (stores guarded per token only in a partial last chunk: per-lane conditions split the
-        // code into small blocks)
-        float* orow = out + (size_t)t0 * ots + (size_t)h * SD + n0 + li;
-        if (L == C) {
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) orow[(size_t)(16 * w + 4 * g + i) * ots + 16 * ni] = oa[ni][i] * rs;
-        } else {
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = 16 * w + 4 * g + i;
-                    if (t < L) orow[(size_t)t * ots + 16 * ni] = oa[ni][i] * rs;
-                }
-        }
-        // ---- S1 = e^{G_last} S0 + Ktilde^T V' (K^T rows 16(2w+mi)+li, tokens 32ks+8g..)
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni) st[mi][ni] *= gc;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-                const int rk = 16 * (2 * w + mi) + li;
-                const h8 a = ld_h8(B.KT + rk * C + 8 * ((4 * ks + g) ^ swz128(rk)));
+            for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni) {
-                    st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
-                    st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
+                    oa[ni] = mfma16x16x32(qg[ks], ld_h8(&S0T[pb][0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+                    oa[ni] = mfma16x16x32(qg[ks], ld_h8(&S0T[pb][1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
                 }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni) {
+                    oa[ni] = mfma16x16x32(aqk[ks], ld_h8(&VpT[pb][0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+                    oa[ni] = mfma16x16x32(aqk[ks], ld_h8(&VpT[pb][1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+                }
+        }
+        if (c < nch) {
+            const ScanStage& B = b ? B1 : B0;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qg[ks] = ld_h8(B.QG + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) aqk[ks] = ld_h8(B.AQK + rw * C + 8 * ((4 * ks + g) ^ swz128(rw)));
+        }
+        lds_barrier();   // B_c
+        if (c > 0) {
+            // (stores guarded per token only in a partial last chunk: per-lane conditions split
+            // the code into small blocks)
+            const int t0 = (c - 1) * C, L = min(C, nt - t0);
+            float* orow = out + (size_t)t0 * ots + (size_t)h * SD + n0 + li;
+            if (L == C) {
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) orow[(size_t)(16 * w + 4 * g + i) * ots + 16 * ni] = oa[ni][i] * rs;
+            } else {
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int t = 16 * w + 4 * g + i;
+                        if (t < L) orow[(size_t)t * ots + 16 * ni] = oa[ni][i] * rs;
+                    }
             }
-    };
-    // two stages as distinct objects, so the compiler can tell the loads streaming into one never
-    // alias the reads of the other (no conservative waits); loop unrolled by two
-    for (int c = 0; c < nch; c += 2) {
-        step(c, B0, B1);
-        if (c + 1 < nch) step(c + 1, B1, B0);
+        }
     }
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li] = st[mi][ni][i];
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -503,7 +547,7 @@ hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const f
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // linear grid of 8 * NCB * ceil(nv / 8) workgroups, mapped to (head, column block) in-kernel
-    gdn_chunk_scan<<<dim3(8 * NCB * ((nv + 7) / 8)), 256, 0, st>>>((const char*)scratch, nch, state, out, ots, nt, nv);
+    gdn_chunk_scan<<<dim3(8 * NCB * ((nv + 7) / 8)), SCAN_THREADS, 0, st>>>((const char*)scratch, nch, state, out, ots, nt, nv);
     return hipGetLastError();
 }
 
