@@ -316,42 +316,42 @@ struct ScanStage {
 __device__ __forceinline__ int swz256(int r) { return r & 15; }
 __device__ __forceinline__ int swz128(int r) { return (r >> 1) & 7; }
 
-// Issue loads of chunk record `rec` into stage B as the share `part` (0 or 1) of two loader waves:
-// instructions of 64 lanes x 16 bytes, per wave W 8, e^G Q 8, K^T 8, Q K^T 4, U CW/8 (+1 for GC on
-// part 0); lane l lands at byte 16*l of its instruction's 1 KB.
+// Issue loads of chunk record `rec` into stage B as the share `part` (0-3) of the loader waves:
+// instructions of 64 lanes x 16 bytes, per wave W 4, e^G Q 4, K^T 4, Q K^T 2, U CW/16 (+1 for GC
+// on part 0); lane l lands at byte 16*l of its instruction's 1 KB.
 __device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, ScanStage& B, int n0, int part, int l) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {   // W and e^G Q: 4 rows of 256 B per instruction
-        const int i = 8 * part + k, r = 4 * i + (l >> 4), j = (l & 15) ^ swz256(r);
+    for (int k = 0; k < 4; ++k) {   // W and e^G Q: 4 rows of 256 B per instruction
+        const int i = 4 * part + k, r = 4 * i + (l >> 4), j = (l & 15) ^ swz256(r);
         __builtin_amdgcn_global_load_lds(rec + OFF_W + r * SD * 2 + 16 * j, (lds_void*)(B.W + 4 * i * SD), 16, 0, 0);
         __builtin_amdgcn_global_load_lds(rec + OFF_QG + r * SD * 2 + 16 * j, (lds_void*)(B.QG + 4 * i * SD), 16, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {   // K^T: 8 rows of 128 B per instruction
-        const int i = 8 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
+    for (int k = 0; k < 4; ++k) {   // K^T: 8 rows of 128 B per instruction
+        const int i = 4 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
         __builtin_amdgcn_global_load_lds(rec + OFF_KT + r * C * 2 + 16 * j, (lds_void*)(B.KT + 8 * i * C), 16, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {   // Q K^T: 8 rows of 128 B
-        const int i = 4 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
+    for (int k = 0; k < 2; ++k) {   // Q K^T: 8 rows of 128 B
+        const int i = 2 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
         __builtin_amdgcn_global_load_lds(rec + OFF_AQK + r * C * 2 + 16 * j, (lds_void*)(B.AQK + 8 * i * C), 16, 0, 0);
     }
     constexpr int UL = CW / 4;       // 16-byte lanes per U row (CW floats)
 #pragma unroll
-    for (int k = 0; k < CW / 8; ++k) {   // this block's U columns: 64/UL rows per instruction
-        const int i = (CW / 8) * part + k, r = (64 / UL) * i + l / UL;
+    for (int k = 0; k < CW / 16; ++k) {   // this block's U columns: 64/UL rows per instruction
+        const int i = (CW / 16) * part + k, r = (64 / UL) * i + l / UL;
         __builtin_amdgcn_global_load_lds(rec + OFF_U + (r * SD + n0) * 4 + 16 * (l % UL), (lds_void*)(B.U + (64 / UL) * i * CW), 16, 0, 0);
     }
     if (part == 0) __builtin_amdgcn_global_load_lds(rec + OFF_GC + 4 * (l & 3), (lds_void*)B.GC, 4, 0, 0);
 }
 
-// Scan workgroup: 8 compute waves + 2 loader waves. The dependency chain per chunk is
+// Scan workgroup: 8 compute waves + 4 loader waves. The dependency chain per chunk is
 // V' = U - W S0 and S1 = e^{G_last} S0 + K~^T V'; the output O = e^G Q S0 + Aqk V' hangs off it.
 // Waves 0-3 ("chain") run the chain for chunk c while waves 4-7 ("output") compute O of chunk c-1
-// from the previous chunk's S0 and V' (both double buffered in LDS). Waves 8-9 ("loaders") stage
+// from the previous chunk's S0 and V' (both double buffered in LDS). Waves 8-11 ("loaders") stage
 // chunk c+1's operands into the other LDS stage and touch chunk c+3's record lines so that the
 // staging hits L2; only they ever wait for global loads, so no compute wave stalls on load issue.
-constexpr int SCAN_THREADS = 640;
+constexpr int SCAN_THREADS = 768;
 
 __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __restrict__ scr, int nch, float* __restrict__ state,
                                                       float* __restrict__ out, int ots, int nt, int nv) {
@@ -380,9 +380,9 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
     if (wv >= 8) {
         const int part = wv - 8;
         constexpr int LINES = (int)(REC / 128);
-        // this block's share of the 128-byte lines of chunk cc's record: 64 lines per loader wave
+        // this block's share of the 128-byte lines of chunk cc's record: 32 lines per loader wave
         auto touch = [&](int cc) {
-            const int line = min((2 * cb + part) * 64 + l, LINES - 1);
+            const int line = min(cb * 128 + part * 32 + (l & 31), LINES - 1);
             __builtin_amdgcn_global_load_lds(hrec + (size_t)min(cc, nch - 1) * REC + 128 * line, (lds_void*)PfSink, 4, 0, 0);
         };
         scan_stage_loads(hrec, B0, n0, part, l);
