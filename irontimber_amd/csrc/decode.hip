@@ -372,6 +372,97 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     }
 }
 
+// Merge without barriers: one wave per (token, head, 16-dim block). Lane l takes splits l, l + 64,
+// ... (SPL of them, loads clamped to the last valid split and masked), merges them in registers,
+// then the 64 lanes are reduced by a halving butterfly: the swap across lane halves (and across
+// 16-lane rows) hands each lane of a pair the half of the other's values it keeps, so 16 dims
+// need 8 + 4 + 2 + 1 + 2 exchanges instead of 16 full reductions. Lane l ends holding dim
+// 8*b5 + 4*b4 + 2*b3 + b2 (bits of l) summed over all lanes.
+__device__ __forceinline__ void swap32(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap16(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+template <int SPL>
+__global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __restrict__ q, int qts, int pos0,
+                                                                int nh, int nt, const float* __restrict__ part,
+                                                                int chunk, int smax, float* __restrict__ out,
+                                                                int ots) {
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    const int th = wid >> 4, d0 = 16 * (wid & 15);
+    if (th >= nt * nh) return;   // whole wave
+    const int t = th / nh, h = th - t * nh;
+    const int ns = (pos0 + t + chunk) / chunk;   // splits that hold keys <= pos0 + t
+    const float* base = part + (size_t)th * smax * PART;
+    f2 hv[SPL];
+    f4 ov[SPL][4];
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        const float* rec = base + (size_t)min(l + 64 * j, ns - 1) * PART;
+        hv[j] = *(const f2*)rec;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ov[j][k] = ld_f4(rec + 4 + d0 + 4 * k);
+    }
+    const float gv = q[(size_t)t * qts + (size_t)h * 2 * HD + HD + d0 + 8 * (l >> 5) + 4 * ((l >> 4) & 1) +
+                       2 * ((l >> 3) & 1) + ((l >> 2) & 1)];
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        if (l + 64 * j >= ns) hv[j][0] = -INFINITY;
+        M = fmaxf(M, hv[j][0]);
+    }
+    M = wave_max(M);   // finite: split 0 always holds key 0
+    float den = 0.f, o[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        const float wgt = hv[j][0] == -INFINITY ? 0.f : __expf(hv[j][0] - M);
+        den += hv[j][1] * wgt;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[4 * k + e] += ov[j][k][e] * wgt;
+    }
+    den = wave_sum(den);
+    // lanes 0-31 keep dims 0-7, lanes 32-63 dims 8-15
+    float r8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float a = o[i], b = o[8 + i];
+        swap32(a, b);
+        r8[i] = a + b;
+    }
+    // within each half: rows 0 and 2 keep the lower 4, rows 1 and 3 the upper 4
+    float r4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float a = r8[i], b = r8[4 + i];
+        swap16(a, b);
+        r4[i] = a + b;
+    }
+    const bool b3 = (l >> 3) & 1, b2 = (l >> 2) & 1;
+    float r2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float keep = b3 ? r4[2 + i] : r4[i], give = b3 ? r4[i] : r4[2 + i];
+        r2[i] = keep + __shfl_xor(give, 8);
+    }
+    float v;
+    {
+        const float keep = b2 ? r2[1] : r2[0], give = b2 ? r2[0] : r2[1];
+        v = keep + __shfl_xor(give, 4);
+    }
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 1);
+    if ((l & 3) == 0) {
+        const int d = d0 + 8 * (l >> 5) + 4 * ((l >> 4) & 1) + 2 * ((l >> 3) & 1) + ((l >> 2) & 1);
+        out[(size_t)t * ots + (size_t)h * HD + d] = v / den * sigmoidf_(gv);
+    }
+}
+
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
                                        int pos0, int nh, int nkv, int nt, float scale, float* part, int chunk,
                                        hipStream_t st) {
@@ -391,8 +482,19 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
 hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                float* out, int ots, hipStream_t st) {
     const int smax = (pos0 + nt + chunk - 1) / chunk;
-    if (smax <= 32)
+    const unsigned wgs = (unsigned)(((long)nt * nh * 16 + 3) / 4);   // 4 waves each
+    // the wave merge for the few rows of decode and verify; the workgroup merge (fewer, longer
+    // waves) for the many rows of a prefill chunk
+    if ((long)nt * nh > 256 && smax <= 32)
         attn_combine_kernel<4><<<dim3(1, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
+    else if ((long)nt * nh > 256)
+        attn_combine_kernel<16><<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
+    else if (smax <= 64)
+        attn_combine_wave_kernel<1><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+    else if (smax <= 128)
+        attn_combine_wave_kernel<2><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+    else if (smax <= 256)
+        attn_combine_wave_kernel<4><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
     else
         attn_combine_kernel<16><<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
     return hipGetLastError();
