@@ -86,7 +86,7 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
     __shared__ __align__(16) _Float16 V1[TK * HD];
     __shared__ __align__(16) _Float16 Qs[2][ROWS][QST];   // [hi|lo][row][dim]
     __shared__ __align__(16) _Float16 Ps[NB][16][PST];    // rows 0-7 P_hi, 8-15 P_lo of a row block
-    __shared__ float Mx[4][ROWS];                          // per-wave tile maxima, then per-wave sums
+    __shared__ float Mx[4][ROWS];                          // per-wave tile maxima
     __shared__ float Al[ROWS];                             // per-row rescale of the tile
 
     const int G = nh / nkv, R = nt * G, r0 = rg * ROWS;
@@ -125,19 +125,23 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
 
     // per-lane row facts for the S^T columns: lane column c is row 8b + (c & 7) of block b
     int lim[NB];
-    float m_run[NB], l_run[NB];
+    float m_run[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int rr = r0 + 8 * b + (c & 7);
         lim[b] = rr < R ? pos0 + rr / G + 1 : 0;
         m_run[b] = -INFINITY;
-        l_run[b] = 0.f;
     }
-    f4 acc[NB][4];
+    f4 acc[NB][4], lacc[NB];   // O over this wave's 64 dims, and P times a ones column (row sums)
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NB; ++b) {
+        lacc[b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int n = 0; n < 4; ++n) acc[b][n] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    h8 ones;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
 
     // transpose-read source offsets (halves) of this lane inside a V tile, for key rows
     // 32ks + 8g + 4e' + (c >> 2) and the 16-dim column block of output tile n of wave w
@@ -198,15 +202,9 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
             const float mnew = fmaxf(m_run[b], mt);
             const float a = (mnew == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run[b] - mnew);
             const float msub = (mnew == -INFINITY) ? 0.0f : mnew;
-            float p[4], sum = 0.f;
+            float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                p[i] = __builtin_amdgcn_exp2f(x[b][i] - msub);
-                sum += p[i];
-            }
-            sum += __shfl_xor(sum, 16);
-            sum += __shfl_xor(sum, 32);
-            l_run[b] = l_run[b] * a + sum;
+            for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(x[b][i] - msub);
             m_run[b] = mnew;
             h4 ph;
 #pragma unroll
@@ -234,10 +232,12 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
                 const float a = Al[8 * b + ((4 * g + i) & 7)];
 #pragma unroll
                 for (int n = 0; n < 4; ++n) acc[b][n][i] *= a;
+                lacc[b][i] *= a;
             }
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const h8 pa = ld_h8(&Ps[b][c][32 * ks + 8 * g]);
+                lacc[b] = mfma16x16x32(pa, ones, lacc[b]);
 #pragma unroll
                 for (int n = 0; n < 4; ++n) {
                     const h8 vb = cat_h4(lds_tr4(Vt + 32 * ks * HD + voff[0][n]), lds_tr4(Vt + 32 * ks * HD + voff[1][n]));
@@ -247,42 +247,32 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
         }
     }
 
-    // ---- records {m (natural log units), l, 0, 0, o[256]}: sums of the per-wave running sums;
-    // the P_hi and P_lo halves of O added across the two lane halves and staged in LDS (the V
-    // buffers are free once every wave is past the last tile), then written as whole 1 KB rows,
-    // one 16-byte store per lane
+    // ---- records {m (natural log units), l, 0, 0, o[256]} straight from registers: adding lanes l
+    // and l ^ 32 sums the P_hi and P_lo halves, after which lane (c, g < 2) holds rows 4g..4g+3 of
+    // each block at dims 64w + 16n + c (16 lanes store 64 contiguous bytes of a row), and the ones
+    // product gives every wave the full row sums. Wave 0 adds the headers.
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
-        if (g == 0 && c < 8) Mx[w][8 * b + c] = l_run[b];
-    float* Os = (float*)V0;   // [ROWS][256]
-    static_assert(ROWS * HD * 4 <= TK * HD * 2, "O fits in a V buffer");
-    __syncthreads();
+    for (int b = 0; b < NB; ++b) {
+        if (r0 + 8 * b >= R) continue;   // wave-uniform
+        // (token, q-head) of row r0 + 8b + 4g, then walked over i (one division per block)
+        const int rb = r0 + 8 * b + 4 * (g & 1);
+        int tq = rb / G, gq = rb - tq * G;
+        float mh[4];
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+        for (int i = 0; i < 4; ++i) mh[i] = __shfl(m_run[b], (4 * g + i) & 7);   // lane row = c & 7
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
+        for (int i = 0; i < 4; ++i) {
+            float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float v = sum_xor32(acc[b][n][i]);
-                if (l < 32) Os[(8 * b + 4 * g + i) * HD + 64 * w + 16 * n + c] = v;
+            for (int n = 0; n < 4; ++n) v[n] = sum_xor32(acc[b][n][i]);
+            const float ls = sum_xor32(lacc[b][i]);
+            if (l < 32 && rb + i < R) {
+                float* rec = part + ((size_t)(tq * nh + kh * G + gq) * smax + s) * PART;
+#pragma unroll
+                for (int n = 0; n < 4; ++n) rec[4 + 64 * w + 16 * n + c] = v[n];
+                if (w == 0 && c == 0) *(f4*)rec = f4{mh[i] * LN2_F, ls, 0.f, 0.f};
             }
-    __syncthreads();
-    for (int row = w; row < ROWS; row += 4) {
-        const int rr = r0 + row;
-        if (rr >= R) break;
-        float* rec = part + ((size_t)((rr / G) * nh + kh * G + rr % G) * smax + s) * PART;
-        *(f4*)(rec + 4 + 4 * l) = *(const f4*)(Os + row * HD + 4 * l);
-    }
-    if (w == 0 && l < ROWS) {
-        const int rr = r0 + l;
-        float mrow = m_run[0];
-#pragma unroll
-        for (int b = 1; b < NB; ++b)
-            if ((l >> 3) == b) mrow = m_run[b];
-        if (rr < R) {
-            const float lsum = (Mx[0][l] + Mx[1][l]) + (Mx[2][l] + Mx[3][l]);
-            *(f4*)(part + ((size_t)((rr / G) * nh + kh * G + rr % G) * smax + s) * PART) =
-                f4{mrow * LN2_F, lsum, 0.f, 0.f};
+            if (++gq == G) { gq = 0; ++tq; }
         }
     }
 }
