@@ -16,12 +16,14 @@
 //            S^T = K q^T: MFMA columns 0-7 carry q_hi, 8-15 q_lo of the block's 8 rows, so the two
 //            halves of one score sit in lanes c and c ^ 8 and one DPP row rotate sums them.
 //   softmax: in registers. Each lane holds 4 keys of one row; the row maximum of the tile needs the
-//            other 48 keys, exchanged through a 4x8-float LDS table (barrier A). Running sums stay
-//            per wave and are added once at the end (every wave uses the same running max).
+//            other 48 keys, exchanged through a 4x8-float LDS table (barrier A).
 //   P.V    : P (hi + lo f16 rows, as for q) goes to a small LDS plane in MFMA A layout (barrier B,
-//            which also covers V); wave w then owns output dims 64w..64w+63 for all 64 keys.
-// Per tile that is two barriers; the K/V/q loads of the first tile are all in flight before any
-// of them is consumed, and later tiles are prefetched while P.V runs.
+//            which also covers V); wave w then owns output dims 64w..64w+63 for all 64 keys, and
+//            one more MFMA per k-step against a ones column gives it the full row sums.
+//   records: stored straight from the accumulators (no staging, no barrier).
+// Per tile that is two barriers. First tile: q and K go out first, the q planes are built while K
+// is in flight, then V goes out and the scores and softmax run while it lands; later tiles are
+// prefetched while P.V runs.
 #include "common.h"
 #include "internal.h"
 
@@ -112,7 +114,6 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
     }
     u4 kr[8];
     k_tile_to_regs(kc, kvd, head_off, p0, pend, kr, w, l);
-    v_tile_to_lds(vc, kvd, head_off, p0, pend, V0, w, l);
 #pragma unroll
     for (int it = 0; it < QPT; ++it) {
         const int idx = tid + 256 * it, row = idx >> 5, d0 = 8 * (idx & 31);
@@ -162,6 +163,9 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
     for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) qb[b][ks] = ld_h8(&Qs[c >> 3][8 * b + (c & 7)][32 * ks + 8 * g]);
+    // V goes out only now: the q planes were built while the K rows were in flight, and the scores
+    // and softmax below run while V lands (the memory system is kept busy by the other waves' K)
+    v_tile_to_lds(vc, kvd, head_off, p0, pend, V0, w, l);
 
     int it = 0;
     for (int kb = p0; kb < pend; kb += TK, ++it) {
