@@ -178,6 +178,17 @@ __global__ __launch_bounds__(256) void l2norm_kernel(float* __restrict__ x, int 
 // across lanes (xor 4..32) and then across the 4 waves through LDS.
 // ck (optional): the state after token ck_after is also written there, straight from the
 // registers (the MTP verify checkpoint; no second pass over the state).
+// Sum over the 16 lanes of a wave that share l & 3 (lane bits 2-5), every lane receiving its
+// group's sum: two DPP row rotates (by 4 and 8) sum within each 16-lane row, then the rows are
+// added by swapping lane halves (v_permlane16_swap, then v_permlane32_swap). No LDS traffic.
+__device__ __forceinline__ float sum_lanes_stride4(float v) {
+    v += dppc<0x124>(v);   // row_ror:4
+    v += dppc<0x128>(v);   // row_ror:8
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return sum_xor32(a + b);
+}
+
 __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__ co, int cts, const float* __restrict__ br,
                                                        const float* __restrict__ ar, int bts, const float* __restrict__ dt,
                                                        const float* __restrict__ A, float* __restrict__ state,
@@ -203,9 +214,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
         s0 *= eg; s1 *= eg;
         f4 p = s0 * k0 + s1 * k1;
 #pragma unroll
-        for (int m = 4; m < 64; m <<= 1)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) p[j] += __shfl_xor(p[j], m);
+        for (int j = 0; j < 4; ++j) p[j] = sum_lanes_stride4(p[j]);
         if (l < 4) red1[w][l] = p;
         __syncthreads();
         const f4 sk = red1[0][cg] + red1[1][cg] + red1[2][cg] + red1[3][cg];
@@ -213,9 +222,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
         s0 += k0 * delta; s1 += k1 * delta;
         f4 o = s0 * q0 + s1 * q1;
 #pragma unroll
-        for (int m = 4; m < 64; m <<= 1)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] += __shfl_xor(o[j], m);
+        for (int j = 0; j < 4; ++j) o[j] = sum_lanes_stride4(o[j]);
         if (l < 4) red2[w][l] = o;
         __syncthreads();
         if (tid < 4) {
