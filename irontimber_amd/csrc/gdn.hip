@@ -151,6 +151,73 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restric
     }
 }
 
+// The same pass with 16-byte accesses (strides and bases 16-byte aligned, cd % 256 == 0): lane l
+// holds channels 256*wb + 4l .. 4l+3 of wave block wb, so lanes 0-31 and 32-63 each hold one
+// 128-channel head and a head's sum of squares is a reduction over its 32 lanes (DPP within the
+// 16-lane rows, then a row swap). A quarter of the memory instructions of the scalar form.
+template <int K>
+__global__ __launch_bounds__(256) void gdn_conv_l2_v4_kernel(const float* __restrict__ x, int xts,
+                                                             const float* __restrict__ w, float* __restrict__ state,
+                                                             float* __restrict__ out, int ots, int cd, int nt, int TT,
+                                                             int nnorm, float eps, float* __restrict__ ck,
+                                                             int ck_after) {
+    constexpr int TMAX = 16;   // tokens per run (the host passes TT <= TMAX)
+    const int wb = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (wb >= cd / 256) return;   // whole waves
+    const int ch = 256 * wb + 4 * l;
+    const bool norm = (ch >> 7) < nnorm;   // uniform over each 32-lane half
+    const int t0 = blockIdx.y * TT, n = min(nt, t0 + TT) - t0;
+    f4 xs[TMAX], wt[K], win[K - 1];
+#pragma unroll
+    for (int j = 0; j < TMAX; ++j) xs[j] = ld_f4(x + (size_t)(t0 + min(j, n - 1)) * xts + ch);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {   // taps of channel ch + e are w[(ch + e) * K .. + K)
+#pragma unroll
+        for (int i = 0; i < K; ++i) wt[i][e] = w[(size_t)(ch + e) * K + i];
+    }
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) {
+        const int tt = t0 - (K - 1) + i;
+        win[i] = tt >= 0 ? ld_f4(x + (size_t)tt * xts + ch) : ld_f4(state + (size_t)(tt + K - 1) * cd + ch);
+    }
+#pragma unroll
+    for (int j = 0; j < TMAX; ++j) {
+        if (j >= n) continue;   // wave-uniform; keeps the loop fully unrollable
+        f4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < K - 1; ++i) acc += win[i][e] * wt[i][e];
+            acc += xs[j][e] * wt[K - 1][e];
+            y[e] = siluf_(acc);
+        }
+        float ss = y[0] * y[0] + y[1] * y[1] + y[2] * y[2] + y[3] * y[3];
+        ss += dppc<0xB1>(ss);    // quad_perm [1,0,3,2]
+        ss += dppc<0x4E>(ss);    // quad_perm [2,3,0,1]
+        ss += dppc<0x141>(ss);   // row_half_mirror
+        ss += dppc<0x140>(ss);   // row_mirror
+        {
+            float a = ss, b = ss;   // rows 0+1 and 2+3: the two heads' sums
+            asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+            ss = a + b;
+        }
+        if (norm) y *= 1.0f / fmaxf(sqrtf(ss), eps);
+        *(f4*)(out + (size_t)(t0 + j) * ots + ch) = y;
+#pragma unroll
+        for (int i = 0; i + 1 < K - 1; ++i) win[i] = win[i + 1];
+        win[K - 2] = xs[j];
+        if (ck && t0 + j == ck_after && gridDim.y == 1) {
+#pragma unroll
+            for (int i = 0; i < K - 1; ++i) *(f4*)(ck + (size_t)i * cd + ch) = win[i];
+        }
+    }
+    if (gridDim.y == 1) {
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i) *(f4*)(state + (size_t)i * cd + ch) = win[i];
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // L2 norm of rows of D floats, one wave per row, in place: x / max(||x||, eps).
 template <int D>
@@ -367,10 +434,19 @@ hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* st
                               int nt, int K, int nnorm, float eps, float* ck, int ck_after, hipStream_t st) {
     const int TT = nt <= 16 ? nt : 16;
     const dim3 grid((cd / 128 + 3) / 4, (nt + TT - 1) / TT);
+    // 16-byte form for prompts (several 16-token runs) when every access is 16-byte aligned and a
+    // wave's 256 channels are whole; a decode or verify token keeps twice the waves of the scalar form
+    const bool v4 = nt > 16 && cd % 256 == 0 && xts % 4 == 0 && ots % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
+                    ((uintptr_t)out & 15) == 0 && ((uintptr_t)state & 15) == 0 && (!ck || ((uintptr_t)ck & 15) == 0);
+    const dim3 grid4((cd / 256 + 3) / 4, (nt + TT - 1) / TT);
 #define IT_CONVL2(KK)                                                                                               \
     if (ck && grid.y > 1)                                                                                           \
         gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, ck, cd, ck_after + 1);          \
-    gdn_conv_l2_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck, ck_after); \
+    if (v4)                                                                                                         \
+        gdn_conv_l2_v4_kernel<KK><<<grid4, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck,    \
+                                                         ck_after);                                                  \
+    else                                                                                                            \
+        gdn_conv_l2_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck, ck_after); \
     if (grid.y > 1) gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, state, cd, nt);
     switch (K) {
         case 2: IT_CONVL2(2) break;
