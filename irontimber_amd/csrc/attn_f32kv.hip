@@ -55,6 +55,7 @@ __device__ __forceinline__ float sum_xor16(float v) {
 constexpr int F32KV_ROW = F32KV_HD + 4;                 // padded LDS row (floats)
 constexpr int F32KV_WAVE = 2 * 16 * F32KV_ROW;          // K then V rows of one wave
 #define IT_F32KV_WAIT_VMCNT0() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
+#define IT_F32KV_WAIT_VMCNT16() asm volatile("s_waitcnt vmcnt(16)" ::: "memory")
 
 __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict__ q, int qts,
                                                          const float* __restrict__ kc, const float* __restrict__ vc,
@@ -76,15 +77,23 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
     float* Vw = Kw + 16 * F32KV_ROW;
 
     // This wave's 16 K and V rows of tile kt (keys kt + 16w + r), lane l bringing dims 4l .. 4l+3.
-    auto stage = [&](int kt) {
+    // K rows first, V rows after: the scores and the softmax only wait for the K rows (16 loads
+    // older than the 16 V loads), so they run while V lands.
+    auto stage_k = [&](int kt) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const size_t row = (size_t)min(kt + 16 * w + r, total - 1) * kvd + (size_t)kh * F32KV_HD + 4 * l;
             __builtin_amdgcn_global_load_lds(kc + row, (lds_void*)(Kw + r * F32KV_ROW), 16, 0, 0);
+        }
+    };
+    auto stage_v = [&](int kt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const size_t row = (size_t)min(kt + 16 * w + r, total - 1) * kvd + (size_t)kh * F32KV_HD + 4 * l;
             __builtin_amdgcn_global_load_lds(vc + row, (lds_void*)(Vw + r * F32KV_ROW), 16, 0, 0);
         }
     };
-    stage(kb0);   // the first tile's rows are in flight while q loads below
+    stage_k(kb0);   // the first tile's K rows are in flight while q loads below
 
     // Score product j = 4*jj + c contracts dims {16*jj + 4*lg + c : lg = 0..3}: lane l holds dims
     // 16*jj + 4*lg .. +3 of its key row (A) and of its query row (B).
@@ -96,6 +105,7 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
     f4 qv[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) qv[j] = ld_f4(qp + 16 * j) * qs;
+    stage_v(kb0);
 
     float m_run = -1e30f, l_run = 0.f;   // log2 units; finite floor keeps fully masked blocks NaN-free
     f4 acc[16];                          // O^T blocks (dq, e): dims 16*lg + 4*ii + 64*dq + e of row lr
@@ -103,8 +113,11 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
     for (int b = 0; b < 16; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
 
     for (int kt = kb0; kt < kend; kt += F32KV_KEYS) {
-        if (kt != kb0) stage(kt);
-        IT_F32KV_WAIT_VMCNT0();
+        if (kt != kb0) {
+            stage_k(kt);
+            stage_v(kt);
+        }
+        IT_F32KV_WAIT_VMCNT16();   // K rows (and q): the 16 V loads may still fly
         // S^T block: element i = key kt + 16w + 4lg + i, query row lr (4 independent chains).
         f4 sa[4] = {};
 #pragma unroll
@@ -133,6 +146,7 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
         }
         l_run = l_run * alpha + sum_xor32(sum_xor16(ps));
         m_run = m_new;
+        IT_F32KV_WAIT_VMCNT0();   // V rows
         // O^T += V^T P^T: MFMA i takes key 4lg + i of the block (its A element from V, its B element
         // this lane's p[i]); output block b = (dq, e) holds dims 16lg + 4ii + 64dq + e.
 #pragma unroll
