@@ -33,9 +33,6 @@ constexpr size_t OFF_AQK = OFF_KT + SD * C * 2;     // f16 [C][C]    lower_incl(
 constexpr size_t OFF_U = OFF_AQK + C * C * 2;       // f32 [C][SD]   U
 constexpr size_t OFF_GC = OFF_U + C * SD * 4;       // f32 [4]       e^{G_last} (4 copies)
 constexpr size_t REC = (OFF_GC + 16 + 255) / 256 * 256;
-// f16 LDS row stride of the solve buffers; transpose reads need every 4-lane 32-byte segment
-// 32-byte aligned, so the row pitch (288 B) is a multiple of 32 bytes
-constexpr int XS = SD + 16;
 }
 #define IT_SCAN_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
 
@@ -45,11 +42,24 @@ size_t gdn_chunked_scratch_bytes(int nt, int nv, int S) {
     return nch * (size_t)nv * REC;
 }
 
+__device__ __forceinline__ f4 mfma16x16x16(h4 a, h4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+// hi + lo f16 split of 4 floats (hi + lo == x to ~2^-22)
+__device__ __forceinline__ void split_hi_lo4(f4 x, h4& hi, h4& lo) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const _Float16 h = (_Float16)x[j];
+        hi[j] = h;
+        lo[j] = (_Float16)(x[j] - (float)h);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
-// 8 waves, 69 KB of LDS (two workgroups per CU, so one's loads overlap the other's products): the
-// K rows as f16 hi/lo pairs, A', the diagonal-block inverses and the current block's right-hand
-// side; the solve rows X reuse the K tile once K is dead. Q never enters LDS: the Q K^T operands
-// and e^G q are read from global (the chunk's q rows stay in L2).
+// 8 waves, 60 KB of LDS (two workgroups per CU, so one's loads overlap the other's products): the
+// K rows as f16 hi/lo pairs (the V rows pass through the same tile once K is dead), A' and the
+// diagonal-block inverses. Q never enters LDS: the Q K^T operands and e^G q are read from global
+// (the chunk's q rows stay in L2). The triangular solve runs in registers.
 constexpr int PREP_THREADS = 512;
 constexpr int KP = SD + 16;    // f16 row pitch of the K tile (288 B, 32-byte multiple)
 
@@ -58,13 +68,11 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
                                                                int bts, const float* __restrict__ dt,
                                                                const float* __restrict__ A, int nt, int nk,
                                                                char* __restrict__ scr) {
-    __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows hi / lo, then the solve rows X
+    __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows hi / lo, then the V rows (f32)
     __shared__ __align__(16) float Ap[C][C + 4];
     __shared__ float sG[C], sB[C];
     __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
-    __shared__ __align__(16) _Float16 Rs[2][16][XS];         // right-hand side of the current block
-    static_assert(KP == XS, "solve rows reuse the K tile");
-    _Float16(*Xs)[C][XS] = Kx;
+    static_assert(2 * C * KP * 2 >= C * SD * 4, "the V rows fit in the K tile");
 
     const int c = blockIdx.x, h = blockIdx.y, nch = gridDim.x;
     const int t0 = c * C, L = min(C, nt - t0);
@@ -178,7 +186,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     // ---- (I + A') [W | U] = diag(beta) [e^G K | V], blocked by 16 rows:
     //   T_i = (I + A'_ii)^-1 (16x16, one wave, forward substitution per column)
     //   X_i = T_i (diag(beta) B_i - sum_{k<i} A'_ik X_k)          (MFMA, hi+lo products)
-    // W and U are solved one after the other (128 columns each, one 16-column tile per wave).
+    // W and U are solved one after the other (128 columns each, one 16-column block per wave).
     if (w == 0) {
         const int kb = l >> 4, ci = l & 15;
         float y[16];
@@ -211,7 +219,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             rhs[0][i][e] = sB[t] * (expf(sG[t]) * ((float)Kx[0][t][col] + (float)Kx[1][t][col]));
         }
     __syncthreads();   // the K tile is dead: V passes through it to its solve lanes
-    float* const Vs = (float*)&Xs[0][0][0];   // [C][SD] f32, 32 KB of the 36 KB tile
+    float* const Vs = (float*)&Kx[0][0][0];   // [C][SD] f32, 32 KB of the 36 KB tile
 #pragma unroll
     for (int j = 0; j < 4; ++j) *(f4*)(Vs + (tid >> 3) * SD + 16 * (tid & 7) + 4 * j) = vreg[j];
     __syncthreads();
@@ -222,69 +230,40 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             const int t = 16 * i + 4 * g + e;
             rhs[1][i][e] = sB[t] * Vs[t * SD + col];
         }
+    // Each wave solves its own 16 columns in registers, no LDS and no barrier: the accumulator of a
+    // 16x16x16 MFMA (lane = column li, rows 4g..4g+3) is exactly its B-operand layout (k = 4g..4g+3),
+    // so X_k feeds the next block rows and R_i feeds T_i R_i straight from registers.
+    //   R_i = beta B_i - sum_{k<i} A'_ik X_k,   X_i = T_i R_i   (hi+lo products on both sides)
     for (int hf = 0; hf < 2; ++hf) {
-        __syncthreads();   // every wave is done with the tile (V, or the previous half's X)
-        for (int idx = tid; idx < 2 * C * XS / 8; idx += PREP_THREADS) ((u4*)&Xs[0][0][0])[idx] = u4{0u, 0u, 0u, 0u};
-        __syncthreads();
+        f4 X[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            // R = beta B_i - sum_{k<i} A'_ik X_k for this wave's 16-column tile
-            f4 acc;
+            f4 acc = {rhs[hf][i][0], rhs[hf][i][1], rhs[hf][i][2], rhs[hf][i][3]};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = rhs[hf][i][e];
-#pragma unroll
-            for (int ks = 0; ks < (i + 1) / 2; ++ks) {
-                // A operand: -A'[16i + li][32ks + 8g + j], zero at and past column 16i
-                const int s0 = 32 * ks + 8 * g;
-                const float* arow = &Ap[16 * i + li][s0];
-                const f4 a0 = s0 < 16 * i ? -*(const f4*)arow : f4{0.f, 0.f, 0.f, 0.f};
-                const f4 a1 = s0 + 4 < 16 * i ? -*(const f4*)(arow + 4) : f4{0.f, 0.f, 0.f, 0.f};
-                h8 ah, al;
-                split_hi_lo(a0, a1, ah, al);
-                const int c0 = 16 * w;
-                const _Float16* xh = &Xs[0][s0 + (li >> 2)][c0 + 4 * (li & 3)];
-                const _Float16* xl = &Xs[1][s0 + (li >> 2)][c0 + 4 * (li & 3)];
-                const h8 bh = cat_h4(lds_tr4(xh), lds_tr4(xh + 4 * XS));
-                const h8 bl = cat_h4(lds_tr4(xl), lds_tr4(xl + 4 * XS));
-                acc = mfma16x16x32(ah, bh, acc);
-                acc = mfma16x16x32(ah, bl, acc);
-                acc = mfma16x16x32(al, bh, acc);
+            for (int k = 0; k < i; ++k) {
+                const f4 a = -*(const f4*)&Ap[16 * i + li][16 * k + 4 * g];
+                h4 ah, al, xh, xl;
+                split_hi_lo4(a, ah, al);
+                split_hi_lo4(X[k], xh, xl);
+                acc = mfma16x16x16(ah, xh, acc);
+                acc = mfma16x16x16(ah, xl, acc);
+                acc = mfma16x16x16(al, xh, acc);
             }
-            // R -> LDS (hi/lo) so it can be the B operand of T_i R
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float v = acc[e];
-                const _Float16 hi = (_Float16)v;
-                Rs[0][4 * g + e][col] = hi;
-                Rs[1][4 * g + e][col] = (_Float16)(v - (float)hi);
-            }
-            __syncthreads();
-            // X_i = T_i R: K = 16 (k-groups 2 and 3 are zero padding)
-            h8 th = {}, tl = {};
-            if (g < 2) split_hi_lo(*(const f4*)&Td[i][li][8 * g], *(const f4*)&Td[i][li][8 * g + 4], th, tl);
-            // transpose reads run with the whole wave active; k-groups 2 and 3 reread rows 0..7
-            const int gr = g & 1, c0 = 16 * w;
-            const _Float16* rh = &Rs[0][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
-            const _Float16* rl = &Rs[1][8 * gr + (li >> 2)][c0 + 4 * (li & 3)];
-            h8 bh = cat_h4(lds_tr4(rh), lds_tr4(rh + 4 * XS));
-            h8 bl = cat_h4(lds_tr4(rl), lds_tr4(rl + 4 * XS));
-            if (g >= 2) { bh = h8{}; bl = h8{}; }
+            h4 th, tl, rh, rl;
+            split_hi_lo4(*(const f4*)&Td[i][li][4 * g], th, tl);
+            split_hi_lo4(acc, rh, rl);
             f4 z = {0.f, 0.f, 0.f, 0.f};
-            z = mfma16x16x32(th, bh, z);
-            z = mfma16x16x32(th, bl, z);
-            z = mfma16x16x32(tl, bh, z);
-            // X_i -> scratch (W f16 / U f32) and -> LDS (hi/lo) for the later block rows
+            z = mfma16x16x16(th, rh, z);
+            z = mfma16x16x16(th, rl, z);
+            z = mfma16x16x16(tl, rh, z);
+            X[i] = z;
+            // X_i -> scratch (W f16 / U f32)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = 16 * i + 4 * g + e;
-                const float v = z[e];
-                const _Float16 hi = (_Float16)v;
-                Xs[0][t][col] = hi;
-                Xs[1][t][col] = (_Float16)(v - (float)hi);
-                if (hf == 0) ((_Float16*)(rec + OFF_W))[t * SD + col] = hi;
-                else ((float*)(rec + OFF_U))[t * SD + col] = v;
+                if (hf == 0) ((_Float16*)(rec + OFF_W))[t * SD + col] = (_Float16)z[e];
+                else ((float*)(rec + OFF_U))[t * SD + col] = z[e];
             }
-            __syncthreads();
         }
     }
 }
