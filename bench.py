@@ -336,6 +336,17 @@ def main():
         res["gdn_step_state_GBs"] = round(gbytes / (gst_us * 1e-6) / 1e9, 1)
         log(f"gdn: layer {res['gdn_decode_layer_us']} us, step {gst_us:.2f} us ({res['gdn_step_state_GBs']} GB/s state)")
 
+        # the same layer in one launch (conv state ping-pongs between two buffers)
+        cst2 = [t(d["conv_state"]), t(d["conv_state"])]
+
+        def gdn_layer_fused(i):
+            call("it_gdn_decode_fused", x.data_ptr(), d["cd"], w.data_ptr(), 4, cst2[i & 1].data_ptr(),
+                 cst2[(i + 1) & 1].data_ptr(), br.data_ptr(), ar.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
+                 states[i % NST].data_ptr(), og.data_ptr(), nv * S, 1, nv, nk, S, 1e-6, stream_of())
+        ms = graph_time_ms(torch, lambda: [gdn_layer_fused(i) for i in range(K)], reps=3)
+        res["gdn_decode_layer_fused_us"] = round(ms * 1000 / K, 3)
+        log(f"gdn: layer in one launch {res['gdn_decode_layer_fused_us']} us")
+
         # the reference's whole GDN decode output: recurrence + gated RMSNorm (rmsnorm mode 1), as two
         # kernels and as one (the per-head recurrence with the epilogue fused)
         zg = torch.randn(1, nv * S, device=dev)

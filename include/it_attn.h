@@ -184,6 +184,21 @@ int it_gdn_step(const float* co, int co_tok_stride, const float* beta_raw, const
                 int ba_tok_stride, const float* dt, const float* a, float* state, float* out,
                 int out_tok_stride, int nt, int nv, int nk, int S, void* stream);
 
+/* A GDN decode layer in one launch: it_gdn_conv_l2norm (nnorm = 2*nk) followed by it_gdn_step,
+ * for 1 <= nt <= 4 tokens, without the conv output ever reaching memory.
+ *   x, x_tok_stride, w, K : as for it_gdn_conv (cd = (2*nk + nv)*S); x and w 16-byte aligned,
+ *                           stride % 4 == 0
+ *   conv_state_in         : f32 [(K-1)][cd], the conv state before token 0 (read only)
+ *   conv_state_out        : f32 [(K-1)][cd], receives the conv state after token nt-1; it must not
+ *                           overlap conv_state_in (every workgroup reads the old state while others
+ *                           write the new one: callers alternate two buffers)
+ *   the rest              : as for it_gdn_step (state updated in place), eps as for the L2 norm.
+ * Replaces the conv, rmsnorm mode 2 and gdn dispatch triple, src/vk/mod.rs:803-806 (cpu.rs:201-232). */
+int it_gdn_decode_fused(const float* x, int x_tok_stride, const float* w, int K, const float* conv_state_in,
+                        float* conv_state_out, const float* beta_raw, const float* alpha_raw, int ba_tok_stride,
+                        const float* dt, const float* a, float* state, float* out, int out_tok_stride, int nt,
+                        int nv, int nk, int S, float eps, void* stream);
+
 /* The GDN output's gated RMSNorm, per (token t, V head h) row of S = 128:
  *   out[t*out_tok_stride + h*S + j] = o_j / sqrt(mean_j(o^2) + eps) * w[j] * silu(z[t*z_tok_stride + h*S + j])
  * with o the row o[t*o_tok_stride + h*S ...] and w [S] (ssm_norm, shared by the heads). out may be

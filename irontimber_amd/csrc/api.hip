@@ -339,6 +339,29 @@ int it_gdn_step(const float* co, int cts, const float* br, const float* ar, int 
                  "it_gdn_step");
 }
 
+int it_gdn_decode_fused(const float* x, int xts, const float* w, int K, const float* cst_in, float* cst_out,
+                        const float* br, const float* ar, int bts, const float* dt, const float* a, float* state,
+                        float* out, int ots, int nt, int nv, int nk, int S, float eps, void* stream) {
+    const char* who = "it_gdn_decode_fused";
+    if (S != 128) return fail("%s: state size %d unsupported (128)", who, S);
+    if (nv <= 0 || nk <= 0 || nv % nk != 0) return fail("%s: nv %d / nk %d invalid", who, nv, nk);
+    if (nt < 1 || nt > 4) return fail("%s: nt %d outside 1..4 (longer runs: it_gdn_conv_l2norm + it_gdn_step)", who, nt);
+    if (K < 2 || K > 4) return fail("%s: kernel size %d unsupported (2..4)", who, K);
+    if (!x || !w || !cst_in || !cst_out || !br || !ar || !dt || !a || !state || !out) return fail("%s: null buffer", who);
+    const int cd = (2 * nk + nv) * S;
+    if (!aligned16(x) || !aligned16(w) || !aligned16(cst_in) || !aligned16(cst_out) || !aligned16(state) ||
+        !aligned16(out))
+        return fail("%s: x / w / conv states / state / out must be 16-byte aligned", who);
+    if (xts % 4 != 0 || ots % 4 != 0) return fail("%s: token strides must be multiples of 4", who);
+    if (nt > 1 && (xts < cd || ots < nv * S || bts < nv)) return fail("%s: token strides overlap rows", who);
+    const size_t cbytes = (size_t)(K - 1) * cd * sizeof(float);
+    const char *pi = (const char*)cst_in, *po = (const char*)cst_out;
+    if (pi < po + cbytes && po < pi + cbytes) return fail("%s: conv_state_out overlaps conv_state_in", who);
+    return check(it::launch_gdn_decode_fused(x, xts, w, K, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv,
+                                             nk, eps, (hipStream_t)stream),
+                 who);
+}
+
 int it_gdn_step_ckpt(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                      const float* a, float* state, float* out, int ots, int nt, int nv, int nk, int S, float* ck_state,
                      int ck_after, void* stream) {

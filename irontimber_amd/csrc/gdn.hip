@@ -307,6 +307,168 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------------
+// Decode layer in one launch: conv + SiLU + q/k L2 norm + recurrence for up to FUSED_TMAX tokens.
+// Same workgroup and thread layout as gdn_step_kernel; each thread also runs the conv of the
+// channels it consumes (q and k at rows i0, i0+1 of its QK head, v at columns j0..j0+3 of its V
+// head) from the old conv state, so no workgroup waits for another. The q/k head norms sum over
+// the workgroup (each row pair is held by the 4 threads of a column group: lanes with equal l & 3
+// cover 16 distinct rows per wave, then the 4 waves through LDS). The new conv state goes to a
+// separate buffer (reading and rewriting one buffer would race between workgroups): q/k channels
+// by the first column block of the QK head's first V head, v channels by row pair 0 of each
+// workgroup. Arithmetic order of the conv and of the step as in gdn_conv_l2_kernel and
+// gdn_step_kernel; the norms' sums are added in another order (last-bit differences).
+constexpr int FUSED_TMAX = 4;
+
+template <int K>
+__global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
+    const float* __restrict__ x, int xts, const float* __restrict__ cw, const float* __restrict__ cst_in,
+    float* __restrict__ cst_out, const float* __restrict__ br, const float* __restrict__ ar, int bts,
+    const float* __restrict__ dt, const float* __restrict__ A, float* __restrict__ state, float* __restrict__ out,
+    int ots, int nt, int nv, int nk, float eps) {
+    constexpr int S = 128;
+    __shared__ f4 red1[4][4], red2[4][4];
+    __shared__ f2 nrm[2][4];   // per wave: {sum q^2, sum k^2} of its 16 row pairs, per token parity
+    const int cb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int cg = tid & 3, rp = tid >> 2;
+    const int kh = h % nk, qk = nk * S, cd = (2 * nk + nv) * S;
+    const int j0 = cb * 16 + 4 * cg, i0 = 2 * rp;
+    const int cq = kh * S + i0, ck = qk + kh * S + i0, cv = 2 * qk + h * S + j0;   // channel bases
+    float* sb = state + (size_t)h * S * S;
+    // every load up front: state, tokens, weights, the conv window
+    f4 s0 = ld_f4(sb + (size_t)i0 * S + j0), s1 = ld_f4(sb + (size_t)(i0 + 1) * S + j0);
+    f2 xq[FUSED_TMAX], xk[FUSED_TMAX];
+    f4 xv[FUSED_TMAX];
+#pragma unroll
+    for (int t = 0; t < FUSED_TMAX; ++t) {
+        const float* xr = x + (size_t)min(t, nt - 1) * xts;
+        xq[t] = *(const f2*)(xr + cq);
+        xk[t] = *(const f2*)(xr + ck);
+        xv[t] = ld_f4(xr + cv);
+    }
+    float wq[2][K], wk[2][K], wv[4][K];
+    if constexpr (K == 4) {   // a channel's taps are one aligned f4 (channel bases are even)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const f4 a4 = ld_f4(cw + (size_t)(cq + e) * 4), b4 = ld_f4(cw + (size_t)(ck + e) * 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { wq[e][i] = a4[i]; wk[e][i] = b4[i]; }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const f4 c4 = ld_f4(cw + (size_t)(cv + e) * 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wv[e][i] = c4[i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                wq[e][i] = cw[(size_t)(cq + e) * K + i];
+                wk[e][i] = cw[(size_t)(ck + e) * K + i];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wv[e][i] = cw[(size_t)(cv + e) * K + i];
+        }
+    }
+    f2 wnq[K - 1], wnk[K - 1];
+    f4 wnv[K - 1];
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) {
+        wnq[i] = *(const f2*)(cst_in + (size_t)i * cd + cq);
+        wnk[i] = *(const f2*)(cst_in + (size_t)i * cd + ck);
+        wnv[i] = ld_f4(cst_in + (size_t)i * cd + cv);
+    }
+    const float scale = 1.0f / sqrtf((float)S);
+    const float dth = dt[h], ah = A[h];
+#pragma unroll
+    for (int t = 0; t < FUSED_TMAX; ++t) {
+        if (t >= nt) break;   // uniform
+        // ---- conv + SiLU of this thread's channels
+        float q[2], k[2];
+        f4 v;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            float a = 0.f, b = 0.f;
+#pragma unroll
+            for (int i = 0; i < K - 1; ++i) { a += wnq[i][e] * wq[e][i]; b += wnk[i][e] * wk[e][i]; }
+            a += xq[t][e] * wq[e][K - 1];
+            b += xk[t][e] * wk[e][K - 1];
+            q[e] = siluf_(a);
+            k[e] = siluf_(b);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < K - 1; ++i) a += wnv[i][e] * wv[e][i];
+            a += xv[t][e] * wv[e][K - 1];
+            v[e] = siluf_(a);
+        }
+#pragma unroll
+        for (int i = 0; i + 1 < K - 1; ++i) { wnq[i] = wnq[i + 1]; wnk[i] = wnk[i + 1]; wnv[i] = wnv[i + 1]; }
+        wnq[K - 2] = xq[t];
+        wnk[K - 2] = xk[t];
+        wnv[K - 2] = xv[t];
+        // ---- L2 norms of the q and k heads
+        const float sq = sum_lanes_stride4(q[0] * q[0] + q[1] * q[1]);
+        const float sk2 = sum_lanes_stride4(k[0] * k[0] + k[1] * k[1]);
+        if (l == 0) nrm[t & 1][w] = f2{sq, sk2};
+        __syncthreads();
+        const f2 n = (nrm[t & 1][0] + nrm[t & 1][1]) + (nrm[t & 1][2] + nrm[t & 1][3]);
+        const float fq = 1.0f / fmaxf(sqrtf(n[0]), eps), fk = 1.0f / fmaxf(sqrtf(n[1]), eps);
+        const float q0 = q[0] * fq, q1 = q[1] * fq, k0 = k[0] * fk, k1 = k[1] * fk;
+        // ---- recurrence (gdn_step_kernel)
+        const float beta = sigmoidf_(br[(size_t)t * bts + h]);
+        const float eg = expf(softplusf_(ar[(size_t)t * bts + h] + dth) * ah);
+        s0 *= eg; s1 *= eg;
+        f4 p = s0 * k0 + s1 * k1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = sum_lanes_stride4(p[j]);
+        if (l < 4) red1[w][l] = p;
+        __syncthreads();
+        const f4 skv = red1[0][cg] + red1[1][cg] + red1[2][cg] + red1[3][cg];
+        const f4 delta = (v - skv) * beta;
+        s0 += k0 * delta; s1 += k1 * delta;
+        f4 o = s0 * q0 + s1 * q1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = sum_lanes_stride4(o[j]);
+        if (l < 4) red2[w][l] = o;
+        __syncthreads();
+        if (tid < 4) {
+            const f4 ot = (red2[0][cg] + red2[1][cg] + red2[2][cg] + red2[3][cg]) * scale;
+            *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = ot;
+        }
+    }
+    *(f4*)(sb + (size_t)i0 * S + j0) = s0;
+    *(f4*)(sb + (size_t)(i0 + 1) * S + j0) = s1;
+    if (cb == 0 && h == kh && cg == 0) {
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i) {
+            *(f2*)(cst_out + (size_t)i * cd + cq) = wnq[i];
+            *(f2*)(cst_out + (size_t)i * cd + ck) = wnk[i];
+        }
+    }
+    if (rp == 0) {
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i) *(f4*)(cst_out + (size_t)i * cd + cv) = wnv[i];
+    }
+}
+
+hipError_t launch_gdn_decode_fused(const float* x, int xts, const float* cw, int K, const float* cst_in, float* cst_out,
+                                   const float* br, const float* ar, int bts, const float* dt, const float* a,
+                                   float* state, float* out, int ots, int nt, int nv, int nk, float eps,
+                                   hipStream_t st) {
+    const dim3 grid(8, nv);
+    switch (K) {
+        case 2: gdn_decode_fused_kernel<2><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps); break;
+        case 3: gdn_decode_fused_kernel<3><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps); break;
+        default: gdn_decode_fused_kernel<4><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps); break;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
 // Gated RMSNorm epilogue of the GDN output, per (token, V head) row of 128:
 //   out = o / sqrt(mean(o^2) + eps) * w * silu(z)
 // One wave per row, lane l holds elements l and l + 64. out may alias o.

@@ -37,6 +37,10 @@ hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state
 hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd,
                               int nt, int K, int nnorm, float eps, float* ck, int ck_after, hipStream_t st);
 hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps, hipStream_t st);
+hipError_t launch_gdn_decode_fused(const float* x, int xts, const float* cw, int K, const float* cst_in, float* cst_out,
+                                   const float* br, const float* ar, int bts, const float* dt, const float* a,
+                                   float* state, float* out, int ots, int nt, int nv, int nk, float eps,
+                                   hipStream_t st);
 hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                            const float* a, float* state, float* out, int ots, int nt, int nv, int nk, float* ck,
                            int ck_after, hipStream_t st);

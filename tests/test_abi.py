@@ -89,6 +89,14 @@ def test_attn_rejects_bad_geometry_before_device_work():
     assert rc != 0 and "kernel size" in _lib.last_error()
     rc = lib.it_kv_append_f16(fake, fake, 512, fake, fake, 0, 1, 512, 2, None)
     assert rc != 0 and "round_mode" in _lib.last_error()
+    # fused GDN decode layer: token count, and the conv-state buffers must not overlap
+    rc = lib.it_gdn_decode_fused(fake, 8192, fake, 4, fake, fake, fake, fake, 32, fake, fake, fake, fake, 4096, 5,
+                                 32, 16, 128, 1e-6, None)
+    assert rc != 0 and "nt 5" in _lib.last_error()
+    st_in, st_out = ctypes.c_void_p(1 << 20), ctypes.c_void_p((1 << 20) + 4096)
+    rc = lib.it_gdn_decode_fused(fake, 8192, fake, 4, st_in, st_out, fake, fake, 32, fake, fake, fake, fake, 4096, 1,
+                                 32, 16, 128, 1e-6, None)
+    assert rc != 0 and "overlaps" in _lib.last_error()
 
 
 def test_scratch_bytes_policy():

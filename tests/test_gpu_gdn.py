@@ -94,6 +94,50 @@ def test_layer_config4(dev):
     assert_argmax_agrees(out, out_ref)
 
 
+def test_decode_fused_config4(dev):
+    """BASELINE config 4 (seed 3) through the one-launch decode layer: against cpu.rs's layer pass
+    (conv -> L2 -> recurrence) at the north-star bounds, the new conv state bit-exact, the old conv
+    state untouched; argmax of a fixed projection agrees."""
+    nv, nk, S = 32, 16, 128
+    d = gdn_inputs(3, nt=1, nv=nv, nk=nk)
+    co_ref = np.zeros((1, d["cd"]), np.float32)
+    cst, sst = d["conv_state"].copy(), d["state"].copy()
+    out_ref = np.zeros((1, nv * S), np.float32)
+    P = lambda a: a.ctypes.data
+    oracle.lib().it_ref_gdn_layer(P(d["x"]), d["cd"], P(d["w"]), P(cst), 4, P(d["beta_raw"]), P(d["alpha_raw"]), nv,
+                                  P(d["dt"]), P(d["a"]), P(sst), P(out_ref), nv * S, P(co_ref), 1, nv, nk, S, 1e-6, 8)
+    cs_in, st = dev_f32(d["conv_state"], dev), dev_f32(d["state"], dev)
+    cs_out = torch.full_like(cs_in, float("nan"))
+    out = host(ops.gdn_decode_fused(dev_f32(d["x"], dev), dev_f32(d["w"], dev), cs_in, cs_out, dev_f32(d["beta_raw"], dev),
+                                    dev_f32(d["alpha_raw"], dev), dev_f32(d["dt"], dev), dev_f32(d["a"], dev), st, nv, nk))
+    assert np.abs(out - out_ref).max() <= OUT_TOL
+    assert np.abs(host(st) - sst).max() <= STATE_TOL
+    np.testing.assert_array_equal(host(cs_out), cst)
+    np.testing.assert_array_equal(host(cs_in), d["conv_state"])
+    assert_argmax_agrees(out, out_ref)
+
+
+@pytest.mark.parametrize("nt,nv,nk,K", [(1, 32, 16, 4), (2, 32, 16, 4), (4, 8, 4, 3), (3, 4, 2, 2), (1, 8, 8, 4)])
+def test_decode_fused_equals_two_kernels(dev, nt, nv, nk, K):
+    """The one-launch layer equals it_gdn_conv_l2norm + it_gdn_step on the same inputs (the q/k
+    norms' sums are added in another order: last-bit differences only) and leaves the same conv
+    state, bit for bit, in its output buffer."""
+    announce(f"gdn fused nt={nt} nv={nv} nk={nk} K={K}")
+    d = gdn_inputs(31, nt=nt, nv=nv, nk=nk)
+    x, w = dev_f32(d["x"], dev), dev_f32(d["w"][:, :K], dev)
+    br, ar = dev_f32(d["beta_raw"], dev), dev_f32(d["alpha_raw"], dev)
+    dt, a = dev_f32(d["dt"], dev), dev_f32(d["a"], dev)
+    cs0 = d["conv_state"][:K - 1]
+    cs, st = dev_f32(cs0, dev), dev_f32(d["state"], dev)
+    co = ops.gdn_conv_l2norm(x, w, cs, 2 * nk)
+    want = host(ops.gdn_step(co, br, ar, dt, a, st, nv, nk))
+    cs_in, cs_out, st2 = dev_f32(cs0, dev), torch.full_like(cs, float("nan")), dev_f32(d["state"], dev)
+    got = host(ops.gdn_decode_fused(x, w, cs_in, cs_out, br, ar, dt, a, st2, nv, nk))
+    assert np.abs(got - want).max() <= 1e-5
+    assert np.abs(host(st2) - host(st)).max() <= 1e-5
+    np.testing.assert_array_equal(host(cs_out), host(cs))
+
+
 def test_step_float64_truth(dev):
     d = gdn_step_inputs(4, 6, nv=4, nk=2)
     st = dev_f32(d["state"], dev)
