@@ -113,39 +113,75 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     }
     __syncthreads();
 
-    // ---- lower 16x16 tiles of K K^T (tiles 0..9) and Q K^T (tiles 10..19), hi+lo products; the
-    // Q operand comes from global and is split in registers
-    for (int tile = w; tile < 20; tile += PREP_THREADS / 64) {
-        const bool isq = tile >= 10;
-        const int tt = isq ? tile - 10 : tile;
-        const int mt = tt >= 6 ? 3 : tt >= 3 ? 2 : tt >= 1 ? 1 : 0;
-        const int nt_ = tt - mt * (mt + 1) / 2;
-        const int ta = 16 * mt + li;              // A-operand row (a q row for Q K^T tiles)
-        const float* qr = qrow(ta);
-        const float qm = ta < L ? 1.f : 0.f;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int d = 32 * ks + 8 * g;
-            h8 ah, al;
-            if (isq) {   // wave-uniform
-                split_hi_lo(ld_f4(qr + d) * qm, ld_f4(qr + d + 4) * qm, ah, al);
-            } else {
-                ah = ld_h8(&Kx[0][ta][d]);
-                al = ld_h8(&Kx[1][ta][d]);
-            }
-            const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
-            acc = mfma16x16x32(ah, bh, acc);
-            acc = mfma16x16x32(ah, bl, acc);
-            acc = mfma16x16x32(al, bh, acc);
-        }
-        _Float16* aqk = (_Float16*)(rec + OFF_AQK);
+    // ---- lower 16x16 tiles of K K^T and Q K^T, hi+lo products. The Q K^T tiles are grouped by
+    // their 16-row block, whose q rows (read from global, split in registers) serve every tile of
+    // the block: wave 0 takes row block 3 (4 tiles), wave 1 row block 2 (3), wave 2 row blocks 1
+    // and 0 (3, both blocks' rows loaded together), so each pays one memory round trip. Waves 3-7
+    // take the 10 K K^T tiles, two each.
+    _Float16* aqk = (_Float16*)(rec + OFF_AQK);
+    auto store_tile = [&](bool isq, int mt, int nt_, f4 acc) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = 16 * mt + 4 * g + i, s = 16 * nt_ + li;
             const float d = expf(fminf(sG[t] - sG[s], 0.f));
             if (!isq) Ap[t][s] = s < t ? sB[t] * d * acc[i] : 0.f;
             else aqk[t * C + s] = (_Float16)(s <= t ? d * acc[i] : 0.f);
+        }
+    };
+    if (w < 3) {
+        const int nb = w == 2 ? 2 : 1;                  // row blocks of this wave
+        const int mb0 = w == 0 ? 3 : w == 1 ? 2 : 1;    // first row block; wave 2 then does block 0
+        f4 qv[2][8];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b >= nb) break;   // uniform
+            const int ta = 16 * (mb0 - b) + li;
+            const float* qr = qrow(ta);
+            const float qm = ta < L ? 1.f : 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                qv[b][2 * ks] = ld_f4(qr + 32 * ks + 8 * g) * qm;
+                qv[b][2 * ks + 1] = ld_f4(qr + 32 * ks + 8 * g + 4) * qm;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b >= nb) break;   // uniform
+            const int mt = mb0 - b;
+            h8 ah[4], al[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) split_hi_lo(qv[b][2 * ks], qv[b][2 * ks + 1], ah[ks], al[ks]);
+            for (int nt_ = 0; nt_ <= mt; ++nt_) {
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int d = 32 * ks + 8 * g;
+                    const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
+                    acc = mfma16x16x32(ah[ks], bh, acc);
+                    acc = mfma16x16x32(ah[ks], bl, acc);
+                    acc = mfma16x16x32(al[ks], bh, acc);
+                }
+                store_tile(true, mt, nt_, acc);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int tt = (w - 3) + 5 * k;   // K K^T tile 0..9
+            const int mt = tt >= 6 ? 3 : tt >= 3 ? 2 : tt >= 1 ? 1 : 0;
+            const int nt_ = tt - mt * (mt + 1) / 2;
+            const int ta = 16 * mt + li;
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int d = 32 * ks + 8 * g;
+                const h8 ah = ld_h8(&Kx[0][ta][d]), al = ld_h8(&Kx[1][ta][d]);
+                const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
+                acc = mfma16x16x32(ah, bh, acc);
+                acc = mfma16x16x32(ah, bl, acc);
+                acc = mfma16x16x32(al, bh, acc);
+            }
+            store_tile(false, mt, nt_, acc);
         }
     }
     // upper tiles of the Q K^T block are zero (16-byte stores)
