@@ -151,6 +151,15 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             h8 ah[4], al[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) split_hi_lo(qv[b][2 * ks], qv[b][2 * ks + 1], ah[ks], al[ks]);
+            // e^G q of these rows (token-major f16) straight from the registers
+            {
+                const int t = 16 * mt + li;
+                const float e = t < L ? expf(sG[t]) : 0.f;
+                u4* QG = (u4*)(rec + OFF_QG);
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+                    QG[t * (SD / 8) + 4 * ks + g] = __builtin_bit_cast(u4, to_h8(qv[b][2 * ks] * e, qv[b][2 * ks + 1] * e));
+            }
             for (int nt_ = 0; nt_ <= mt; ++nt_) {
                 f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -192,20 +201,10 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             if ((s8 >> 4) > (t >> 4)) aqk[idx] = u4{0u, 0u, 0u, 0u};
         }
     }
-    // ---- e^G q (token-major, from global) and e^{G_last - G} k (dim-major), 8 halves per store
+    // ---- e^{G_last - G} k (dim-major), 8 halves per store (e^G q went out with the Q K^T tiles)
     {
-        u4* QG = (u4*)(rec + OFF_QG);
         u4* KT = (u4*)(rec + OFF_KT);
         const float glast = sG[C - 1];
-#pragma unroll
-        for (int it = 0; it < C * SD / 8 / PREP_THREADS; ++it) {
-            const int idx = tid + it * PREP_THREADS;
-            const int t = idx >> 4, d8 = 8 * (idx & 15);
-            const float* qr = qrow(t) + d8;
-            const float e = t < L ? expf(sG[t]) : 0.f;
-            const f4 q0 = ld_f4(qr) * e, q1 = ld_f4(qr + 4) * e;
-            QG[idx] = __builtin_bit_cast(u4, to_h8(q0, q1));
-        }
         for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
             const int d = idx >> 3, t8 = 8 * (idx & 7);
             h8 r;
