@@ -84,6 +84,13 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     // q row of this lane in the Q K^T and e^G q products (global; rows past the prompt masked)
     auto qrow = [&](int t) { return co + (size_t)(t0 + min(t, L - 1)) * cts + kh * SD; };
 
+    // the gate inputs go out first (wave 7 computes beta and the cumulative log-decay below)
+    float braw = 0.f, araw = 0.f;
+    if (w == 7) {
+        const int tl = t0 + min(l, L - 1);
+        braw = br[(size_t)tl * bts + h];
+        araw = ar[(size_t)tl * bts + h];
+    }
     // ---- K rows (zero past the prompt) as hi/lo, beta and the cumulative log-decay; unconditional
     // loads (clamped row, then masked) so no branch separates them from their use
 #pragma unroll
@@ -97,11 +104,30 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         split_hi_lo(k0, k1, hi, lo);
         *(h8*)&Kx[0][t][d8] = hi; *(h8*)&Kx[1][t][d8] = lo;
     }
-    if (w == 0) {
+    // q rows of the Q K^T waves (below), issued after the K rows so the K staging never waits for
+    // them, and their round trip overlaps the staging and the gates
+    const int nb = w == 2 ? 2 : 1;                  // row blocks of waves 0-2
+    const int mb0 = w == 0 ? 3 : w == 1 ? 2 : 1;    // first row block; wave 2 then does block 0
+    f4 qv[2][8];
+    if (w < 3) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b >= nb) break;   // uniform
+            const int ta = 16 * (mb0 - b) + li;
+            const float* qr = qrow(ta);
+            const float qm = ta < L ? 1.f : 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                qv[b][2 * ks] = ld_f4(qr + 32 * ks + 8 * g) * qm;
+                qv[b][2 * ks + 1] = ld_f4(qr + 32 * ks + 8 * g + 4) * qm;
+            }
+        }
+    }
+    if (w == 7) {   // a wave without q loads in flight
         float gg = 0.f, b = 0.f;
         if (l < L) {
-            b = sigmoidf_(br[(size_t)(t0 + l) * bts + h]);
-            gg = softplusf_(ar[(size_t)(t0 + l) * bts + h] + dt[h]) * A[h];
+            b = sigmoidf_(braw);
+            gg = softplusf_(araw + dt[h]) * A[h];
         }
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -129,21 +155,6 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         }
     };
     if (w < 3) {
-        const int nb = w == 2 ? 2 : 1;                  // row blocks of this wave
-        const int mb0 = w == 0 ? 3 : w == 1 ? 2 : 1;    // first row block; wave 2 then does block 0
-        f4 qv[2][8];
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            if (b >= nb) break;   // uniform
-            const int ta = 16 * (mb0 - b) + li;
-            const float* qr = qrow(ta);
-            const float qm = ta < L ? 1.f : 0.f;
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                qv[b][2 * ks] = ld_f4(qr + 32 * ks + 8 * g) * qm;
-                qv[b][2 * ks + 1] = ld_f4(qr + 32 * ks + 8 * g + 4) * qm;
-            }
-        }
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             if (b >= nb) break;   // uniform
