@@ -138,6 +138,44 @@ def test_decode_fused_equals_two_kernels(dev, nt, nv, nk, K):
     np.testing.assert_array_equal(host(cs_out), host(cs))
 
 
+@pytest.mark.parametrize("nt,K", [(40, 4), (19, 3)])
+def test_conv_l2norm_prompt_equals_token_calls(dev, nt, K):
+    """One call over a prompt (the 16-byte, multi-run form) equals nt one-token calls with the conv
+    state carried between them (the decode form); the norms' sums differ in order only."""
+    announce(f"conv prompt vs tokens nt={nt} K={K}")
+    d = gdn_inputs(12, nt=nt, nv=8, nk=4)
+    x, w = dev_f32(d["x"], dev), dev_f32(d["w"][:, :K], dev)
+    st_a, st_b = dev_f32(d["conv_state"][:K - 1], dev), dev_f32(d["conv_state"][:K - 1], dev)
+    whole = host(ops.gdn_conv_l2norm(x, w, st_a, 8))
+    steps = np.concatenate([host(ops.gdn_conv_l2norm(x[t:t + 1].contiguous(), w, st_b, 8)) for t in range(nt)])
+    assert np.abs(whole - steps).max() <= 1e-6
+    np.testing.assert_array_equal(host(st_a), host(st_b))
+
+
+def test_prefill_equals_fused_decode_steps(dev):
+    """GDN prefill over a prompt (conv + L2 in one pass, then the chunk-64 scan) equals the same
+    tokens fed one at a time through the one-launch decode layer (conv state alternating between
+    two buffers): outputs, final recurrent state and final conv state."""
+    nt, nv, nk, S = 70, 8, 4, 128
+    d = gdn_inputs(13, nt=nt, nv=nv, nk=nk)
+    x, w = dev_f32(d["x"], dev), dev_f32(d["w"], dev)
+    br, ar = dev_f32(d["beta_raw"], dev), dev_f32(d["alpha_raw"], dev)
+    dt, a = dev_f32(d["dt"], dev), dev_f32(d["a"], dev)
+    cs, st = dev_f32(d["conv_state"], dev), dev_f32(d["state"], dev)
+    co = ops.gdn_conv_l2norm(x, w, cs, 2 * nk)
+    pre = host(ops.gdn_step(co, br, ar, dt, a, st, nv, nk, chunked=True))
+    cbuf = [dev_f32(d["conv_state"], dev), torch.empty_like(cs)]
+    st2 = dev_f32(d["state"], dev)
+    outs = []
+    for t in range(nt):
+        outs.append(host(ops.gdn_decode_fused(x[t:t + 1].contiguous(), w, cbuf[t & 1], cbuf[(t + 1) & 1],
+                                              br[t:t + 1].contiguous(), ar[t:t + 1].contiguous(), dt, a, st2, nv, nk)))
+    dec = np.concatenate(outs)
+    assert np.abs(pre - dec).max() <= OUT_TOL
+    assert np.abs(host(st) - host(st2)).max() <= STATE_TOL
+    np.testing.assert_array_equal(host(cs), host(cbuf[nt & 1]))
+
+
 def test_step_float64_truth(dev):
     d = gdn_step_inputs(4, 6, nv=4, nk=2)
     st = dev_f32(d["state"], dev)
