@@ -131,6 +131,18 @@ def test_flash_whole_prompt_8192(dev):
         assert np.abs(whole - chunked).max() <= TOL
 
 
+def test_decode_tokens_equal_single_pass(dev):
+    """Token-by-token decode (nt = 1 at every position, split-K with the library's splits) equals
+    one causal prefill pass over the same prompt (decode == single-pass causal)."""
+    T = 160
+    q, kb, vb = attn_inputs(5, ctx=T, nt=T)
+    qd = dev_f32(q.reshape(T, -1), dev)
+    kc, vc = dev_f16bits(kb, dev), dev_f16bits(vb, dev)
+    whole = host(ops.attn_f16(qd, kc, vc, 0, 16, 2, kernel=ops.KERNEL_FLASH))
+    toks = np.concatenate([host(ops.attn_f16(qd[t:t + 1].contiguous(), kc, vc, t, 16, 2)) for t in range(T)])
+    assert np.abs(whole - toks).max() <= TOL
+
+
 def test_kv_append_rne_bits(dev):
     rng = np.random.default_rng(0)
     k = (rng.standard_normal((5, 512)) * 3).astype(np.float32)
