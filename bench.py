@@ -245,7 +245,9 @@ def main():
         def whole():
             call("it_attn_f16", qp.data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, 0, HD, NH, NKV, T, scale,
                  outp.data_ptr(), NH * HD, scr.data_ptr(), scr.numel(), stream_of())
-        ms = graph_time_ms(torch, whole, reps=3)
+        # one call processes the whole prompt; four back-to-back calls per graph replay amortise the
+        # replay's own launch cost, as the decode figure does over its 400 layers
+        ms = graph_time_ms(torch, lambda: [whole() for _ in range(4)], reps=3) / 4
         res["prefill_8192_single_call_ms"] = round(ms, 3)
         res["prefill_8192_single_call_TFLOPs"] = round(f / (ms * 1e-3) / 1e12, 2)
         prefill_tflops = max(res["prefill_8192_single_call_TFLOPs"], res["prefill_8192_as_128_chunks_TFLOPs"])
