@@ -396,13 +396,21 @@ def main():
         ms = graph_time_ms(torch, lambda: [gdn_verify(i) for i in range(K)], reps=3)
         res["gdn_verify_nt2_layer_us"] = round(ms * 1000 / K, 3)
 
+        def gdn_verify_fused(i):
+            call("it_gdn_decode_fused_ckpt", x2.data_ptr(), d["cd"], w.data_ptr(), 4, cst2[i & 1].data_ptr(),
+                 cst2[(i + 1) & 1].data_ptr(), br2.data_ptr(), ar2.data_ptr(), nv, dtv.data_ptr(), av.data_ptr(),
+                 states[i % NST].data_ptr(), og2.data_ptr(), nv * S, 2, nv, nk, S, 1e-6, ck_ssm.data_ptr(),
+                 ck_conv.data_ptr(), 0, stream_of())
+        ms = graph_time_ms(torch, lambda: [gdn_verify_fused(i) for i in range(K)], reps=3)
+        res["gdn_verify_nt2_layer_fused_us"] = round(ms * 1000 / K, 3)
+
         def gdn_reject(i):
             call("it_gdn_rollback", ck_conv.data_ptr(), cst.data_ptr(), cst.numel(), ck_ssm.data_ptr(),
                  states[i % NST].data_ptr(), ck_ssm.numel(), stream_of())
         ms = graph_time_ms(torch, lambda: [gdn_reject(i) for i in range(K)], reps=3)
         res["gdn_rollback_us"] = round(ms * 1000 / K, 3)
         log(f"gdn verify nt=2 layer (with checkpoints) {res['gdn_verify_nt2_layer_us']} us, "
-            f"rollback {res['gdn_rollback_us']} us")
+            f"in one launch {res['gdn_verify_nt2_layer_fused_us']} us, rollback {res['gdn_rollback_us']} us")
         del states
 
         # ------------------------------------------------------------------ GDN chunked prefill (config 5)

@@ -199,6 +199,18 @@ int it_gdn_decode_fused(const float* x, int x_tok_stride, const float* w, int K,
                         const float* dt, const float* a, float* state, float* out, int out_tok_stride, int nt,
                         int nv, int nk, int S, float eps, void* stream);
 
+/* it_gdn_decode_fused for an MTP verify batch, plus the checkpoints of both states after token
+ * ck_after (0 <= ck_after < nt), written from registers: ck_state [nv][S][S] (the recurrent state,
+ * as it_gdn_step_ckpt) and ck_conv [(K-1)][cd] (the conv state, as it_gdn_conv_l2norm_ckpt). Neither
+ * may overlap the state it snapshots or the other buffers.
+ * Replaces the verify loop's conv / rmsnorm / gdn dispatches and checkpoint copies,
+ * src/vk/mod.rs:790-806 (mtp.rs:227-234). */
+int it_gdn_decode_fused_ckpt(const float* x, int x_tok_stride, const float* w, int K, const float* conv_state_in,
+                             float* conv_state_out, const float* beta_raw, const float* alpha_raw,
+                             int ba_tok_stride, const float* dt, const float* a, float* state, float* out,
+                             int out_tok_stride, int nt, int nv, int nk, int S, float eps, float* ck_state,
+                             float* ck_conv, int ck_after, void* stream);
+
 /* The GDN output's gated RMSNorm, per (token t, V head h) row of S = 128:
  *   out[t*out_tok_stride + h*S + j] = o_j / sqrt(mean_j(o^2) + eps) * w[j] * silu(z[t*z_tok_stride + h*S + j])
  * with o the row o[t*o_tok_stride + h*S ...] and w [S] (ssm_norm, shared by the heads). out may be

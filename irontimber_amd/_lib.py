@@ -37,6 +37,8 @@ SIGNATURES = {
     "it_gdn_step": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "it_gdn_decode_fused": (c_int, [P, c_int, P, c_int, P, P, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                     c_float, P]),
+    "it_gdn_decode_fused_ckpt": (c_int, [P, c_int, P, c_int, P, P, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int,
+                                         c_int, c_float, P, P, c_int, P]),
     "it_gdn_conv_ckpt": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P, c_int, P]),
     "it_gdn_conv_l2norm_ckpt": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P]),
     "it_gdn_step_ckpt": (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_int, P]),

@@ -339,10 +339,10 @@ int it_gdn_step(const float* co, int cts, const float* br, const float* ar, int 
                  "it_gdn_step");
 }
 
-int it_gdn_decode_fused(const float* x, int xts, const float* w, int K, const float* cst_in, float* cst_out,
-                        const float* br, const float* ar, int bts, const float* dt, const float* a, float* state,
-                        float* out, int ots, int nt, int nv, int nk, int S, float eps, void* stream) {
-    const char* who = "it_gdn_decode_fused";
+static int validate_decode_fused(const char* who, const float* x, int xts, const float* w, int K, const float* cst_in,
+                                 const float* cst_out, const float* br, const float* ar, int bts, const float* dt,
+                                 const float* a, const float* state, const float* out, int ots, int nt, int nv, int nk,
+                                 int S) {
     if (S != 128) return fail("%s: state size %d unsupported (128)", who, S);
     if (nv <= 0 || nk <= 0 || nv % nk != 0) return fail("%s: nv %d / nk %d invalid", who, nv, nk);
     if (nt < 1 || nt > 4) return fail("%s: nt %d outside 1..4 (longer runs: it_gdn_conv_l2norm + it_gdn_step)", who, nt);
@@ -357,8 +357,34 @@ int it_gdn_decode_fused(const float* x, int xts, const float* w, int K, const fl
     const size_t cbytes = (size_t)(K - 1) * cd * sizeof(float);
     const char *pi = (const char*)cst_in, *po = (const char*)cst_out;
     if (pi < po + cbytes && po < pi + cbytes) return fail("%s: conv_state_out overlaps conv_state_in", who);
+    return 0;
+}
+
+int it_gdn_decode_fused(const float* x, int xts, const float* w, int K, const float* cst_in, float* cst_out,
+                        const float* br, const float* ar, int bts, const float* dt, const float* a, float* state,
+                        float* out, int ots, int nt, int nv, int nk, int S, float eps, void* stream) {
+    const char* who = "it_gdn_decode_fused";
+    if (validate_decode_fused(who, x, xts, w, K, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, S))
+        return -1;
     return check(it::launch_gdn_decode_fused(x, xts, w, K, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv,
-                                             nk, eps, (hipStream_t)stream),
+                                             nk, eps, nullptr, nullptr, -1, (hipStream_t)stream),
+                 who);
+}
+
+int it_gdn_decode_fused_ckpt(const float* x, int xts, const float* w, int K, const float* cst_in, float* cst_out,
+                             const float* br, const float* ar, int bts, const float* dt, const float* a, float* state,
+                             float* out, int ots, int nt, int nv, int nk, int S, float eps, float* ck_state,
+                             float* ck_conv, int ck_after, void* stream) {
+    const char* who = "it_gdn_decode_fused_ckpt";
+    if (validate_decode_fused(who, x, xts, w, K, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, S))
+        return -1;
+    if (validate_ckpt(who, ck_state, state, (size_t)nv * S * S, ck_after, nt)) return -1;
+    const size_t cwords = (size_t)(K - 1) * (2 * nk + nv) * S;
+    if (validate_ckpt(who, ck_conv, cst_in, cwords, ck_after, nt)) return -1;
+    if (ck_conv < cst_out + cwords && cst_out < ck_conv + cwords) return fail("%s: conv checkpoint overlaps the conv state", who);
+    if (!aligned16(ck_state) || !aligned16(ck_conv)) return fail("%s: checkpoint buffers must be 16-byte aligned", who);
+    return check(it::launch_gdn_decode_fused(x, xts, w, K, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv,
+                                             nk, eps, ck_state, ck_conv, ck_after, (hipStream_t)stream),
                  who);
 }
 

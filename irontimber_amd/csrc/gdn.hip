@@ -324,7 +324,8 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     const float* __restrict__ x, int xts, const float* __restrict__ cw, const float* __restrict__ cst_in,
     float* __restrict__ cst_out, const float* __restrict__ br, const float* __restrict__ ar, int bts,
     const float* __restrict__ dt, const float* __restrict__ A, float* __restrict__ state, float* __restrict__ out,
-    int ots, int nt, int nv, int nk, float eps) {
+    int ots, int nt, int nv, int nk, float eps, float* __restrict__ ck_state, float* __restrict__ ck_conv,
+    int ck_after) {
     constexpr int S = 128;
     __shared__ f4 red1[4][4], red2[4][4];
     __shared__ f2 nrm[2][4];   // per wave: {sum q^2, sum k^2} of its 16 row pairs, per token parity
@@ -439,6 +440,26 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
             const f4 ot = (red2[0][cg] + red2[1][cg] + red2[2][cg] + red2[3][cg]) * scale;
             *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = ot;
         }
+        if (t == ck_after) {   // MTP verify checkpoint: both states after this token, from registers
+            if (ck_state) {
+                float* cb_ = ck_state + (size_t)h * S * S;
+                *(f4*)(cb_ + (size_t)i0 * S + j0) = s0;
+                *(f4*)(cb_ + (size_t)(i0 + 1) * S + j0) = s1;
+            }
+            if (ck_conv) {
+                if (cb == 0 && h == kh && cg == 0) {
+#pragma unroll
+                    for (int i = 0; i < K - 1; ++i) {
+                        *(f2*)(ck_conv + (size_t)i * cd + cq) = wnq[i];
+                        *(f2*)(ck_conv + (size_t)i * cd + ck) = wnk[i];
+                    }
+                }
+                if (rp == 0) {
+#pragma unroll
+                    for (int i = 0; i < K - 1; ++i) *(f4*)(ck_conv + (size_t)i * cd + cv) = wnv[i];
+                }
+            }
+        }
     }
     *(f4*)(sb + (size_t)i0 * S + j0) = s0;
     *(f4*)(sb + (size_t)(i0 + 1) * S + j0) = s1;
@@ -458,12 +479,12 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
 hipError_t launch_gdn_decode_fused(const float* x, int xts, const float* cw, int K, const float* cst_in, float* cst_out,
                                    const float* br, const float* ar, int bts, const float* dt, const float* a,
                                    float* state, float* out, int ots, int nt, int nv, int nk, float eps,
-                                   hipStream_t st) {
+                                   float* ck_state, float* ck_conv, int ck_after, hipStream_t st) {
     const dim3 grid(8, nv);
     switch (K) {
-        case 2: gdn_decode_fused_kernel<2><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps); break;
-        case 3: gdn_decode_fused_kernel<3><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps); break;
-        default: gdn_decode_fused_kernel<4><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps); break;
+        case 2: gdn_decode_fused_kernel<2><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after); break;
+        case 3: gdn_decode_fused_kernel<3><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after); break;
+        default: gdn_decode_fused_kernel<4><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after); break;
     }
     return hipGetLastError();
 }

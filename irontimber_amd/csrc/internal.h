@@ -40,7 +40,7 @@ hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps,
 hipError_t launch_gdn_decode_fused(const float* x, int xts, const float* cw, int K, const float* cst_in, float* cst_out,
                                    const float* br, const float* ar, int bts, const float* dt, const float* a,
                                    float* state, float* out, int ots, int nt, int nv, int nk, float eps,
-                                   hipStream_t st);
+                                   float* ck_state, float* ck_conv, int ck_after, hipStream_t st);
 hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                            const float* a, float* state, float* out, int ots, int nt, int nv, int nk, float* ck,
                            int ck_after, hipStream_t st);

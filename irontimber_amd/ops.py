@@ -206,11 +206,12 @@ def l2norm_heads(x: torch.Tensor, nheads: int, d: int, eps: float = 1e-6) -> tor
 
 
 def gdn_decode_fused(x, w, conv_state_in, conv_state_out, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int,
-                     eps: float = 1e-6, out=None):
+                     eps: float = 1e-6, out=None, ckpt_state=None, ckpt_conv=None, ckpt_after: int = 0):
     """One launch for a GDN decode layer (1 <= nt <= 4 tokens): gdn_conv_l2norm(x, w, ...) then
     gdn_step, with the conv state read from conv_state_in and the new one written to
     conv_state_out (a different buffer). x [nt, (2nk+nv)*128], state updated in place -> out
-    [nt, nv*128]."""
+    [nt, nv*128]. ckpt_state / ckpt_conv (optional, together): both states after token ckpt_after
+    (the MTP verify checkpoint)."""
     for t, n in ((x, "x"), (w, "w"), (conv_state_in, "conv_state_in"), (conv_state_out, "conv_state_out"),
                  (beta_raw, "beta_raw"), (alpha_raw, "alpha_raw"), (dt, "dt"), (a, "a"), (state, "state")):
         _need(t, torch.float32, n)
@@ -218,9 +219,15 @@ def gdn_decode_fused(x, w, conv_state_in, conv_state_out, beta_raw, alpha_raw, d
     S = state.shape[-1]
     if out is None:
         out = torch.empty(nt, nv * S, device=x.device, dtype=torch.float32)
-    call("it_gdn_decode_fused", x.data_ptr(), cd, w.data_ptr(), w.shape[1], conv_state_in.data_ptr(),
-         conv_state_out.data_ptr(), beta_raw.data_ptr(), alpha_raw.data_ptr(), beta_raw.shape[1], dt.data_ptr(),
-         a.data_ptr(), state.data_ptr(), out.data_ptr(), out.shape[1], nt, nv, nk, S, float(eps), _stream())
+    args = [x.data_ptr(), cd, w.data_ptr(), w.shape[1], conv_state_in.data_ptr(), conv_state_out.data_ptr(),
+            beta_raw.data_ptr(), alpha_raw.data_ptr(), beta_raw.shape[1], dt.data_ptr(), a.data_ptr(), state.data_ptr(),
+            out.data_ptr(), out.shape[1], nt, nv, nk, S, float(eps)]
+    if ckpt_state is None and ckpt_conv is None:
+        call("it_gdn_decode_fused", *args, _stream())
+    else:
+        _ckpt(ckpt_state, state)
+        _ckpt(ckpt_conv, conv_state_in)
+        call("it_gdn_decode_fused_ckpt", *args, ckpt_state.data_ptr(), ckpt_conv.data_ptr(), ckpt_after, _stream())
     return out
 
 

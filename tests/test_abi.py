@@ -97,6 +97,14 @@ def test_attn_rejects_bad_geometry_before_device_work():
     rc = lib.it_gdn_decode_fused(fake, 8192, fake, 4, st_in, st_out, fake, fake, 32, fake, fake, fake, fake, 4096, 1,
                                  32, 16, 128, 1e-6, None)
     assert rc != 0 and "overlaps" in _lib.last_error()
+    # checkpointed form: ck_after inside the batch, checkpoint buffers apart from the states
+    st_in2 = ctypes.c_void_p(1 << 24)
+    rc = lib.it_gdn_decode_fused_ckpt(fake, 8192, fake, 4, st_in2, st_out, fake, fake, 32, fake, fake, fake, fake, 4096,
+                                      2, 32, 16, 128, 1e-6, ctypes.c_void_p(1 << 28), ctypes.c_void_p(1 << 29), 2, None)
+    assert rc != 0 and "checkpoint token 2" in _lib.last_error()
+    rc = lib.it_gdn_decode_fused_ckpt(fake, 8192, fake, 4, st_in2, st_out, fake, fake, 32, fake, fake, fake, fake, 4096,
+                                      2, 32, 16, 128, 1e-6, ctypes.c_void_p(1 << 28), st_out, 0, None)
+    assert rc != 0 and "overlaps" in _lib.last_error()
 
 
 def test_scratch_bytes_policy():

@@ -138,6 +138,32 @@ def test_decode_fused_equals_two_kernels(dev, nt, nv, nk, K):
     np.testing.assert_array_equal(host(cs_out), host(cs))
 
 
+@pytest.mark.parametrize("nt,nv,nk,K,ck_after", [(2, 32, 16, 4, 0), (4, 8, 4, 3, 2), (3, 4, 2, 4, 2), (1, 8, 4, 4, 0)])
+def test_decode_fused_ckpt_equals_two_kernels(dev, nt, nv, nk, K, ck_after):
+    """The MTP verify layer in one launch equals it_gdn_conv_l2norm_ckpt + it_gdn_step_ckpt:
+    outputs and final states as in the plain form, the conv checkpoint bit for bit, the state
+    checkpoint within last-bit differences."""
+    announce(f"gdn fused ckpt nt={nt} nv={nv} nk={nk} K={K} ck_after={ck_after}")
+    d = gdn_inputs(37, nt=nt, nv=nv, nk=nk)
+    x, w = dev_f32(d["x"], dev), dev_f32(d["w"][:, :K], dev)
+    br, ar = dev_f32(d["beta_raw"], dev), dev_f32(d["alpha_raw"], dev)
+    dt, a = dev_f32(d["dt"], dev), dev_f32(d["a"], dev)
+    cs0 = d["conv_state"][:K - 1]
+    cs, st = dev_f32(cs0, dev), dev_f32(d["state"], dev)
+    ck_c, ck_s = torch.full_like(cs, float("nan")), torch.full_like(st, float("nan"))
+    co = ops.gdn_conv_l2norm(x, w, cs, 2 * nk, ckpt=ck_c, ckpt_after=ck_after)
+    want = host(ops.gdn_step(co, br, ar, dt, a, st, nv, nk, ckpt=ck_s, ckpt_after=ck_after))
+    cs_in, cs_out, st2 = dev_f32(cs0, dev), torch.full_like(cs, float("nan")), dev_f32(d["state"], dev)
+    ck_c2, ck_s2 = torch.full_like(cs, float("nan")), torch.full_like(st, float("nan"))
+    got = host(ops.gdn_decode_fused(x, w, cs_in, cs_out, br, ar, dt, a, st2, nv, nk, ckpt_state=ck_s2,
+                                    ckpt_conv=ck_c2, ckpt_after=ck_after))
+    assert np.abs(got - want).max() <= 1e-5
+    assert np.abs(host(st2) - host(st)).max() <= 1e-5
+    assert np.abs(host(ck_s2) - host(ck_s)).max() <= 1e-5
+    np.testing.assert_array_equal(host(cs_out), host(cs))
+    np.testing.assert_array_equal(host(ck_c2), host(ck_c))
+
+
 @pytest.mark.parametrize("nt,K", [(40, 4), (19, 3)])
 def test_conv_l2norm_prompt_equals_token_calls(dev, nt, K):
     """One call over a prompt (the 16-byte, multi-run form) equals nt one-token calls with the conv
