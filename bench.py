@@ -218,7 +218,15 @@ def main():
         del kcs, vcs, k5, v5
 
     # ------------------------------------------------------------------ prefill attention (config 3)
+    mfma_meas = None
     if args.only in ("all", "prefill"):
+        # the device's sustained f16 matrix-core rate (it_calib_mfma_f16: MFMA chains, no memory)
+        cw, ci = 2048, 2048
+        cout = torch.empty(cw * 256, device=dev)
+        ms = graph_time_ms(torch, lambda: call("it_calib_mfma_f16", cw, ci, cout.data_ptr(), stream_of()), reps=3)
+        mfma_meas = round(cw * 4 * 4 * ci * 32768 / (ms * 1e-3) / 1e12, 1)
+        res["mfma_f16_measured_TFLOPs"] = mfma_meas
+        log(f"mfma: sustained f16 32x32x16 rate {mfma_meas} TF/s")
         T = 8192
         qp_np, kbp, vbp = attn_inputs(2, ctx=T, nt=T)
         qp = torch.from_numpy(qp_np.reshape(T, -1)).to(dev)
@@ -519,7 +527,10 @@ def main():
                      "kernel": "attn_decode_kernel<1>", "kernel_us": rnd(part_us, 3),
                      "bytes_per_launch": dbytes},
         "roofline_prefill": {"bound": "mfma", "achieved": prefill_tflops, "peak": F16_MFMA_PEAK_TFLOPS,
-                             "unit": "TFLOP/s", "frac": rnd(None if prefill_tflops is None else prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4)},
+                             "unit": "TFLOP/s", "frac": rnd(None if prefill_tflops is None else prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4),
+                             "measured_peak": mfma_meas,
+                             "frac_of_measured": rnd(None if prefill_tflops is None or not mfma_meas
+                                                     else prefill_tflops / mfma_meas, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

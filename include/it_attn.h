@@ -285,6 +285,12 @@ int it_attention_chunk(uint32_t nt, uint32_t nh, uint32_t pos0, size_t room);
 int it_validate_geometry(int ctx_len, int head_dim, int n_head, int n_head_kv, int ssm_state,
                          int ssm_groups, int ssm_vheads, int ssm_inner, int conv_k);
 
+/* Measurement only, no counterpart in the reference: the device's sustained f16 matrix-core
+ * rate. wgs workgroups of 256 threads; each of their waves issues 4 * iters independent
+ * 32x32x16 f16 MFMAs (32768 flops each) and touches no memory besides one float per thread
+ * written to out (wgs * 256 floats). Rate = wgs * 4 * 4 * iters * 32768 / elapsed time. */
+int it_calib_mfma_f16(int wgs, int iters, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

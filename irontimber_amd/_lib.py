@@ -24,6 +24,7 @@ SIGNATURES = {
     "it_attn_f32kv": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P, c_size_t,
                               P]),
     "it_attn_scratch_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "it_calib_mfma_f16": (c_int, [c_int, c_int, P, P]),
     "it_attn_f16": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P, c_size_t, P]),
     "it_attn_scratch_bytes_ex": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "it_attn_f16_ex": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P, c_size_t,

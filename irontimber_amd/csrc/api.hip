@@ -496,3 +496,8 @@ int it_validate_geometry(int ctx_len, int head_dim, int n_head, int n_head_kv, i
 }
 
 }  // extern "C"
+
+int it_calib_mfma_f16(int wgs, int iters, float* out, void* stream) {
+    if (wgs < 1 || iters < 1 || !out) return fail("it_calib_mfma_f16: wgs %d / iters %d / out invalid", wgs, iters);
+    return check(it::launch_mfma_peak(wgs, iters, out, (hipStream_t)stream), "it_calib_mfma_f16");
+}

@@ -55,4 +55,8 @@ hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const f
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
                               hipStream_t st);
 
+// f16 matrix-core rate probe: wgs workgroups of 4 waves, each wave 4 x iters 32x32x16 MFMAs;
+// out receives wgs * 256 floats.
+hipError_t launch_mfma_peak(int wgs, int iters, float* out, hipStream_t st);
+
 }  // namespace it
