@@ -256,7 +256,8 @@ int it_gdn_step_ckpt(const float* co, int co_tok_stride, const float* beta_raw, 
                      void* stream);
 
 /* Rollback after a rejected draft: conv_state <- ck_conv (conv_words floats) and ssm <- ck_ssm
- * (ssm_words floats), two device copies on the stream (either count may be 0). */
+ * (ssm_words floats), both in one copy kernel on the stream (either count may be 0; no buffer may
+ * overlap another). */
 int it_gdn_rollback(const float* ck_conv, float* conv_state, size_t conv_words, const float* ck_ssm, float* ssm,
                     size_t ssm_words, void* stream);
 

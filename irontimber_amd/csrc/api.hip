@@ -438,15 +438,9 @@ int it_gdn_rollback(const float* ck_conv, float* conv_state, size_t conv_words, 
                     size_t ssm_words, void* stream) {
     if ((conv_words && (!ck_conv || !conv_state)) || (ssm_words && (!ck_ssm || !ssm)))
         return fail("it_gdn_rollback: null buffer");
-    hipStream_t st = (hipStream_t)stream;
-    if (conv_words) {
-        const hipError_t e = hipMemcpyAsync(conv_state, ck_conv, conv_words * sizeof(float), hipMemcpyDeviceToDevice, st);
-        if (e != hipSuccess) return check(e, "it_gdn_rollback");
-    }
-    if (ssm_words) return check(hipMemcpyAsync(ssm, ck_ssm, ssm_words * sizeof(float), hipMemcpyDeviceToDevice, st),
-                                "it_gdn_rollback");
-    g_err.clear();
-    return 0;
+    if (!conv_words && !ssm_words) { g_err.clear(); return 0; }
+    return check(it::launch_gdn_rollback(ck_conv, conv_state, conv_words, ck_ssm, ssm, ssm_words, (hipStream_t)stream),
+                 "it_gdn_rollback");
 }
 
 size_t it_gdn_chunked_scratch_bytes(int nt, int nv, int S) {

@@ -256,6 +256,18 @@ __device__ __forceinline__ float sum_lanes_stride4(float v) {
     return sum_xor32(a + b);
 }
 
+// Workgroup id -> (16-column block cb, V head h) of the 8 x nv step grid, launched 1-D.
+// Workgroups go to the 8 XCDs round-robin by id, each XCD with its own L2; the two column blocks
+// that share every 128-byte state line get ids 8 apart (the same XCD), so each line is fetched
+// from HBM once instead of once per block. Needs nv even; odd nv keeps the plain order.
+__device__ __forceinline__ void step_wg(int id, int nv, int& cb, int& h) {
+    if (nv & 1) { cb = id & 7; h = id >> 3; return; }
+    const int xcd = id & 7, slot = id >> 3;
+    const int u = ((slot >> 1) << 3) | xcd;   // (head, column-block pair)
+    h = u >> 2;
+    cb = 2 * (u & 3) + (slot & 1);
+}
+
 __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__ co, int cts, const float* __restrict__ br,
                                                        const float* __restrict__ ar, int bts, const float* __restrict__ dt,
                                                        const float* __restrict__ A, float* __restrict__ state,
@@ -263,7 +275,9 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
                                                        float* __restrict__ ck, int ck_after) {
     constexpr int S = 128;
     __shared__ f4 red1[4][4], red2[4][4];
-    const int cb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    int cb, h;
+    step_wg(blockIdx.x, nv, cb, h);
     const int cg = tid & 3, rp = tid >> 2;
     const int kh = h % nk, qk = nk * S;
     const int j0 = cb * 16 + 4 * cg, i0 = 2 * rp;
@@ -329,7 +343,9 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     constexpr int S = 128;
     __shared__ f4 red1[4][4], red2[4][4];
     __shared__ f2 nrm[2][4];   // per wave: {sum q^2, sum k^2} of its 16 row pairs, per token parity
-    const int cb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    int cb, h;
+    step_wg(blockIdx.x, nv, cb, h);
     const int cg = tid & 3, rp = tid >> 2;
     const int kh = h % nk, qk = nk * S, cd = (2 * nk + nv) * S;
     const int j0 = cb * 16 + 4 * cg, i0 = 2 * rp;
@@ -480,7 +496,7 @@ hipError_t launch_gdn_decode_fused(const float* x, int xts, const float* cw, int
                                    const float* br, const float* ar, int bts, const float* dt, const float* a,
                                    float* state, float* out, int ots, int nt, int nv, int nk, float eps,
                                    float* ck_state, float* ck_conv, int ck_after, hipStream_t st) {
-    const dim3 grid(8, nv);
+    const dim3 grid(8 * nv);
     switch (K) {
         case 2: gdn_decode_fused_kernel<2><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after); break;
         case 3: gdn_decode_fused_kernel<3><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after); break;
@@ -651,7 +667,7 @@ hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps,
 hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                            const float* a, float* state, float* out, int ots, int nt, int nv, int nk, float* ck,
                            int ck_after, hipStream_t st) {
-    gdn_step_kernel<<<dim3(8, nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, ck, ck_after);
+    gdn_step_kernel<<<dim3(8 * nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, ck, ck_after);
     return hipGetLastError();
 }
 
@@ -668,6 +684,38 @@ hipError_t launch_gdn_gated_norm(const float* o, int ots, const float* z, int zt
                                  float* out, int outs, int nv, int nt, hipStream_t st) {
     const long rows = (long)nv * nt;
     gdn_gated_norm_kernel<<<dim3((unsigned)((rows + 3) / 4)), 256, 0, st>>>(o, ots, z, zts, w, eps, out, outs, nv, nt);
+    return hipGetLastError();
+}
+
+// Rollback of both checkpointed states in one launch (two device copies would be two dispatches):
+// element e < na of the combined range copies a, the rest b. vec: all four pointers 16-byte
+// aligned and the counts multiples of 4, so whole f4s move; otherwise floats.
+__global__ __launch_bounds__(256) void gdn_rollback_kernel(const float* __restrict__ as, float* __restrict__ ad,
+                                                           size_t na, const float* __restrict__ bs,
+                                                           float* __restrict__ bd, size_t nb, int vec) {
+    const size_t stride = (size_t)gridDim.x * 256;
+    if (vec) {
+        const size_t na4 = na / 4, n4 = na4 + nb / 4;
+        for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n4; e += stride) {
+            if (e < na4) ((f4*)ad)[e] = ((const f4*)as)[e];
+            else ((f4*)bd)[e - na4] = ((const f4*)bs)[e - na4];
+        }
+        return;
+    }
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < na + nb; e += stride) {
+        if (e < na) ad[e] = as[e];
+        else bd[e - na] = bs[e - na];
+    }
+}
+
+hipError_t launch_gdn_rollback(const float* ck_conv, float* conv, size_t nc, const float* ck_ssm, float* ssm,
+                               size_t ns, hipStream_t st) {
+    auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    const int vec = (!nc || (al(ck_conv) && al(conv) && nc % 4 == 0)) && (!ns || (al(ck_ssm) && al(ssm) && ns % 4 == 0));
+    const size_t units = vec ? (nc + ns) / 4 : nc + ns;
+    const size_t wgs = std::min<size_t>((units + 511) / 512, 2048);   // ~2 units per thread
+    if (!wgs) return hipSuccess;
+    gdn_rollback_kernel<<<(unsigned)wgs, 256, 0, st>>>(ck_conv, conv, nc, ck_ssm, ssm, ns, vec);
     return hipGetLastError();
 }
 

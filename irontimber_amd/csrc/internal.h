@@ -59,4 +59,8 @@ hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const f
 // out receives wgs * 256 floats.
 hipError_t launch_mfma_peak(int wgs, int iters, float* out, hipStream_t st);
 
+// conv <- ck_conv (nc floats) and ssm <- ck_ssm (ns floats) in one launch.
+hipError_t launch_gdn_rollback(const float* ck_conv, float* conv, size_t nc, const float* ck_ssm, float* ssm,
+                               size_t ns, hipStream_t st);
+
 }  // namespace it

@@ -116,3 +116,21 @@ def test_checkpoint_validation(dev):
         ops.gdn_step(co, br, ar, dt, a, st, 4, 2, ckpt=torch.empty_like(st), ckpt_after=2)
     with pytest.raises(ItError, match="overlaps"):
         ops.gdn_step(co, br, ar, dt, a, st, 4, 2, ckpt=st, ckpt_after=0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nc,ns,offs", [(24576, 524288, 0), (3 * 8192, 0, 0), (0, 4096, 0), (1001, 777, 1), (5, 4099, 0)])
+def test_rollback_copies(dev, nc, ns, offs):
+    """it_gdn_rollback's one copy kernel: both ranges restored exactly and nothing past them touched,
+    with whole-f4 moves (aligned, multiples of 4) and the float path (odd counts, unaligned)."""
+    announce(f"rollback nc={nc} ns={ns} offs={offs}")
+    g = torch.Generator().manual_seed(nc * 7 + ns)
+    ckc = torch.randn(nc + offs + 8, generator=g).to(dev)
+    cks = torch.randn(ns + offs + 8, generator=g).to(dev)
+    cst = torch.full((nc + offs + 8,), 7.0, device=dev)
+    sst = torch.full((ns + offs + 8,), 7.0, device=dev)
+    ops.gdn_rollback(ckc[offs:offs + nc], cst[offs:offs + nc], cks[offs:offs + ns], sst[offs:offs + ns])
+    torch.cuda.synchronize()
+    assert torch.equal(cst[offs:offs + nc], ckc[offs:offs + nc]) and torch.equal(sst[offs:offs + ns], cks[offs:offs + ns])
+    assert bool((cst[:offs] == 7).all()) and bool((cst[offs + nc:] == 7).all())
+    assert bool((sst[:offs] == 7).all()) and bool((sst[offs + ns:] == 7).all())
