@@ -63,10 +63,27 @@ __device__ __forceinline__ void split_hi_lo4(f4 x, h4& hi, h4& lo) {
 constexpr int PREP_THREADS = 512;
 constexpr int KP = SD + 16;    // f16 row pitch of the K tile (288 B, 32-byte multiple)
 
+// Workgroup id -> (chunk c, V head h) of the prep grid, launched 1-D. The nv / nk V heads that
+// share a QK head read the same q and k rows; they get ids 8 apart (one XCD, under the
+// round-robin XCD dispatch) and are resident together, so those rows come from HBM once into that
+// XCD's L2 instead of once per V head.
+__device__ __forceinline__ void prep_wg(int id, int nch, int nv, int nk, int& c, int& h) {
+    const int r = nv / nk;
+    if (r > 1 && (nch * nk) % 8 == 0) {
+        const int xcd = id & 7, slot = id >> 3;
+        const int u = (slot / r) * 8 + xcd;   // (chunk, QK head)
+        c = u % nch;
+        h = u / nch + (slot % r) * nk;
+    } else {
+        c = id % nch;
+        h = id / nch;
+    }
+}
+
 __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void gdn_chunk_prep(const float* __restrict__ co, int cts,
                                                                const float* __restrict__ br, const float* __restrict__ ar,
                                                                int bts, const float* __restrict__ dt,
-                                                               const float* __restrict__ A, int nt, int nk,
+                                                               const float* __restrict__ A, int nt, int nv, int nk,
                                                                char* __restrict__ scr) {
     __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows hi / lo, then the V rows (f32)
     __shared__ __align__(16) float Ap[C][C + 4];
@@ -74,7 +91,9 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
     static_assert(2 * C * KP * 2 >= C * SD * 4, "the V rows fit in the K tile");
 
-    const int c = blockIdx.x, h = blockIdx.y, nch = gridDim.x;
+    const int nch = (nt + C - 1) / C;
+    int c, h;
+    prep_wg(blockIdx.x, nch, nv, nk, c, h);
     const int t0 = c * C, L = min(C, nt - t0);
     const int kh = h % nk, qk = nk * SD;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
@@ -568,7 +587,7 @@ hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const f
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
                               hipStream_t st) {
     const int nch = (nt + C - 1) / C;
-    gdn_chunk_prep<<<dim3(nch, nv), PREP_THREADS, 0, st>>>(co, cts, br, ar, bts, dt, a, nt, nk, (char*)scratch);
+    gdn_chunk_prep<<<dim3(nch * nv), PREP_THREADS, 0, st>>>(co, cts, br, ar, bts, dt, a, nt, nv, nk, (char*)scratch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // linear grid of 8 * NCB * ceil(nv / 8) workgroups, mapped to (head, column block) in-kernel
