@@ -23,7 +23,8 @@
 //   records: stored straight from the accumulators (no staging, no barrier).
 // Per tile that is two barriers. First tile: q and K go out first, the q planes are built while K
 // is in flight, then V goes out and the scores and softmax run while it lands; later tiles are
-// prefetched while P.V runs.
+// prefetched while P.V runs. MULTI = false (splits of one tile) declares a single V buffer, which
+// lets two or three workgroups share a CU.
 #include "common.h"
 #include "internal.h"
 
@@ -78,14 +79,14 @@ template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
 
 }  // namespace
 
-template <int NB>
+template <int NB, bool MULTI>
 __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc,
                                                const uint16_t* __restrict__ vc, int kvd, int pos0, int nh, int nkv,
                                                int nt, float scale, float* __restrict__ part, int chunk, int smax,
                                                int s, int kh, int rg) {
     constexpr int ROWS = 8 * NB;
     __shared__ __align__(16) _Float16 V0[TK * HD];
-    __shared__ __align__(16) _Float16 V1[TK * HD];
+    __shared__ __align__(16) _Float16 V1[MULTI ? TK * HD : 8];   // only when a split has several tiles
     __shared__ __align__(16) _Float16 Qs[2][ROWS][QST];   // [hi|lo][row][dim]
     __shared__ __align__(16) _Float16 Ps[NB][16][PST];    // rows 0-7 P_hi, 8-15 P_lo of a row block
     __shared__ float Mx[4][ROWS];                          // per-wave tile maxima
@@ -169,7 +170,7 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
 
     int it = 0;
     for (int kb = p0; kb < pend; kb += TK, ++it) {
-        const _Float16* Vt = (it & 1) ? V1 : V0;
+        const _Float16* Vt = (MULTI && (it & 1)) ? V1 : V0;
         // ---- scores S^T (rows = this wave's 16 keys, columns = q hi/lo rows)
         f4 sacc[NB];
 #pragma unroll
@@ -223,7 +224,7 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
         __syncthreads();    // B: P planes, alpha, V tile
         // prefetch the next tile (K registers are free, the other V buffer was last read two
         // barriers ago)
-        if (kb + TK < pend) {
+        if (MULTI && kb + TK < pend) {
             k_tile_to_regs(kc, kvd, head_off, kb + TK, pend, kr, w, l);
             v_tile_to_lds(vc, kvd, head_off, kb + TK, pend, (it & 1) ? V0 : V1, w, l);
         }
@@ -281,13 +282,13 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
     }
 }
 
-template <int NB>
+template <int NB, bool MULTI>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, int qts,
                                                           const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, int kvd, int pos0, int nh,
                                                           int nkv, int nt, float scale, float* __restrict__ part,
                                                           int chunk, int smax) {
-    decode_partial<NB>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax, blockIdx.x, blockIdx.y,
+    decode_partial<NB, MULTI>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax, blockIdx.x, blockIdx.y,
                        blockIdx.z);
 }
 
@@ -462,14 +463,26 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
                                        hipStream_t st) {
     const int G = nh / nkv, R = nt * G;
     const int smax = (pos0 + nt + chunk - 1) / chunk;
-    const int rows = R <= 8 ? 8 : R <= 16 ? 16 : R <= 24 ? 24 : 32;
+    // one tile per split (chunk <= 64 keys) needs one V buffer, so two or three workgroups share a
+    // CU; verify rows are then spread over more workgroups (8 rows each up to 16 rows, 16 rows up to
+    // 32: measured best at nt = 2 and nt = 4), with the K/V tile of a split read by each of them
+    // from the same XCD's L2 when smax * nkv (the id distance of a split's row groups) is a
+    // multiple of 8. Splits of several tiles keep the smallest block that holds all rows.
+    const bool multi = chunk > TK;
+    const int rows = multi ? (R <= 8 ? 8 : R <= 16 ? 16 : R <= 24 ? 24 : 32) : (R <= 16 ? 8 : R <= 32 ? 16 : 32);
     const dim3 grid(smax, nkv, (R + rows - 1) / rows);
+#define IT_DECODE_LAUNCH(NB_)                                                                                         \
+    (multi ? attn_decode_kernel<NB_, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, \
+                                                                chunk, smax)                                        \
+           : attn_decode_kernel<NB_, false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, \
+                                                                 chunk, smax))
     switch (rows / 8) {
-        case 1: attn_decode_kernel<1><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax); break;
-        case 2: attn_decode_kernel<2><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax); break;
-        case 3: attn_decode_kernel<3><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax); break;
-        default: attn_decode_kernel<4><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax); break;
+        case 1: IT_DECODE_LAUNCH(1); break;
+        case 2: IT_DECODE_LAUNCH(2); break;
+        case 3: IT_DECODE_LAUNCH(3); break;
+        default: IT_DECODE_LAUNCH(4); break;
     }
+#undef IT_DECODE_LAUNCH
     return hipGetLastError();
 }
 
