@@ -524,7 +524,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": rnd(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": rnd(None if part_gbs is None else part_gbs / HBM_PEAK_GBS, 4),
                      "traffic": DECODE_TRAFFIC_BYTES, "traffic_unit": "bytes per launch",
-                     "kernel": "attn_decode_kernel<1>", "kernel_us": rnd(part_us, 3),
+                     "kernel": "attn_decode_kernel<1, false>", "kernel_us": rnd(part_us, 3),
                      "bytes_per_launch": dbytes},
         "roofline_prefill": {"bound": "mfma", "achieved": prefill_tflops, "peak": F16_MFMA_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": rnd(None if prefill_tflops is None else prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4),

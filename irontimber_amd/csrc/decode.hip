@@ -385,8 +385,20 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __r
                                                                 int nh, int nt, const float* __restrict__ part,
                                                                 int chunk, int smax, float* __restrict__ out,
                                                                 int ots) {
-    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
-    const int th = wid >> 4, d0 = 16 * (wid & 15);
+    // workgroup = 4 waves = 64 dims of one row; the 4 workgroups of a row read the same record
+    // lines, so they get ids 8 apart (one XCD under the round-robin dispatch) when the row count
+    // allows it, and each line comes from HBM into that XCD's L2 once
+    int row, quarter;
+    if ((nt * nh) % 8 == 0) {
+        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+        row = ((slot >> 2) << 3) | xcd;
+        quarter = slot & 3;
+    } else {
+        row = blockIdx.x >> 2;
+        quarter = blockIdx.x & 3;
+    }
+    const int l = threadIdx.x & 63;
+    const int th = row, d0 = 16 * (4 * quarter + (threadIdx.x >> 6));
     if (th >= nt * nh) return;   // whole wave
     const int t = th / nh, h = th - t * nh;
     const int ns = (pos0 + t + chunk) / chunk;   // splits that hold keys <= pos0 + t
