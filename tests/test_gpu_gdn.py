@@ -57,7 +57,7 @@ def test_l2norm(dev, d):
     np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("nt,nv,nk", [(1, 32, 16), (4, 32, 16), (2, 4, 2), (17, 8, 8)])
+@pytest.mark.parametrize("nt,nv,nk", [(1, 32, 16), (4, 32, 16), (2, 4, 2), (17, 8, 8), (3, 3, 1), (2, 5, 5)])
 def test_step(dev, nt, nv, nk):
     announce(f"gdn_step nt={nt} nv={nv} nk={nk}")
     d = gdn_step_inputs(3, nt, nv=nv, nk=nk)
@@ -117,7 +117,8 @@ def test_decode_fused_config4(dev):
     assert_argmax_agrees(out, out_ref)
 
 
-@pytest.mark.parametrize("nt,nv,nk,K", [(1, 32, 16, 4), (2, 32, 16, 4), (4, 8, 4, 3), (3, 4, 2, 2), (1, 8, 8, 4)])
+@pytest.mark.parametrize("nt,nv,nk,K", [(1, 32, 16, 4), (2, 32, 16, 4), (4, 8, 4, 3), (3, 4, 2, 2), (1, 8, 8, 4),
+                                        (2, 3, 1, 4)])
 def test_decode_fused_equals_two_kernels(dev, nt, nv, nk, K):
     """The one-launch layer equals it_gdn_conv_l2norm + it_gdn_step on the same inputs (the q/k
     norms' sums are added in another order: last-bit differences only) and leaves the same conv
