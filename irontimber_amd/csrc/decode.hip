@@ -273,9 +273,17 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
             const float ls = sum_xor32(lacc[b][i]);
             if (l < 32 && rb + i < R) {
                 float* rec = part + ((size_t)(tq * nh + kh * G + gq) * smax + s) * PART;
+                // blocks of 16 or more rows (verify at nt = 4) store their records non-temporally:
+                // measured faster there (15.7 -> 14.6 us per layer), slower for decode (10.3 -> 11.1)
+                if constexpr (NB >= 2) {
 #pragma unroll
-                for (int n = 0; n < 4; ++n) rec[4 + 64 * w + 16 * n + c] = v[n];
-                if (w == 0 && c == 0) *(f4*)rec = f4{mh[i] * LN2_F, ls, 0.f, 0.f};
+                    for (int n = 0; n < 4; ++n) __builtin_nontemporal_store(v[n], rec + 4 + 64 * w + 16 * n + c);
+                    if (w == 0 && c == 0) __builtin_nontemporal_store(f4{mh[i] * LN2_F, ls, 0.f, 0.f}, (f4*)rec);
+                } else {
+#pragma unroll
+                    for (int n = 0; n < 4; ++n) rec[4 + 64 * w + 16 * n + c] = v[n];
+                    if (w == 0 && c == 0) *(f4*)rec = f4{mh[i] * LN2_F, ls, 0.f, 0.f};
+                }
             }
             if (++gq == G) { gq = 0; ++tq; }
         }
