@@ -72,7 +72,11 @@ size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv);
  *   Token t attends keys 0..pos0+t (n = pos0+t+1, cpu.rs:260; kernels/src/lib.rs:764); q-head h
  *   reads KV head h/(nh/nkv) (cpu.rs:265).
  *   out  : f32 out[t*out_tok_stride + h*hd + d] = softmax(scale*q.K) V * sigmoid(gate).
- *   scratch: device buffer of at least it_attn_scratch_bytes(...) bytes (may be NULL if that is 0).
+ *   scratch: device buffer for the split-K partial records. it_attn_scratch_bytes(...) bytes give the
+ *          library's preferred split; with fewer bytes the keys per split double until the records
+ *          fit (the reference's rule for its fixed arena, src/vk/mod.rs:714-716), and the prefill
+ *          kernel falls back to one pass with no scratch. The reference's own room,
+ *          it_attention_dispatch_room(ctx_len, nh, nt) * 4 bytes, is always enough. NULL = 0 bytes.
  * Requires hd == 256, nh % nkv == 0, q_tok_stride and out_tok_stride multiples of 4, 16-byte
  * aligned q/out/kc/vc (the reference asserts the same f16 layout, src/vk/mod.rs:713).
  * Replaces VkEngine::attention_kv(qo,qts,kco,vco,kvd,pos0,hd,nh,nkv,oo,nt,f16=true),
@@ -90,11 +94,19 @@ int it_attn_f16(const float* q, int q_tok_stride, const uint16_t* kc, const uint
  *          partial records are merged like kernel 1's.
  *   chunk  = keys per split (multiple of 64), 0 = automatic. For kernel 2 a chunk of at least
  *          pos0 + nt means one pass.
- * it_attn_scratch_bytes_ex gives the scratch for the same choice. */
+ * it_attn_scratch_bytes_ex gives the scratch for the same choice. With chunk = 0 the split is fitted
+ * to scratch_bytes as in it_attn_f16; an explicit chunk needs its full record set. */
 size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int kernel, int chunk);
 int it_attn_f16_ex(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,
                    int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
                    void* scratch, size_t scratch_bytes, int kernel, int chunk, void* stream);
+
+/* The choice it_attn_f16 makes for this geometry and scratch budget: *kernel 1 (split-K) or 2
+ * (flash), *chunk keys per split (0 = flash in one pass, no scratch), *bytes of scratch used.
+ * Returns nonzero if no split fits (only possible for nt < 16 with fewer than nt*nh*1040 bytes).
+ * Host-only; the chunk loop is the reference's, src/vk/mod.rs:714-716. */
+int it_attn_plan(int pos0, int nt, int hd, int nh, int nkv, size_t scratch_bytes, int* kernel, int* chunk,
+                 size_t* bytes);
 
 /* The two phases of the split-K path as separate calls (the reference dispatches them separately
  * too: attn_s_h then attn_comb, src/vk/mod.rs:725-727). Partial record of (token t, q-head h,
@@ -282,6 +294,12 @@ size_t it_attention_dispatch_room(size_t ctx, size_t heads, size_t nt);
 /* Keys per split the reference would choose: 64 doubled (at most to 1024) until
  * nt*nh*ceil((pos0+nt)/C)*260 <= room (src/vk/mod.rs:714-716); -1 if even 1024 does not fit. */
 int it_attention_chunk(uint32_t nt, uint32_t nh, uint32_t pos0, size_t room);
+/* The prompt split of src/vk/mod.rs:130-134 (prefill_chunks): consecutive ranges of at most `batch`
+ * tokens (batch 64, 128, 256 or 512) covering 0..len, where a range longer than 64 whose length
+ * leaves a tail of 1..21 tokens past a multiple of 64 gives that tail to the next range (no token
+ * is dropped or repeated). Range i is starts[i] .. starts[i]+lens[i]. Writes at most cap ranges and
+ * returns the number of ranges (which may exceed cap), or -1 if batch is not 64/128/256/512. */
+long it_prefill_chunks(size_t len, size_t batch, size_t* starts, size_t* lens, size_t cap);
 /* Geometry check of src/vk/mod.rs:207-220 restricted to the attention/GDN fields; 0 = supported. */
 int it_validate_geometry(int ctx_len, int head_dim, int n_head, int n_head_kv, int ssm_state,
                          int ssm_groups, int ssm_vheads, int ssm_inner, int conv_k);

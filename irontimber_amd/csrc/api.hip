@@ -57,6 +57,32 @@ size_t splitk_scratch(int pos0, int nt, int nh, int chunk) {
     return (size_t)nt * nh * smax * PART_WORDS * sizeof(float);
 }
 
+// Kernel and keys per split for an automatic call that must fit `budget` bytes of scratch. The
+// library's preferred split is kept when it fits; otherwise the split doubles until the records
+// fit, which is the reference's rule for its fixed arena (src/vk/mod.rs:714-716: C doubles from 64
+// while nt*nh*ceil((pos0+nt)/C)*260 words exceed the room). The flash kernel ends at one pass over
+// all keys, which needs no scratch, so it always has a plan; the split-K kernel (nt < 16) can run
+// out of doublings only when even one record per (token, head) exceeds the budget. A chunk of 0
+// from the flash plan means the one-pass form. Returns false if nothing fits.
+struct AttnPlan { int kernel, chunk; size_t bytes; };
+bool plan_attn(int pos0, int nt, int nh, int nkv, int kernel, size_t budget, AttnPlan& p) {
+    const long total = (long)pos0 + nt;
+    if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
+    p.kernel = kernel;
+    if (kernel == KERNEL_FLASH) {
+        int c = flash_chunk(pos0, nt, nh, nkv, 0);
+        while (c && splitk_scratch(pos0, nt, nh, c) > budget) c = (2L * c >= total) ? 0 : 2 * c;
+        p.chunk = c;
+        p.bytes = c ? splitk_scratch(pos0, nt, nh, c) : 0;
+        return true;
+    }
+    int c = auto_chunk(pos0, nt, nh, nkv);
+    while (splitk_scratch(pos0, nt, nh, c) > budget && c < total) c *= 2;
+    p.chunk = c;
+    p.bytes = splitk_scratch(pos0, nt, nh, c);
+    return p.bytes <= budget;
+}
+
 int validate_attn(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
                   int nkv, int nt, const float* out, int ots) {
     if (hd != HD) return fail("it_attn_f16: head_dim %d unsupported (the f16 KV path requires 256)", hd);
@@ -187,6 +213,20 @@ size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int k
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
     return splitk_scratch(pos0, nt, nh, chunk);
 }
+int it_attn_plan(int pos0, int nt, int hd, int nh, int nkv, size_t scratch_bytes, int* kernel, int* chunk,
+                 size_t* bytes) {
+    if (hd != HD || nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv || (long)pos0 + nt > (1L << 22))
+        return fail("it_attn_plan: bad geometry");
+    AttnPlan p;
+    const bool ok = plan_attn(pos0, nt, nh, nkv, KERNEL_AUTO, scratch_bytes, p);
+    if (kernel) *kernel = p.kernel;
+    if (chunk) *chunk = p.chunk;
+    if (bytes) *bytes = p.bytes;
+    if (!ok) return fail("it_attn_plan: %zu bytes of scratch cannot hold one record per (token, head)", scratch_bytes);
+    g_err.clear();
+    return 0;
+}
+
 size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv) {
     return it_attn_scratch_bytes_ex(pos0, nt, hd, nh, nkv, KERNEL_AUTO, 0);
 }
@@ -195,11 +235,26 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
                    int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes, int kernel,
                    int chunk, void* stream) {
     if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, out, ots)) return -1;
+    if (kernel != KERNEL_AUTO && kernel != KERNEL_SPLITK && kernel != KERNEL_FLASH)
+        return fail("it_attn_f16: unknown kernel %d", kernel);
+    if (kernel == KERNEL_FLASH && nt < 16) return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
+    if (chunk == 0) {
+        // automatic split: fit the caller's scratch (the reference's arena rule), never refuse a
+        // geometry for which a smaller record set exists
+        AttnPlan p;
+        if (!plan_attn(pos0, nt, nh, nkv, kernel, scratch ? scratch_bytes : 0, p))
+            return fail("it_attn_f16: scratch of %zu bytes cannot hold even one partial record per (token, head) "
+                        "(%zu bytes)", scratch_bytes, p.bytes);
+        kernel = p.kernel;
+        if (kernel == KERNEL_FLASH && p.chunk == 0) chunk = 1 << 30;   // one pass
+        else chunk = p.chunk;
+    }
     if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
     hipStream_t st = (hipStream_t)stream;
     if (kernel == KERNEL_FLASH) {
         if (nt < 16) return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
         if (chunk < 0 || chunk % 64 != 0) return fail("it_attn_f16: flash chunk %d must be a multiple of 64", chunk);
+        // (chunk is never 0 here: the automatic plan above has replaced it)
         const int c = flash_chunk(pos0, nt, nh, nkv, chunk);
         if (!c)
             return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st),
@@ -478,6 +533,25 @@ int it_attention_chunk(uint32_t nt, uint32_t nh, uint32_t pos0, size_t room) {
     return (int)c;
 }
 
+long it_prefill_chunks(size_t len, size_t batch, size_t* starts, size_t* lens, size_t cap) {
+    if (batch != 64 && batch != 128 && batch != 256 && batch != 512)
+        return fail("it_prefill_chunks: unsupported prefill batch %zu; use 64/128/256/512", batch), -1;
+    long count = 0;
+    for (size_t start = 0; start < len;) {
+        size_t n = len - start < batch ? len - start : batch;
+        const size_t tail = n % 64;
+        if (n > 64 && tail > 0 && tail < 22) n -= tail;   // the short tail goes to the next range
+        if ((size_t)count < cap) {
+            if (starts) starts[count] = start;
+            if (lens) lens[count] = n;
+        }
+        ++count;
+        start += n;
+    }
+    g_err.clear();
+    return count;
+}
+
 int it_validate_geometry(int ctx_len, int head_dim, int n_head, int n_head_kv, int ssm_state, int ssm_groups,
                          int ssm_vheads, int ssm_inner, int conv_k) {
     if (ctx_len <= 0 || ctx_len > 8192) return fail("supported context capacity is 1..=8192");
@@ -489,9 +563,9 @@ int it_validate_geometry(int ctx_len, int head_dim, int n_head, int n_head_kv, i
     return 0;
 }
 
-}  // extern "C"
-
 int it_calib_mfma_f16(int wgs, int iters, float* out, void* stream) {
     if (wgs < 1 || iters < 1 || !out) return fail("it_calib_mfma_f16: wgs %d / iters %d / out invalid", wgs, iters);
     return check(it::launch_mfma_peak(wgs, iters, out, (hipStream_t)stream), "it_calib_mfma_f16");
 }
+
+}  // extern "C"

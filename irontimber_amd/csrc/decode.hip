@@ -333,7 +333,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
         // reuse them while the load is in flight, which costs a wait per load.
 #pragma unroll
         for (int j = 0; j < COMB_SPL; ++j) {
-            const float* rec = base + (size_t)(s0 + sg + SL * max(0, min(j, nb - 1))) * PART;
+            // a lane with no split left in the batch (nb <= 0) reloads split ns - 1: every index
+            // stays inside this row's records, so a buffer sized exactly for them is never overrun
+            const float* rec = base + (size_t)min(s0 + sg + SL * max(0, min(j, nb - 1)), ns - 1) * PART;
             hv[j] = *(const f2*)rec;
             ov[j] = ld_f4(rec + 4 + d0);
         }

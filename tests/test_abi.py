@@ -120,3 +120,94 @@ def test_scratch_bytes_policy():
     # forced one-pass flash (chunk >= keys) and forced splits
     assert lib.it_attn_scratch_bytes_ex(4096, 64, 256, 16, 2, 2, 8192) == 0
     assert lib.it_attn_scratch_bytes_ex(4096, 64, 256, 16, 2, 2, 1024) == 64 * 16 * 5 * 260 * 4
+
+
+@pytest.mark.parametrize("nh,nkv", [(16, 2), (24, 4)])
+def test_plan_fits_reference_room_sweep(tmp_path, nh, nkv):
+    """Every (nt 1..512, pos0 <= 8192-nt) with the engine's capacity at pos0+nt and at 8192: the
+    split it_attn_f16 picks fits attention_dispatch_room words (src/vk/mod.rs:148-150, 714-716)."""
+    import subprocess
+    exe = tmp_path / "plan_sweep"
+    subprocess.run(["gcc", "-O2", "-o", str(exe), os.path.join(ROOT, "tests", "csrc", "plan_sweep.c"), "-ldl"],
+                   check=True)
+    r = subprocess.run([str(exe), _lib.LIB_PATH, str(nh), str(nkv), "8192", "512"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout + r.stderr
+    plans, grown, _ = map(int, r.stdout.split()[1:])
+    assert plans == 8126464 and grown > 0
+
+
+def plan(pos0, nt, nh, nkv, budget):
+    k, c, b = ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+    rc = _lib.lib().it_attn_plan(pos0, nt, 256, nh, nkv, budget, ctypes.byref(k), ctypes.byref(c), ctypes.byref(b))
+    return rc, k.value, c.value, b.value
+
+
+def test_plan_config3_positions_fit_reference_room():
+    """The config-3 chunk positions that overflowed the room with the preferred split now grow it."""
+    lib = _lib.lib()
+    room = lib.it_attention_dispatch_room(8192, 16, 64) * 4
+    for pos0 in (3968, 4032, 5952, 6016, 6080, 7936, 8000, 8064, 8128):
+        pref = lib.it_attn_scratch_bytes(pos0, 64, 256, 16, 2)
+        rc, k, c, b = plan(pos0, 64, 16, 2, room)
+        assert rc == 0 and k == 2 and b <= room
+        assert pref > room or b == pref
+        assert c == 0 or c % 64 == 0
+
+
+def test_plan_decode_keeps_64_and_small_budget_fails_cleanly():
+    lib = _lib.lib()
+    room = lib.it_attention_dispatch_room(8192, 16, 1) * 4
+    assert plan(8191, 1, 16, 2, room)[1:3] == (1, 64)
+    # one record per (token, head) is the floor of the split-K kernel
+    rc, k, c, b = plan(8191, 1, 16, 2, 16 * 1040 - 1)
+    assert rc != 0 and "one record" in _lib.last_error()
+    assert plan(8191, 1, 16, 2, 16 * 1040)[0] == 0
+    # the flash kernel always has a plan: one pass needs no scratch
+    assert plan(4096, 64, 16, 2, 0)[1:] == (2, 0, 0)
+
+
+def prefill_chunks(n, batch):
+    lib = _lib.lib()
+    cnt = lib.it_prefill_chunks(n, batch, None, None, 0)
+    if cnt < 0:
+        return None
+    st, ln = (ctypes.c_size_t * max(cnt, 1))(), (ctypes.c_size_t * max(cnt, 1))()
+    assert lib.it_prefill_chunks(n, batch, st, ln, cnt) == cnt
+    return [(st[i], st[i] + ln[i]) for i in range(cnt)]
+
+
+def test_prefill_chunks_cover_every_token():
+    """prefill_review.rs:20-25: every range non-empty and <= batch, ids 0..n in order, 129 @ 512."""
+    for batch in (64, 128, 256, 512):
+        for n in (0, 1, 21, 22, 64, 65, 129, 2091, 4191, 7416, 8192):
+            rr = prefill_chunks(n, batch)
+            ids = []
+            for a, b in rr:
+                assert 0 < b - a <= batch
+                ids.extend(range(a, b))
+            assert ids == list(range(n))
+    assert prefill_chunks(129, 512) == [(0, 128), (128, 129)]
+    assert prefill_chunks(8192, 64) == [(64 * i, 64 * i + 64) for i in range(128)]
+    # a tail of 22 or more tokens stays in its range; 1..21 past a multiple of 64 is peeled
+    assert prefill_chunks(150, 512) == [(0, 150)]
+    assert prefill_chunks(148, 512) == [(0, 128), (128, 148)]
+    assert prefill_chunks(85, 128) == [(0, 64), (64, 85)]
+    assert prefill_chunks(86, 128) == [(0, 86)]
+    assert prefill_chunks(70, 64) == [(0, 64), (64, 70)]
+    for bad in (0, 32, 65, 1024):
+        assert prefill_chunks(100, bad) is None and "unsupported prefill batch" in _lib.last_error()
+
+
+def test_prefill_chunks_brute_force():
+    """Against a direct statement of the rule for every n <= 1100 and every batch."""
+    for batch in (64, 128, 256, 512):
+        for n in range(0, 1100):
+            want, s = [], 0
+            while s < n:
+                m = min(n - s, batch)
+                if m > 64 and 0 < m % 64 < 22:
+                    m -= m % 64
+                want.append((s, s + m))
+                s += m
+            assert prefill_chunks(n, batch) == want

@@ -185,3 +185,32 @@ def test_two_phase_abi_equals_single_call(dev):
     call("it_attn_combine", qd.data_ptr(), nh * 512, part.data_ptr(), ctx - nt, 256, nh, nt, chunk, out.data_ptr(),
          nh * 256, s)
     np.testing.assert_array_equal(host(out), ref)
+
+
+@pytest.mark.parametrize("pos0,nt,cap", [(3968, 64, 8192), (4032, 64, 8192), (8128, 64, 8192), (3977, 64, 4041),
+                                         (245, 13, 258), (8188, 4, 8192), (4096, 64, 0)])
+def test_reference_room_is_enough(dev, pos0, nt, cap):
+    """it_attn_f16 with scratch of exactly the reference arena's room (attention_dispatch_room at
+    capacity `cap`, src/vk/mod.rs:148-150, 714-716; cap 0 = no scratch at all): the split grows until
+    the records fit, nothing past the room is written, and the result matches the oracle."""
+    from irontimber_amd import _lib
+    lib = _lib.lib()
+    ctx = pos0 + nt
+    room = lib.it_attention_dispatch_room(cap, 16, nt) * 4 if cap else 0
+    announce(f"attn room pos0={pos0} nt={nt} cap={cap} room={room} preferred={ops.attn_scratch_bytes(pos0, nt, 16, 2)}")
+    q, kb, vb = attn_inputs(2, ctx=ctx, nt=nt)
+    guard = 1 << 16
+    buf = torch.full((room + guard,), 0x5A, dtype=torch.uint8, device=dev)
+    scratch = buf if room else None
+    qd = dev_f32(q.reshape(nt, -1), dev)
+    out = torch.empty(nt, 16 * 256, device=dev)
+    _lib.call("it_attn_f16", qd.data_ptr(), 16 * 512, dev_f16bits(kb, dev).data_ptr(), dev_f16bits(vb, dev).data_ptr(),
+              512, pos0, 256, 16, 2, nt, 1.0 / 16, out.data_ptr(), 16 * 256,
+              scratch.data_ptr() if scratch is not None else None, room, None)
+    got = host(out)
+    assert bool((buf[room:] == 0x5A).all()), "scratch written past the room"
+    want = oracle.attn(q.reshape(nt, -1), kb, vb, pos0, 16, 2)
+    err = np.abs(got - want).max()
+    print(f"max_abs={err:.3g}")
+    assert np.isfinite(got).all() and err <= TOL
+    assert assert_argmax_agrees(got, want) == 0
