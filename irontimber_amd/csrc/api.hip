@@ -267,7 +267,6 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
                                                  (float*)scratch, c, st),
                      "it_attn_f16 (flash, key splits)");
     }
-    if (kernel != KERNEL_SPLITK) return fail("it_attn_f16: unknown kernel %d", kernel);
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
     if (chunk % 64 != 0) return fail("it_attn_f16: chunk %d must be a multiple of 64", chunk);
     const size_t need = splitk_scratch(pos0, nt, nh, chunk);

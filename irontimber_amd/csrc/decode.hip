@@ -390,25 +390,12 @@ __device__ __forceinline__ void swap16(float& a, float& b) {
     asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
 
+// One wave merges the records of query row th (token t = th / nh, head h) for output dims
+// d0 .. d0+15; lane l = the wave's lane.
 template <int SPL>
-__global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __restrict__ q, int qts, int pos0,
-                                                                int nh, int nt, const float* __restrict__ part,
-                                                                int chunk, int smax, float* __restrict__ out,
-                                                                int ots) {
-    // workgroup = 4 waves = 64 dims of one row; the 4 workgroups of a row read the same record
-    // lines, so they get ids 8 apart (one XCD under the round-robin dispatch) when the row count
-    // allows it, and each line comes from HBM into that XCD's L2 once
-    int row, quarter;
-    if ((nt * nh) % 8 == 0) {
-        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-        row = ((slot >> 2) << 3) | xcd;
-        quarter = slot & 3;
-    } else {
-        row = blockIdx.x >> 2;
-        quarter = blockIdx.x & 3;
-    }
-    const int l = threadIdx.x & 63;
-    const int th = row, d0 = 16 * (4 * quarter + (threadIdx.x >> 6));
+__device__ __forceinline__ void combine_wave_row(const float* __restrict__ q, int qts, int pos0, int nh, int nt,
+                                                 const float* __restrict__ part, int chunk, int smax,
+                                                 float* __restrict__ out, int ots, int th, int d0, int l) {
     if (th >= nt * nh) return;   // whole wave
     const int t = th / nh, h = th - t * nh;
     const int ns = (pos0 + t + chunk) / chunk;   // splits that hold keys <= pos0 + t
@@ -478,6 +465,27 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __r
         const int d = d0 + 8 * (l >> 5) + 4 * ((l >> 4) & 1) + 2 * ((l >> 3) & 1) + ((l >> 2) & 1);
         out[(size_t)t * ots + (size_t)h * HD + d] = v / den * sigmoidf_(gv);
     }
+}
+
+template <int SPL>
+__global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __restrict__ q, int qts, int pos0,
+                                                                int nh, int nt, const float* __restrict__ part,
+                                                                int chunk, int smax, float* __restrict__ out,
+                                                                int ots) {
+    // workgroup = 4 waves = 64 dims of one row; the 4 workgroups of a row read the same record
+    // lines, so they get ids 8 apart (one XCD under the round-robin dispatch) when the row count
+    // allows it, and each line comes from HBM into that XCD's L2 once
+    int row, quarter;
+    if ((nt * nh) % 8 == 0) {
+        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+        row = ((slot >> 2) << 3) | xcd;
+        quarter = slot & 3;
+    } else {
+        row = blockIdx.x >> 2;
+        quarter = blockIdx.x & 3;
+    }
+    combine_wave_row<SPL>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots, row,
+                          16 * (4 * quarter + (threadIdx.x >> 6)), threadIdx.x & 63);
 }
 
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,

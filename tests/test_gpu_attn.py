@@ -204,7 +204,8 @@ def test_reference_room_is_enough(dev, pos0, nt, cap):
     scratch = buf if room else None
     qd = dev_f32(q.reshape(nt, -1), dev)
     out = torch.empty(nt, 16 * 256, device=dev)
-    _lib.call("it_attn_f16", qd.data_ptr(), 16 * 512, dev_f16bits(kb, dev).data_ptr(), dev_f16bits(vb, dev).data_ptr(),
+    kc, vc = dev_f16bits(kb, dev), dev_f16bits(vb, dev)   # held: a freed block could be reused by the next upload
+    _lib.call("it_attn_f16", qd.data_ptr(), 16 * 512, kc.data_ptr(), vc.data_ptr(),
               512, pos0, 256, 16, 2, nt, 1.0 / 16, out.data_ptr(), 16 * 256,
               scratch.data_ptr() if scratch is not None else None, room, None)
     got = host(out)
