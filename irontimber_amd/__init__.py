@@ -1,8 +1,8 @@
 """irontimber_amd: MI355X (gfx950) attention / Gated-DeltaNet hot path of the IronTimber engine.
 
 The compute lives in lib/libit_attn.so (hand-written HIP, C ABI in include/it_attn.h); this
-package only binds it (`_lib`), offers torch-tensor wrappers (`ops`), the reference-shaped arena
-dispatcher (`engine`) and seeded workload generators (`synth`).
+package only binds it (`_lib`), offers torch-tensor wrappers (`ops`) and seeded workload
+generators (`synth`).
 """
 import os
 

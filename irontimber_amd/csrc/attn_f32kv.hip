@@ -27,18 +27,6 @@ __device__ __forceinline__ f4 mfma16x16x4f32(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Lanes l and l ^ 16 (v_permlane16_swap exchanges the odd 16-lane rows of its first operand with
-// the even rows of its second; with both holding v every lane sees its partner's value).
-__device__ __forceinline__ float max_xor16(float v) {
-    float a = v, b = v;
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return fmaxf(a, b);
-}
-__device__ __forceinline__ float sum_xor16(float v) {
-    float a = v, b = v;
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return a + b;
-}
 
 }  // namespace
 

@@ -88,21 +88,35 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (a + b) + (c + d);
 }
 
-// max / sum over lanes l and l ^ 32 without going through LDS (a ds_bpermute would make the next
-// wait on LDS results also wait for every LDS operand read in flight): v_permlane32_swap exchanges
-// the two lane halves between two registers, both holding v. Written out because the compiler
-// folds the builtin's two results when both inputs are the same value. The swap reads VGPRs just
-// written by VALU ops, which needs two wait states first.
-__device__ __forceinline__ float max_xor32(float v) {
-    float a = v, b = v;
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return fmaxf(a, b);
+// s_waitcnt immediate that waits until at most N vector-memory operations of this wave are still
+// outstanding, leaving the other counters alone. gfx9-family simm16 layout (gfx950 included):
+// bits [3:0] vmcnt[3:0], [6:4] expcnt (7 = no wait), [11:8] lgkmcnt (15 = no wait),
+// [15:14] vmcnt[5:4]. Used where a wait for the global->LDS copies must not also wait for LDS
+// reads (the builtin __syncthreads() fence would wait for every counter).
+#define IT_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
+
+// Lane exchanges written as inline asm: v_permlane16_swap_b32 / v_permlane32_swap_b32 swap the odd
+// 16-lane rows (resp. the upper 32 lanes) of the first operand with the even rows (lower lanes) of
+// the second, so with both holding v each lane sees its partner l ^ 16 (l ^ 32). Written out
+// because the compiler folds the builtin's two results when both inputs are the same value, and
+// kept off LDS (a ds_bpermute would make the next wait on LDS results also wait for every LDS
+// operand read in flight).
+// Hazard: the ISA requires two wait states between a VALU write of a VGPR and a permlane swap
+// reading it, and the compiler's hazard recognizer does not look inside inline asm, so each swap
+// carries its own "s_nop 1" (two wait states). A missing wait reads a stale register and breaks
+// every reduction built on these helpers: the split-K records, the decode merge and the GDN
+// L2 norms, all of which the GPU parity tests check against the oracle.
+__device__ __forceinline__ void swap16(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
-__device__ __forceinline__ float sum_xor32(float v) {
-    float a = v, b = v;
+__device__ __forceinline__ void swap32(float& a, float& b) {
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return a + b;
 }
+// max / sum over lanes l and l ^ 32, and over l and l ^ 16
+__device__ __forceinline__ float max_xor32(float v) { float a = v, b = v; swap32(a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float sum_xor32(float v) { float a = v, b = v; swap32(a, b); return a + b; }
+__device__ __forceinline__ float max_xor16(float v) { float a = v, b = v; swap16(a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float sum_xor16(float v) { float a = v, b = v; swap16(a, b); return a + b; }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }

@@ -41,8 +41,6 @@ constexpr float LOG2E_F = 1.4426950408889634f;
 constexpr float LN2_F = 0.6931471805599453f;
 constexpr int COMB_SPL = 8;     // splits per merge split lane per batch of loads
 
-#define IT_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
-
 // V tile chunk swizzle. The transpose read of one 16-lane group covers rows r0..r0+3 (r0 % 4 == 0)
 // x 32 bytes (two chunks of one 128-byte line); unswizzled, the four 512-byte-apart rows would hit
 // the same banks. XOR-ing the chunk index with 2*(r & 3) moves the four rows to four different
@@ -383,12 +381,6 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // 16-lane rows) hands each lane of a pair the half of the other's values it keeps, so 16 dims
 // need 8 + 4 + 2 + 1 + 2 exchanges instead of 16 full reductions. Lane l ends holding dim
 // 8*b5 + 4*b4 + 2*b3 + b2 (bits of l) summed over all lanes.
-__device__ __forceinline__ void swap32(float& a, float& b) {
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap16(float& a, float& b) {
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
 
 // One wave merges the records of query row th (token t = th / nh, head h) for output dims
 // d0 .. d0+15; lane l = the wave's lane.

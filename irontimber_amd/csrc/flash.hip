@@ -77,8 +77,6 @@ __device__ __forceinline__ void scale_acc(f16v& acc, float a) {
 
 // s_waitcnt immediates (gfx9 encoding): wait until at most N vector-memory ops are outstanding
 // (expcnt/lgkmcnt left unconstrained).
-#define IT_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
-
 __global__ __launch_bounds__(256) void attn_flash_kernel(
     const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int kvd,
     int pos0, int nh, int nkv, int nt, float scale, float* __restrict__ out, int ots, float* __restrict__ part,
@@ -232,9 +230,12 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
             const float mnew = grow ? mx : m_run;
             const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - mnew);
             l_run *= alpha;
-            // the previous tile's last P.V matrix ops may still be writing O: the reads below are
-            // inline assembly, which the compiler's hazard checks do not see into, so give them
-            // time to finish (> 18 wait states for a 16-pass op)
+            // the previous tile's last P.V matrix ops may still be writing O. The ISA requires, after
+            // an XDL matrix op that writes accumulation registers, (passes + 2) wait states before a
+            // v_accvgpr_read of them: 18 for the 16-pass 32x32x16 f16 op. scale_acc is inline assembly,
+            // which the compiler's hazard recognizer does not look into, so the wait is explicit:
+            // four s_nop 7 give 32 wait states. Too few would scale a stale O on the rare tiles
+            // where a row's reference max grows (every prefill parity test crosses such tiles).
             asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");
 #pragma unroll
             for (int db = 0; db < 8; ++db) scale_acc(o[db], alpha);

@@ -197,11 +197,7 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_v4_kernel(const float* __rest
         ss += dppc<0x4E>(ss);    // quad_perm [2,3,0,1]
         ss += dppc<0x141>(ss);   // row_half_mirror
         ss += dppc<0x140>(ss);   // row_mirror
-        {
-            float a = ss, b = ss;   // rows 0+1 and 2+3: the two heads' sums
-            asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-            ss = a + b;
-        }
+        ss = sum_xor16(ss);      // rows 0+1 and 2+3: the two heads' sums
         if (norm) y *= 1.0f / fmaxf(sqrtf(ss), eps);
         *(f4*)(out + (size_t)(t0 + j) * ots + ch) = y;
 #pragma unroll
@@ -251,9 +247,7 @@ __global__ __launch_bounds__(256) void l2norm_kernel(float* __restrict__ x, int 
 __device__ __forceinline__ float sum_lanes_stride4(float v) {
     v += dppc<0x124>(v);   // row_ror:4
     v += dppc<0x128>(v);   // row_ror:8
-    float a = v, b = v;
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return sum_xor32(a + b);
+    return sum_xor32(sum_xor16(v));
 }
 
 // Workgroup id -> (16-column block cb, V head h) of the 8 x nv step grid, launched 1-D.
