@@ -26,6 +26,7 @@ _i = ctypes.c_int
 _f = ctypes.c_float
 _SIG = {
     "it_ref_hardware_threads": (_i, []),
+    "it_ref_xorshift_fill": (None, [_P, ctypes.c_size_t, _P]),
     "it_ref_f32_to_f16_rne": (ctypes.c_uint16, [_f]),
     "it_ref_f16_to_f32": (_f, [ctypes.c_uint16]),
     "it_ref_rmsnorm": (None, [_P, _P, _i, _f, _P]),
@@ -63,6 +64,17 @@ def lib() -> ctypes.CDLL:
 def _p(a: np.ndarray) -> int:
     assert a.flags["C_CONTIGUOUS"]
     return a.ctypes.data
+
+
+def kparity_draws(n_arena: int, n_params: int, seed: int = 0x9E3779B97F4A7C15):
+    """The arena and params floats of the reference's kernel-parity harness (src/vk/kparity.rs:13,
+    59-62): n_arena then n_params uniform [-1, 1) draws from one xorshift64 stream."""
+    st = np.array([seed], np.uint64)
+    a = np.empty(n_arena, np.float32)
+    p = np.empty(n_params, np.float32)
+    lib().it_ref_xorshift_fill(_p(st), n_arena, _p(a))
+    lib().it_ref_xorshift_fill(_p(st), n_params, _p(p))
+    return a, p
 
 
 def hardware_threads() -> int:

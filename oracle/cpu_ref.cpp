@@ -62,6 +62,21 @@ extern "C" {
 
 int it_ref_hardware_threads() { return (int)std::max(1u, std::thread::hardware_concurrency()); }
 
+// The kernel-parity harness's input generator (src/vk/kparity.rs:13, Rng::f): xorshift64 with shifts
+// 13, 7, 17, then the top 24 bits of the state scaled to [-1, 1). Fills out[0..n) starting from
+// *state and leaves the advanced state in *state, so the arena draw (kparity.rs:61) followed by
+// the params draw (kparity.rs:62) is two calls.
+void it_ref_xorshift_fill(uint64_t* state, size_t n, float* out) {
+    uint64_t x = *state;
+    for (size_t i = 0; i < n; ++i) {
+        x ^= x << 13;
+        x ^= x >> 7;
+        x ^= x << 17;
+        out[i] = ((float)(x >> 40) / (float)(1u << 24)) * 2.0f - 1.0f;
+    }
+    *state = x;
+}
+
 // f32 -> f16 bits, round to nearest even (the `half` crate's f16::from_f32, cpu.rs:22).
 uint16_t it_ref_f32_to_f16_rne(float x) {
     uint32_t b; std::memcpy(&b, &x, 4);

@@ -46,6 +46,7 @@ def assert_argmax_agrees(got: np.ndarray, want: np.ndarray, n_cls: int = 997, se
     ag, aw = lg.argmax(-1), lw.argmax(-1)
     rows = np.nonzero(ag != aw)[0]
     if rows.size == 0:
+        print(f"argmax: identical on all {g.shape[0]} rows")
         return 0
     margin = lw[rows, aw[rows]] - lw[rows, ag[rows]]
     noise = np.sqrt(2.0) * np.linalg.norm(g[rows] - w[rows], axis=-1)

@@ -91,7 +91,7 @@ def test_layer_config4(dev):
     assert np.abs(out - out_ref).max() <= OUT_TOL
     assert np.abs(host(st) - sst).max() <= STATE_TOL
     np.testing.assert_array_equal(host(cs), cst)
-    assert_argmax_agrees(out, out_ref)
+    assert assert_argmax_agrees(out, out_ref) == 0   # no flip
 
 
 def test_decode_fused_config4(dev):
@@ -114,7 +114,7 @@ def test_decode_fused_config4(dev):
     assert np.abs(host(st) - sst).max() <= STATE_TOL
     np.testing.assert_array_equal(host(cs_out), cst)
     np.testing.assert_array_equal(host(cs_in), d["conv_state"])
-    assert_argmax_agrees(out, out_ref)
+    assert assert_argmax_agrees(out, out_ref) == 0   # no flip
 
 
 @pytest.mark.parametrize("nt,nv,nk,K", [(1, 32, 16, 4), (2, 32, 16, 4), (4, 8, 4, 3), (3, 4, 2, 2), (1, 8, 8, 4),
@@ -248,7 +248,7 @@ def test_chunked_prefill_config5(dev):
     """BASELINE config 5 (seed 4): conv (K=4) -> L2 -> chunk-64 scan over an 8192-token prompt,
     32 V / 16 QK heads, against 8192 sequential steps of the cpu.rs restatement (per-token conv,
     L2 and recurrence); also against the GPU's own token-sequential kernel. Final-state bound
-    5e-3, output bound 2e-3, identical argmax of a fixed projection of the last token."""
+    5e-3, output bound 2e-3, identical argmax of a fixed projection on every token."""
     nv, nk, S, nt = 32, 16, 128, 8192
     d = gdn_inputs(4, nt=nt, nv=nv, nk=nk)
     announce("gdn config5 oracle (cpu)")
@@ -271,7 +271,7 @@ def test_chunked_prefill_config5(dev):
     print(f"config5 chunked vs oracle: out max_abs={eo:.3g} state max_abs={es:.3g}")
     assert eo <= OUT_TOL and es <= STATE_TOL
     np.testing.assert_array_equal(host(cs), cst)
-    assert_argmax_agrees(out[-1:], out_ref[-1:])
+    assert assert_argmax_agrees(out, out_ref) == 0   # every token of BASELINE config 5: no flip
     st2 = dev_f32(d["state"], dev)
     seq = host(ops.gdn_step(co, *args, st2, nv, nk))
     assert np.abs(seq - out).max() <= OUT_TOL and np.abs(host(st2) - gst).max() <= STATE_TOL
@@ -360,3 +360,29 @@ def test_gated_layer_config4(dev):
     assert np.abs(host(st) - sst).max() <= STATE_TOL
     np.testing.assert_array_equal(host(cs), cst)
     assert_argmax_agrees(out, want)
+
+
+def test_conv_kparity_geometry(dev):
+    """The reference's kernel-parity conv case (src/vk/kparity.rs:32: cd 1000, 5 tokens, K 4, input
+    rows at arena 0 with stride 1000, weights at params 0, state at arena 2M), on the harness's own
+    xorshift inputs (kparity.rs:13, 59-62): a channel count that is not a multiple of 4 or 128. The
+    GPU conv matches the oracle within 1e-6 and leaves the rolling state bit-exact; a second call
+    continues from that state."""
+    MB = 1 << 20
+    arena, params = oracle.kparity_draws(5 << 20, 1 << 16)
+    cd, nt, K = 1000, 5, 4
+    x = arena[:nt * cd].reshape(nt, cd)
+    w = params[:cd * K].reshape(cd, K)
+    st0 = arena[2 * MB:2 * MB + (K - 1) * cd].reshape(K - 1, cd)
+    announce("gdn conv kparity cd=1000 nt=5 K=4")
+    want, wst = oracle.gdn_conv(x, w, st0)
+    st = dev_f32(st0, dev)
+    got = host(ops.gdn_conv(dev_f32(x, dev), dev_f32(w, dev), st))
+    print(f"kparity conv max_abs={np.abs(got - want).max():.3g}")
+    assert np.abs(got - want).max() <= 1e-6
+    np.testing.assert_array_equal(host(st), wst)
+    x2 = arena[MB:MB + 3 * cd].reshape(3, cd)
+    want2, wst2 = oracle.gdn_conv(x2, w, wst)
+    got2 = host(ops.gdn_conv(dev_f32(x2, dev), dev_f32(w, dev), st))
+    assert np.abs(got2 - want2).max() <= 1e-6
+    np.testing.assert_array_equal(host(st), wst2)

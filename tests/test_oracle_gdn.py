@@ -123,3 +123,75 @@ def test_gated_norm_closed_forms():
     np.testing.assert_allclose(oracle.gdn_gated_norm(c, z, w, nv), want, rtol=2e-6, atol=1e-7)
     want = (rn * silu.reshape(nt, nv, hv)).reshape(nt, -1)
     np.testing.assert_allclose(oracle.gdn_gated_norm(o, z, w, nv), want, rtol=1e-5, atol=1e-6)
+
+
+def _conv_l2_f64(x, w, state, nnorm, S=128, eps=1e-6):
+    """cpu.rs:201-214 in float64, written independently: per token the K-tap window (the K-1 state
+    rows oldest first, then x_t) times w[ch, :], SiLU, state shift; then each of the first nnorm
+    S-wide heads divided by max(||row||, eps)."""
+    x = x.astype(np.float64); w = w.astype(np.float64); st = state.astype(np.float64).copy()
+    nt, cd = x.shape
+    out = np.zeros((nt, cd))
+    for t in range(nt):
+        win = np.vstack([st, x[t:t + 1]])                  # [K, cd]
+        y = (win.T * w).sum(axis=1)
+        y = y / (1.0 + np.exp(-y))
+        for h in range(nnorm):
+            r = y[h * S:(h + 1) * S]
+            y[h * S:(h + 1) * S] = r / max(np.sqrt((r * r).sum()), eps)
+        out[t] = y
+        st = np.vstack([st[1:], x[t:t + 1]])
+    return out, st
+
+
+def test_ref_gdn_layer_direct_strided():
+    """it_ref_gdn_layer itself (the oracle of every GPU GDN-layer test) at nt > 1 with padded token
+    strides: equal bit for bit to its pieces (conv -> l2norm -> step) called separately, and within
+    f32 rounding of an independent float64 statement (conv + L2 above, then gdn_seq_f64)."""
+    nt, nv, nk, S, K = 7, 4, 2, 128, 4
+    d = gdn_inputs(9, nt=nt, nv=nv, nk=nk)
+    cd = d["cd"]
+    xs, bs, os_ = cd + 64, nv + 3, nv * S + 32           # padded token strides
+    xbuf = np.full((nt, xs), np.nan, np.float32); xbuf[:, :cd] = d["x"]
+    bbuf = np.full((nt, bs), np.nan, np.float32); bbuf[:, :nv] = d["beta_raw"]
+    abuf = np.full((nt, bs), np.nan, np.float32); abuf[:, :nv] = d["alpha_raw"]
+    obuf = np.full((nt, os_), 7.0, np.float32)
+    co = np.zeros((nt, cd), np.float32)
+    cst, sst = d["conv_state"].copy(), d["state"].copy()
+    P = lambda a: a.ctypes.data
+    oracle.lib().it_ref_gdn_layer(P(xbuf), xs, P(d["w"]), P(cst), K, P(bbuf), P(abuf), bs, P(d["dt"]), P(d["a"]),
+                                  P(sst), P(obuf), os_, P(co), nt, nv, nk, S, 1e-6, 4)
+    assert np.all(obuf[:, nv * S:] == 7.0)               # nothing written into the stride padding
+    out = obuf[:, :nv * S]
+    # the pieces, each called on its own
+    co2, cst2 = oracle.gdn_conv(d["x"], d["w"], d["conv_state"])
+    co2 = oracle.l2norm_heads(co2, 2 * nk, S)
+    out2, sst2 = oracle.gdn_step(co2, d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
+    np.testing.assert_array_equal(co, co2)
+    np.testing.assert_array_equal(cst, cst2)
+    np.testing.assert_array_equal(out, out2)
+    np.testing.assert_array_equal(sst, sst2)
+    # independent float64 truth
+    co64, st64 = _conv_l2_f64(d["x"], d["w"], d["conv_state"], 2 * nk)
+    np.testing.assert_allclose(co, co64, atol=2e-6)
+    np.testing.assert_allclose(cst, st64, atol=0)
+    o64, s64 = gdn_seq_f64(co64.astype(np.float32), d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
+    np.testing.assert_allclose(out, o64, atol=2e-5)
+    np.testing.assert_allclose(sst, s64, atol=2e-5)
+
+
+def test_conv_oracle_kparity_inputs():
+    """The oracle conv on the reference's kernel-parity conv inputs (kparity.rs:32, cd 1000, 5 tokens,
+    K 4) against the float64 statement: outputs within f32 rounding, the state exactly the last
+    three input rows."""
+    MB = 1 << 20
+    arena, params = oracle.kparity_draws(5 << 20, 1 << 16)
+    cd, nt, K = 1000, 5, 4
+    x = arena[:nt * cd].reshape(nt, cd)
+    w = params[:cd * K].reshape(cd, K)
+    st0 = arena[2 * MB:2 * MB + (K - 1) * cd].reshape(K - 1, cd)
+    out, st = oracle.gdn_conv(x, w, st0)
+    o64, s64 = _conv_l2_f64(x, w, st0, nnorm=0)
+    np.testing.assert_allclose(out, o64, atol=1e-6)
+    np.testing.assert_array_equal(st, x[-3:])
+    np.testing.assert_array_equal(s64.astype(np.float32), x[-3:])
