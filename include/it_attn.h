@@ -101,6 +101,22 @@ int it_attn_f16_ex(const float* q, int q_tok_stride, const uint16_t* kc, const u
                    int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
                    void* scratch, size_t scratch_bytes, int kernel, int chunk, void* stream);
 
+/* it_attn_f16 that allocates nothing and takes no scratch argument. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory or hand over a workspace (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The split-K partial
+ * records go to a file-scope device array of IT_NOALLOC_SCRATCH_BYTES (16 MiB) that each GPU the
+ * library runs on holds until the process ends; the split is fitted to that size as for a caller
+ * buffer of the same size (it_attn_plan(..., IT_NOALLOC_SCRATCH_BYTES, ...) gives the choice), and
+ * a geometry whose records cannot fit (split-K with nt*nh*1040 bytes above the maximum) is rejected
+ * with an error before any device work. Nothing in the array needs to start at zero: every record a
+ * merge reads is written earlier in the same call. All calls on one GPU share that GPU's array, so
+ * calls that overlap on one GPU (different streams, or graphs replayed concurrently) race; calls in
+ * order on one stream do not. Other arguments and results as it_attn_f16. */
+#define IT_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int it_attn_f16_noalloc(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,
+                        int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
+                        void* stream);
+
 /* The choice it_attn_f16 makes for this geometry and scratch budget: *kernel 1 (split-K) or 2
  * (flash), *chunk keys per split (0 = flash in one pass, no scratch), *bytes of scratch used.
  * Returns nonzero if no split fits (only possible for nt < 16 with fewer than nt*nh*1040 bytes).

@@ -2,6 +2,7 @@
 // kernel launches. Validation runs before any device work, like the reference's fail-closed
 // checks (src/vk/mod.rs:179-220); runtime errors come back as nonzero codes with a thread-local
 // message instead of the reference's panics.
+#include <mutex>
 #include <string>
 #include <cstdio>
 #include <cstdarg>
@@ -95,6 +96,36 @@ int validate_attn(const float* q, int qts, const uint16_t* kc, const uint16_t* v
         return fail("it_attn_f16: q/kc/vc/out must be 16-byte aligned");
     if (qts % 4 != 0 || ots % 4 != 0) return fail("it_attn_f16: token strides must be multiples of 4");
     if (nt > 1 && (qts < 2 * nh * hd || ots < nh * hd)) return fail("it_attn_f16: token strides overlap rows");
+    return 0;
+}
+
+// ---- the no-allocation variant of it_attn_f16 ------------------------------------------------
+// Its split-K partial records live in this file-scope device array instead of a caller buffer.
+// Every GPU the library runs on holds its own copy (IT_NOALLOC_SCRATCH_BYTES) until the process
+// ends. In host code `scratch` names a host-side stand-in, not the device copy: the device address
+// comes from hipGetSymbolAddress, once per device with that device current, and only that address
+// is passed to kernels.
+static __device__ __align__(256) unsigned char scratch[IT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEV = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[NOALLOC_MAX_DEV] = {};
+
+// Device address of the current device's `scratch` (looked up on the first call per device).
+int noalloc_scratch(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail("it_attn_f16_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= NOALLOC_MAX_DEV) return fail("it_attn_f16_noalloc: device %d beyond %d", dev, NOALLOC_MAX_DEV);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail("it_attn_f16_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
     return 0;
 }
 
@@ -281,6 +312,20 @@ int it_attn_f16(const float* q, int qts, const uint16_t* kc, const uint16_t* vc,
                 int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes, void* stream) {
     return it_attn_f16_ex(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, ots, scratch, scratch_bytes,
                           KERNEL_AUTO, 0, stream);
+}
+
+int it_attn_f16_noalloc(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd,
+                        int nh, int nkv, int nt, float scale, float* out, int ots, void* stream) {
+    if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, out, ots)) return -1;
+    AttnPlan p;
+    if (!plan_attn(pos0, nt, nh, nkv, KERNEL_AUTO, IT_NOALLOC_SCRATCH_BYTES, p))
+        return fail("it_attn_f16_noalloc: this geometry needs %zu bytes of partial records, more than the %zu-byte "
+                    "device scratch (use it_attn_f16 with a caller buffer)", p.bytes, (size_t)IT_NOALLOC_SCRATCH_BYTES);
+    void* scr = nullptr;
+    if (noalloc_scratch(&scr)) return -1;
+    // the same launch path as it_attn_f16 with the plan fixed: no allocation anywhere below
+    return it_attn_f16_ex(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, ots, scr, IT_NOALLOC_SCRATCH_BYTES,
+                          p.kernel, p.kernel == KERNEL_FLASH && p.chunk == 0 ? (1 << 30) : p.chunk, stream);
 }
 
 int it_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
