@@ -119,6 +119,11 @@ __device__ __forceinline__ float max_xor16(float v) { float a = v, b = v; swap16
 __device__ __forceinline__ float sum_xor16(float v) { float a = v, b = v; swap16(a, b); return a + b; }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// The same on the hardware exp2 and reciprocal (a few ulp, ~1e-7 relative): for epilogues that apply
+// the gate to many values per lane, where the accurate forms (~20 VALU ops each) dominate.
+__device__ __forceinline__ float sigmoid_hw(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
 
