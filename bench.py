@@ -29,7 +29,8 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant decode kernel (attn_decode_kernel<1>, ctx 8192), from two
 # rocprofv3 --pmc runs of `bench.py --only decode` scaled by a 256 MiB copy's readings:
-# FETCH_SIZE 8,311.0 KiB x 2.0 + WRITE_SIZE 2,112 KiB x 1.0 (profiles/attn_decode_ctx8192.md).
+# FETCH_SIZE 8,305.0 KiB x 2.0 + WRITE_SIZE 2,112 KiB x 1.0, re-measured on the current build (the
+# counter table of profiles/attn_decode_ctx8192.md; a --pmc run cannot share the timed process).
 DECODE_TRAFFIC_BYTES = int((8305.0 * 2.0 + 2112.0 * 1.0) * 1024)
 F16_MFMA_PEAK_TFLOPS = 2500.0
 NH, NKV, HD = 16, 2, 256
