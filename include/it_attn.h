@@ -292,7 +292,9 @@ int it_gdn_rollback(const float* ck_conv, float* conv_state, size_t conv_words, 
 /* Same contract and result as it_gdn_step over nt tokens, computed with the chunk-64 WY/UT form of
  * the gated delta rule on f16 MFMA with f32 state and accumulation (a new algorithm: the reference
  * runs the recurrence token-sequentially, kernels/src/lib.rs:285-331). Scratch as returned by
- * it_gdn_chunked_scratch_bytes. */
+ * it_gdn_chunked_scratch_bytes. The q and k heads must be L2-normalised, as the layer's rmsnorm
+ * mode 2 leaves them before the recurrence (cpu.rs:214): the chunk operands are kept as f16, which
+ * assumes |k| <= 1 (it_gdn_step has no such bound). */
 size_t it_gdn_chunked_scratch_bytes(int nt, int nv, int S);
 int it_gdn_chunked(const float* co, int co_tok_stride, const float* beta_raw, const float* alpha_raw,
                    int ba_tok_stride, const float* dt, const float* a, float* state, float* out,

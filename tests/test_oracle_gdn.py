@@ -195,3 +195,19 @@ def test_conv_oracle_kparity_inputs():
     np.testing.assert_allclose(out, o64, atol=1e-6)
     np.testing.assert_array_equal(st, x[-3:])
     np.testing.assert_array_equal(s64.astype(np.float32), x[-3:])
+
+
+def test_oracle_gdn_kparity_inputs():
+    """The oracle recurrence on the reference's kernel-parity gdn inputs (kparity.rs:35, unnormalised
+    q/k) against the float64 recurrence, relative to max(1, |x|) as the harness measures."""
+    MB = 1 << 20
+    a, p = oracle.kparity_draws(5 << 20, 1 << 16)
+    p = p.copy()
+    p[16:20] = -np.abs(p[16:20]) - 0.1
+    co = a[:6 * 1024].reshape(6, 1024)
+    br, ar = a[MB:MB + 24].reshape(6, 4), a[MB + 64:MB + 88].reshape(6, 4)
+    st = a[2 * MB:2 * MB + 4 * 128 * 128].reshape(4, 128, 128)
+    out, sn = oracle.gdn_step(co, br, ar, p[0:4], p[16:20], st, 4, 2)
+    o64, s64 = gdn_seq_f64(co, br, ar, p[0:4], p[16:20], st, 4, 2)
+    rel = lambda x, y: np.max(np.abs(x - y) / np.maximum(1.0, np.abs(y)))
+    assert rel(out, o64) <= 1e-4 and rel(sn, s64) <= 1e-4
