@@ -1,0 +1,179 @@
+// Engine-shaped C++ caller of the C ABI (include/it_attn.h), the way the reference's Vulkan engine
+// drives its attention and Gated-DeltaNet dispatches (src/vk/mod.rs:544-566, 790-806, 839, 896):
+// one caller-owned device arena addressed by word offsets, a prompt split by prefill_chunks
+// (it_prefill_chunks, vk/mod.rs:130-134), each attention call given exactly the arena room the
+// reference reserves for its dispatch (attention_dispatch_room, vk/mod.rs:148) as scratch, then
+// decode tokens one at a time with the one-launch GDN layer and its ping-pong conv state.
+//
+// Test driver only (tests/test_gpu_engine_harness.py builds the inputs and checks the outputs
+// against the oracle). Usage: engine_harness DIR T_PROMPT T_DECODE UBATCH
+//   DIR holds q.bin k.bin v.bin (attention inputs, f32 [T][...]) and x.bin w.bin cst.bin st.bin
+//   br.bin ar.bin dt.bin a.bin (GDN inputs); attn_out.bin gdn_out.bin state_out.bin cst_out.bin are
+//   written back. Geometry: 16 q / 2 KV heads, head_dim 256; 32 V / 16 QK heads, state 128, conv 4.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+#include <vector>
+
+#include "../../include/it_attn.h"
+
+namespace {
+
+constexpr int NH = 16, NKV = 2, HD = 256, KVD = NKV * HD, QTS = NH * 2 * HD, OTS = NH * HD;
+constexpr int NV = 32, NK = 16, S = 128, CD = (2 * NK + NV) * S, KC = 4;
+constexpr float EPS = 1e-6f;
+
+#define HIPCHECK(x)                                                                                  \
+    do {                                                                                             \
+        hipError_t e_ = (x);                                                                         \
+        if (e_ != hipSuccess) {                                                                      \
+            std::fprintf(stderr, "%s:%d %s: %s\n", __FILE__, __LINE__, #x, hipGetErrorString(e_)); \
+            std::exit(2);                                                                            \
+        }                                                                                            \
+    } while (0)
+#define ITCHECK(x)                                                                              \
+    do {                                                                                        \
+        if ((x) != 0) {                                                                         \
+            std::fprintf(stderr, "%s:%d %s failed: %s\n", __FILE__, __LINE__, #x, it_last_error()); \
+            std::exit(3);                                                                       \
+        }                                                                                       \
+    } while (0)
+
+std::vector<float> read_file(const std::string& path, size_t n) {
+    std::vector<float> v(n);
+    FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f || std::fread(v.data(), sizeof(float), n, f) != n) {
+        std::fprintf(stderr, "cannot read %zu floats from %s\n", n, path.c_str());
+        std::exit(4);
+    }
+    std::fclose(f);
+    return v;
+}
+void write_file(const std::string& path, const float* d, size_t n) {
+    FILE* f = std::fopen(path.c_str(), "wb");
+    if (!f || std::fwrite(d, sizeof(float), n, f) != n) {
+        std::fprintf(stderr, "cannot write %s\n", path.c_str());
+        std::exit(4);
+    }
+    std::fclose(f);
+}
+
+// Word offsets into the arena (f32 words; the f16 KV caches take kvd/2 words a position).
+struct Layout {
+    size_t q, k, v, kc, vc, aout, scr, x, w, cst0, cst1, st, br, ar, dt, a, co, gout, gscr, words;
+};
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc < 5) {
+        std::fprintf(stderr, "usage: engine_harness DIR T_PROMPT T_DECODE UBATCH\n");
+        return 1;
+    }
+    const std::string dir = argv[1];
+    const int tp = std::atoi(argv[2]), td = std::atoi(argv[3]), ub = std::atoi(argv[4]);
+    const int T = tp + td, ctx = T;   // context capacity of the engine = the whole sequence
+
+    Layout L{};
+    size_t o = 0;
+    auto take = [&](size_t words) { const size_t at = o; o += (words + 63) / 64 * 64; return at; };
+    L.q = take((size_t)T * QTS);
+    L.k = take((size_t)T * KVD);
+    L.v = take((size_t)T * KVD);
+    L.kc = take((size_t)ctx * KVD / 2);
+    L.vc = take((size_t)ctx * KVD / 2);
+    L.aout = take((size_t)T * OTS);
+    L.scr = take(it_attention_scratch_words(ctx, NH));   // the arena's split-K reservation (vk/mod.rs:138)
+    L.x = take((size_t)T * CD);
+    L.w = take((size_t)CD * KC);
+    L.cst0 = take((size_t)(KC - 1) * CD);
+    L.cst1 = take((size_t)(KC - 1) * CD);
+    L.st = take((size_t)NV * S * S);
+    L.br = take((size_t)T * NV);
+    L.ar = take((size_t)T * NV);
+    L.dt = take(NV);
+    L.a = take(NV);
+    L.co = take((size_t)ub * CD);
+    L.gout = take((size_t)T * NV * S);
+    L.gscr = take((it_gdn_chunked_scratch_bytes(ub, NV, S) + 3) / 4);
+    L.words = o;
+
+    float* arena = nullptr;
+    HIPCHECK(hipMalloc(&arena, L.words * sizeof(float)));
+    hipStream_t s;
+    HIPCHECK(hipStreamCreate(&s));
+    auto up = [&](size_t off, const char* name, size_t n) {
+        const std::vector<float> h = read_file(dir + "/" + name, n);
+        HIPCHECK(hipMemcpy(arena + off, h.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    };
+    up(L.q, "q.bin", (size_t)T * QTS);
+    up(L.k, "k.bin", (size_t)T * KVD);
+    up(L.v, "v.bin", (size_t)T * KVD);
+    up(L.x, "x.bin", (size_t)T * CD);
+    up(L.w, "w.bin", (size_t)CD * KC);
+    up(L.cst0, "cst.bin", (size_t)(KC - 1) * CD);
+    up(L.st, "st.bin", (size_t)NV * S * S);
+    up(L.br, "br.bin", (size_t)T * NV);
+    up(L.ar, "ar.bin", (size_t)T * NV);
+    up(L.dt, "dt.bin", NV);
+    up(L.a, "a.bin", NV);
+
+    auto a = [&](size_t off) { return arena + off; };
+    uint16_t* kc = (uint16_t*)(arena + L.kc);
+    uint16_t* vc = (uint16_t*)(arena + L.vc);
+    const size_t gscr_bytes = it_gdn_chunked_scratch_bytes(ub, NV, S);
+
+    // one attention layer call and one GDN layer call for tokens [t0, t0 + nt)
+    auto attention = [&](int t0, int nt) {
+        const size_t room = it_attention_dispatch_room(ctx, NH, nt) * sizeof(float);
+        ITCHECK(it_kv_append_f16(a(L.k + (size_t)t0 * KVD), a(L.v + (size_t)t0 * KVD), KVD, kc, vc, t0, nt, KVD, 0, s));
+        ITCHECK(it_attn_f16(a(L.q + (size_t)t0 * QTS), QTS, kc, vc, KVD, t0, HD, NH, NKV, nt, 0.0625f,
+                            a(L.aout + (size_t)t0 * OTS), OTS, a(L.scr), room, s));
+    };
+
+    // ---- prefill: the reference's chunk loop (vk/mod.rs:896)
+    const long nr = it_prefill_chunks(tp, ub, nullptr, nullptr, 0);
+    if (nr < 0) { std::fprintf(stderr, "it_prefill_chunks: %s\n", it_last_error()); return 3; }
+    std::vector<size_t> starts(nr > 0 ? nr : 1), lens(nr > 0 ? nr : 1);
+    it_prefill_chunks(tp, ub, starts.data(), lens.data(), nr);
+    for (long i = 0; i < nr; ++i) {
+        const int t0 = (int)starts[i], nt = (int)lens[i];
+        attention(t0, nt);
+        // GDN layer: conv + q/k L2 (vk/mod.rs:803-804), then the recurrence (806): the chunk-64 scan
+        // for full chunks, the token-sequential kernel for short ones
+        ITCHECK(it_gdn_conv_l2norm(a(L.x + (size_t)t0 * CD), CD, a(L.w), a(L.cst0), a(L.co), CD, CD, nt, KC, 2 * NK, EPS,
+                                   s));
+        if (nt >= 64)
+            ITCHECK(it_gdn_chunked(a(L.co), CD, a(L.br + (size_t)t0 * NV), a(L.ar + (size_t)t0 * NV), NV, a(L.dt), a(L.a),
+                                   a(L.st), a(L.gout + (size_t)t0 * NV * S), NV * S, nt, NV, NK, S, a(L.gscr), gscr_bytes, s));
+        else
+            ITCHECK(it_gdn_step(a(L.co), CD, a(L.br + (size_t)t0 * NV), a(L.ar + (size_t)t0 * NV), NV, a(L.dt), a(L.a),
+                                a(L.st), a(L.gout + (size_t)t0 * NV * S), NV * S, nt, NV, NK, S, s));
+    }
+    // ---- decode: one token per call; the GDN layer in one launch with the conv state alternating
+    // between two arena slots
+    int p = 0;
+    for (int t = tp; t < T; ++t) {
+        attention(t, 1);
+        ITCHECK(it_gdn_decode_fused(a(L.x + (size_t)t * CD), CD, a(L.w), KC, a(p ? L.cst1 : L.cst0), a(p ? L.cst0 : L.cst1),
+                                    a(L.br + (size_t)t * NV), a(L.ar + (size_t)t * NV), NV, a(L.dt), a(L.a), a(L.st),
+                                    a(L.gout + (size_t)t * NV * S), NV * S, 1, NV, NK, S, EPS, s));
+        p ^= 1;
+    }
+    HIPCHECK(hipStreamSynchronize(s));
+
+    auto down = [&](size_t off, const char* name, size_t n) {
+        std::vector<float> h(n);
+        HIPCHECK(hipMemcpy(h.data(), arena + off, n * sizeof(float), hipMemcpyDeviceToHost));
+        write_file(dir + "/" + name, h.data(), n);
+    };
+    down(L.aout, "attn_out.bin", (size_t)T * OTS);
+    down(L.gout, "gdn_out.bin", (size_t)T * NV * S);
+    down(L.st, "state_out.bin", (size_t)NV * S * S);
+    down(p ? L.cst1 : L.cst0, "cst_out.bin", (size_t)(KC - 1) * CD);
+    std::printf("ok %ld prefill calls, %d decode steps, arena %zu MiB\n", nr, td, L.words * 4 >> 20);
+    HIPCHECK(hipFree(arena));
+    return 0;
+}
