@@ -305,7 +305,9 @@ int it_gdn_chunked(const float* co, int co_tok_stride, const float* beta_raw, co
  * Reference-shaped dispatch policy (pure host functions, no device access).
  * ---------------------------------------------------------------------------------------------- */
 
-/* 64*heads*max(ctx,260): split-K partial words reserved per layer arena (src/vk/mod.rs:138). */
+/* 64*heads*max(ctx,260) (src/vk/mod.rs:138): the arena's scratch words for a 64-token batch. An
+ * arena for larger chunks holds it_attention_dispatch_room(ctx, heads, ubatch) words, as the
+ * reference's scr slot does (src/vk/mod.rs:546). */
 size_t it_attention_scratch_words(size_t ctx, size_t heads);
 /* ceil(nt/64)*64*heads*max(ctx,260), nt in 1..=512 (src/vk/mod.rs:148-150); 0 if nt is invalid. */
 size_t it_attention_dispatch_room(size_t ctx, size_t heads, size_t nt);

@@ -85,7 +85,9 @@ int main(int argc, char** argv) {
     L.kc = take((size_t)ctx * KVD / 2);
     L.vc = take((size_t)ctx * KVD / 2);
     L.aout = take((size_t)T * OTS);
-    L.scr = take(it_attention_scratch_words(ctx, NH));   // the arena's split-K reservation (vk/mod.rs:138)
+    // the arena's attention scratch: ubatch x heads x max(ctx, 260) words (vk/mod.rs:546), which is
+    // the dispatch room of the largest chunk; it_attention_scratch_words is only the 64-token case
+    L.scr = take(it_attention_dispatch_room(ctx, NH, ub));
     L.x = take((size_t)T * CD);
     L.w = take((size_t)CD * KC);
     L.cst0 = take((size_t)(KC - 1) * CD);

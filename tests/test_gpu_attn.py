@@ -189,7 +189,8 @@ def test_two_phase_abi_equals_single_call(dev):
 
 
 @pytest.mark.parametrize("pos0,nt,cap", [(3968, 64, 8192), (4032, 64, 8192), (8128, 64, 8192), (3977, 64, 4041),
-                                         (245, 13, 258), (8188, 4, 8192), (4096, 64, 0)])
+                                         (245, 13, 258), (8188, 4, 8192), (4096, 64, 0), (7680, 512, 8192),
+                                         (7000, 300, 7300)])
 def test_reference_room_is_enough(dev, pos0, nt, cap):
     """it_attn_f16 with scratch of exactly the reference arena's room (attention_dispatch_room at
     capacity `cap`, src/vk/mod.rs:148-150, 714-716; cap 0 = no scratch at all): the split grows until

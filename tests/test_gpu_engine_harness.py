@@ -18,7 +18,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "tests", "csrc", "engine_harness")
 
 
-@pytest.mark.parametrize("tp,td,ub", [(200, 3, 64), (150, 2, 128)])
+@pytest.mark.parametrize("tp,td,ub", [(200, 3, 64), (150, 2, 128), (600, 2, 512)])
 def test_engine_harness_matches_oracle(tmp_path, tp, td, ub):
     if not os.path.exists(EXE):
         pytest.fail(f"{EXE} is not built (__graft_entry__.build() runs make -C tests/csrc)")
