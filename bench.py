@@ -193,6 +193,24 @@ def main():
         res["decode_ctx8192_GBs"] = round(value_gbs, 1)
         log(f"decode ctx8192: {us_layer:.2f} us/layer, {value_gbs:.0f} GB/s")
 
+        # the same decode layer in one launch through a mailbox (it_attn_f16_mailbox), a named extra
+        mbox = ops.attn_mailbox(ctx, 1, NH, dev)
+
+        def decode_one_launch(i):
+            call("it_attn_f16_mailbox", q1.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(),
+                 vcs[i % NSETS].data_ptr(), KVD, ctx - 1, HD, NH, NKV, 1, scale, out.data_ptr(), NH * HD,
+                 mbox.data_ptr(), mbox.numel(), part.data_ptr(), part.numel(), stream_of())
+
+        assert ops.attn_mailbox_would_launch(ctx - 1, 1, NH, NKV, mbox)
+        decode_one_launch(0)
+        torch.cuda.synchronize()
+        if not args.decode_chunk:   # same 64-key splits and merge order as the two-launch path
+            assert torch.equal(out[:1], ref_out), "one-launch decode differs from the two-launch result"
+        ms = graph_time_ms(torch, lambda: [decode_one_launch(i) for i in range(K)], reps=3)
+        assert not ops.attn_mailbox_poisoned(mbox)
+        res["decode_ctx8192_one_launch_us_per_layer"] = round(ms * 1000.0 / K, 3)
+        log(f"decode ctx8192 in one launch (mailbox): {ms * 1000.0 / K:.2f} us/layer")
+
         # dominant kernel alone: the split-K partial kernel, K launches per graph
         ms_part = graph_time_ms(torch, lambda: [decode_partials(i) for i in range(K)], reps=3)
         part_us = ms_part * 1000.0 / K

@@ -117,6 +117,32 @@ int it_attn_f16_noalloc(const float* q, int q_tok_stride, const uint16_t* kc, co
                         int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
                         void* stream);
 
+/* Decode attention in one launch. Replaces the same reference call as it_attn_f16 for decode
+ * (VkEngine::attention_kv, src/vk/mod.rs:710-729: the attn_s_h partial dispatch and attn_comb,
+ * kernels/src/lib.rs:722-798), with the split records and their merge in one kernel: each split
+ * writes its record to a caller-owned mailbox, per 16 output dims, and the waves that merge a
+ * (token, head, 16 dims) unit wait for exactly the pieces they read. Results are bit-identical to
+ * it_attn_f16's. Taken when the geometry qualifies: a split-K call (nt < 16) with at most 8 query
+ * rows per KV head (nt * nh / nkv <= 8: decode), at most 256 splits of 64 keys (pos0 + nt <= 16384),
+ * a mailbox of at least it_attn_mailbox_bytes(pos0 + nt, nt, nh) bytes, and a grid the device
+ * holds at once (so every piece a merge waits for is being produced). Any other call runs
+ * it_attn_f16 with `scratch` / `scratch_bytes`; it_attn_mailbox_would_launch reports which.
+ *
+ * The mailbox: 16-byte aligned device memory, initialised once with it_attn_mailbox_init and left
+ * initialised by every call (each merge clears what it read). One mailbox serves any sequence of
+ * calls in order on one stream (every layer and step of an engine); calls that overlap on the
+ * device (other streams, concurrent graph replays) need one each. A merge that has waited 10 ms
+ * (possible only if other work holds the device's compute units) gives up, writes NaN outputs and
+ * poisons the mailbox: every later call then gives NaN at once until it_attn_mailbox_init runs
+ * again; it_attn_mailbox_poisoned reports the flag. */
+size_t it_attn_mailbox_bytes(int ctx, int nt, int nh);
+int it_attn_mailbox_init(void* mailbox, size_t bytes, void* stream);
+int it_attn_mailbox_poisoned(const void* mailbox, int* poisoned, void* stream);   /* synchronises stream */
+int it_attn_mailbox_would_launch(int pos0, int nt, int hd, int nh, int nkv, size_t mailbox_bytes);
+int it_attn_f16_mailbox(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,
+                        int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
+                        void* mailbox, size_t mailbox_bytes, void* scratch, size_t scratch_bytes, void* stream);
+
 /* The choice it_attn_f16 makes for this geometry and scratch budget: *kernel 1 (split-K) or 2
  * (flash), *chunk keys per split (0 = flash in one pass, no scratch), *bytes of scratch used.
  * Returns nonzero if no split fits (only possible for nt < 16 with fewer than nt*nh*1040 bytes).

@@ -328,6 +328,55 @@ int it_attn_f16_noalloc(const float* q, int qts, const uint16_t* kc, const uint1
                           p.kernel, p.kernel == KERNEL_FLASH && p.chunk == 0 ? (1 << 30) : p.chunk, stream);
 }
 
+size_t it_attn_mailbox_bytes(int ctx, int nt, int nh) {
+    if (ctx <= 0 || nt <= 0 || nh <= 0) return 0;
+    return it::mailbox_bytes(ctx, nt, nh);
+}
+
+int it_attn_mailbox_init(void* mailbox, size_t bytes, void* stream) {
+    if (!mailbox || bytes < it::mailbox_bytes(1, 1, 1) || bytes % 4) return fail("it_attn_mailbox_init: bad buffer");
+    if (!aligned16(mailbox)) return fail("it_attn_mailbox_init: the mailbox must be 16-byte aligned");
+    return check(it::launch_mailbox_fill(mailbox, bytes, (hipStream_t)stream), "it_attn_mailbox_init");
+}
+
+int it_attn_mailbox_poisoned(const void* mailbox, int* poisoned, void* stream) {
+    if (!mailbox || !poisoned) return fail("it_attn_mailbox_poisoned: null argument");
+    uint32_t w = 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (check(hipMemcpyAsync(&w, mailbox, 4, hipMemcpyDeviceToHost, st), "it_attn_mailbox_poisoned")) return -1;
+    if (check(hipStreamSynchronize(st), "it_attn_mailbox_poisoned")) return -1;
+    *poisoned = w != 0;
+    return 0;
+}
+
+int it_attn_mailbox_would_launch(int pos0, int nt, int hd, int nh, int nkv, size_t mailbox_bytes) {
+    if (hd != HD || nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv) return 0;
+    if (auto_kernel(nt) != KERNEL_SPLITK) return 0;
+    bool launched = false;
+    float dummy;
+    if (it::launch_attn_decode_mailbox(nullptr, 0, nullptr, nullptr, nkv * HD, pos0, nh, nkv, nt, 0.f, nullptr, 0,
+                                       &dummy, mailbox_bytes, nullptr, &launched, true) != hipSuccess)
+        return 0;
+    return launched ? 1 : 0;
+}
+
+int it_attn_f16_mailbox(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd,
+                        int nh, int nkv, int nt, float scale, float* out, int ots, void* mailbox, size_t mailbox_bytes,
+                        void* scratch, size_t scratch_bytes, void* stream) {
+    if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, out, ots)) return -1;
+    if (mailbox && !aligned16(mailbox)) return fail("it_attn_f16_mailbox: the mailbox must be 16-byte aligned");
+    if (auto_kernel(nt) == KERNEL_SPLITK) {
+        bool launched = false;
+        if (check(it::launch_attn_decode_mailbox(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots,
+                                                 (float*)mailbox, mailbox ? mailbox_bytes : 0, (hipStream_t)stream,
+                                                 &launched),
+                  "it_attn_f16_mailbox"))
+            return -1;
+        if (launched) return 0;
+    }
+    return it_attn_f16(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, ots, scratch, scratch_bytes, stream);
+}
+
 int it_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
                      int nkv, int nt, float scale, float* part, size_t part_bytes, int chunk, void* stream) {
     if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, q, qts)) return -1;

@@ -25,6 +25,9 @@
 // is in flight, then V goes out and the scores and softmax run while it lands; later tiles are
 // prefetched while P.V runs. MULTI = false (splits of one tile) declares a single V buffer, which
 // lets two or three workgroups share a CU.
+#include <algorithm>
+#include <atomic>
+
 #include "common.h"
 #include "internal.h"
 
@@ -77,11 +80,51 @@ template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
 
 }  // namespace
 
-template <int NB, bool MULTI>
+// ------------------------------------------------------------------------------------------------
+// Mailbox for decode in one launch. The split records go, per 16-dim block, into pieces
+// {o[16], m, l, -, -} of a caller-owned buffer whose words all hold MB_EMPTY between calls (an f32
+// NaN pattern no arithmetic produces: generated NaNs are the canonical quiet NaN, and an f16 NaN
+// widened keeps its low 13 bits zero). Pieces are written and read device-coherently (past the
+// per-XCD L2), and each word is checked on its own, so no flag, fence or store ordering is needed:
+// a piece is complete when none of its 18 words is MB_EMPTY. The merging wave then writes
+// MB_EMPTY back, which leaves the buffer ready for the next call. Word 0 of the buffer is the
+// poison flag, set by a merge that gave up waiting.
+constexpr int MB_PIECE = 20;        // floats per piece
+constexpr int MB_HEAD = 64;         // floats before the first piece
+constexpr uint32_t MB_EMPTY = 0xFFFFFFFFu;
+constexpr int MB_COHERENT = 16;     // buffer cache-policy bit: device-coherent access
+constexpr uint64_t MB_SPIN_TICKS = 1000000;   // 10 ms of the 100 MHz real-time counter
+typedef __amdgpu_buffer_rsrc_t MbRsrc;
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ MbRsrc mb_rsrc(float* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, (int)bytes, 0x00020000);
+}
+// float index of piece (row th, dim block db, split s)
+__device__ __forceinline__ int mb_piece(int th, int db, int s, int smax) {
+    return MB_HEAD + ((th * 16 + db) * smax + s) * MB_PIECE;
+}
+__device__ __forceinline__ void mb_store1(MbRsrc r, int idx, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, 4 * idx, 0, MB_COHERENT);
+}
+__device__ __forceinline__ void mb_store2(MbRsrc r, int idx, f2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), r, 4 * idx, 0, MB_COHERENT);
+}
+__device__ __forceinline__ void mb_store4(MbRsrc r, int idx, u4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, 4 * idx, 0, MB_COHERENT);
+}
+__device__ __forceinline__ u4 mb_load4(MbRsrc r, int idx) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, 4 * idx, 0, MB_COHERENT);
+}
+__device__ __forceinline__ u2 mb_load2(MbRsrc r, int idx) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, 4 * idx, 0, MB_COHERENT);
+}
+
+template <int NB, bool MULTI, bool MB = false>
 __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc,
                                                const uint16_t* __restrict__ vc, int kvd, int pos0, int nh, int nkv,
                                                int nt, float scale, float* __restrict__ part, int chunk, int smax,
-                                               int s, int kh, int rg) {
+                                               int s, int kh, int rg, float* mb = nullptr, uint32_t mbb = 0) {
     constexpr int ROWS = 8 * NB;
     __shared__ __align__(16) _Float16 V0[TK * HD];
     __shared__ __align__(16) _Float16 V1[MULTI ? TK * HD : 8];   // only when a split has several tiles
@@ -270,14 +313,27 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
             for (int n = 0; n < 4; ++n) v[n] = sum_xor32(acc[b][n][i]);
             const float ls = sum_xor32(lacc[b][i]);
             if (l < 32 && rb + i < R) {
-                float* rec = part + ((size_t)(tq * nh + kh * G + gq) * smax + s) * PART;
-                // blocks of 16 or more rows (verify at nt = 4) store their records non-temporally:
-                // measured faster there (15.7 -> 14.6 us per layer), slower for decode (10.3 -> 11.1)
-                if constexpr (NB >= 2) {
+                const int th = tq * nh + kh * G + gq;
+                if constexpr (MB) {
+                    // mailbox pieces of dim blocks 4w .. 4w+3: dims from every lane, {m, l} from
+                    // lanes c < 4 (one piece each); only for rows that see this split's keys
+                    // (the merge reads exactly those pieces and clears them)
+                    const MbRsrc mbr = mb_rsrc(mb, mbb);
+                    if (p0 <= pos0 + tq) {
+#pragma unroll
+                        for (int n = 0; n < 4; ++n) mb_store1(mbr, mb_piece(th, 4 * w + n, s, smax) + c, v[n]);
+                        if (c < 4) mb_store2(mbr, mb_piece(th, 4 * w + c, s, smax) + 16, f2{mh[i] * LN2_F, ls});
+                    }
+                } else if constexpr (NB >= 2) {
+                    // blocks of 16 or more rows (verify at nt = 4) store their records
+                    // non-temporally: measured faster there (15.7 -> 14.6 us per layer), slower for
+                    // decode (10.3 -> 11.1)
+                    float* rec = part + ((size_t)th * smax + s) * PART;
 #pragma unroll
                     for (int n = 0; n < 4; ++n) __builtin_nontemporal_store(v[n], rec + 4 + 64 * w + 16 * n + c);
                     if (w == 0 && c == 0) __builtin_nontemporal_store(f4{mh[i] * LN2_F, ls, 0.f, 0.f}, (f4*)rec);
                 } else {
+                    float* rec = part + ((size_t)th * smax + s) * PART;
 #pragma unroll
                     for (int n = 0; n < 4; ++n) rec[4 + 64 * w + 16 * n + c] = v[n];
                     if (w == 0 && c == 0) *(f4*)rec = f4{mh[i] * LN2_F, ls, 0.f, 0.f};
@@ -382,27 +438,17 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // need 8 + 4 + 2 + 1 + 2 exchanges instead of 16 full reductions. Lane l ends holding dim
 // 8*b5 + 4*b4 + 2*b3 + b2 (bits of l) summed over all lanes.
 
-// One wave merges the records of query row th (token t = th / nh, head h) for output dims
-// d0 .. d0+15; lane l = the wave's lane.
+// Given lane l's headers hv[j] = {m, l} and dims d0 .. d0+15 ov[j] of splits l + 64j (those at or
+// past ns masked here), merge them over the wave and store the 16 gated outputs of row (t, h).
+// The gate input of the output dim lane l ends up holding (see the butterfly below).
+__device__ __forceinline__ float merge_gate(const float* __restrict__ q, int qts, int t, int h, int d0, int l) {
+    return q[(size_t)t * qts + (size_t)h * 2 * HD + HD + d0 + 8 * (l >> 5) + 4 * ((l >> 4) & 1) + 2 * ((l >> 3) & 1) +
+             ((l >> 2) & 1)];
+}
 template <int SPL>
-__device__ __forceinline__ void combine_wave_row(const float* __restrict__ q, int qts, int pos0, int nh, int nt,
-                                                 const float* __restrict__ part, int chunk, int smax,
-                                                 float* __restrict__ out, int ots, int th, int d0, int l) {
-    if (th >= nt * nh) return;   // whole wave
-    const int t = th / nh, h = th - t * nh;
-    const int ns = (pos0 + t + chunk) / chunk;   // splits that hold keys <= pos0 + t
-    const float* base = part + (size_t)th * smax * PART;
-    f2 hv[SPL];
-    f4 ov[SPL][4];
-#pragma unroll
-    for (int j = 0; j < SPL; ++j) {
-        const float* rec = base + (size_t)min(l + 64 * j, ns - 1) * PART;
-        hv[j] = *(const f2*)rec;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) ov[j][k] = ld_f4(rec + 4 + d0 + 4 * k);
-    }
-    const float gv = q[(size_t)t * qts + (size_t)h * 2 * HD + HD + d0 + 8 * (l >> 5) + 4 * ((l >> 4) & 1) +
-                       2 * ((l >> 3) & 1) + ((l >> 2) & 1)];
+__device__ __forceinline__ void merge_wave_store(float gv, int nh, int t, int h, int ns, f2 (&hv)[SPL],
+                                                 const f4 (&ov)[SPL][4], float* __restrict__ out, int ots, int d0,
+                                                 int l) {
     float M = -INFINITY;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
@@ -459,6 +505,28 @@ __device__ __forceinline__ void combine_wave_row(const float* __restrict__ q, in
     }
 }
 
+// One wave merges the records of query row th (token t = th / nh, head h) for output dims
+// d0 .. d0+15; lane l = the wave's lane.
+template <int SPL>
+__device__ __forceinline__ void combine_wave_row(const float* __restrict__ q, int qts, int pos0, int nh, int nt,
+                                                 const float* __restrict__ part, int chunk, int smax,
+                                                 float* __restrict__ out, int ots, int th, int d0, int l) {
+    if (th >= nt * nh) return;   // whole wave
+    const int t = th / nh, h = th - t * nh;
+    const int ns = (pos0 + t + chunk) / chunk;   // splits that hold keys <= pos0 + t
+    const float* base = part + (size_t)th * smax * PART;
+    f2 hv[SPL];
+    f4 ov[SPL][4];
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        const float* rec = base + (size_t)min(l + 64 * j, ns - 1) * PART;
+        hv[j] = *(const f2*)rec;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ov[j][k] = ld_f4(rec + 4 + d0 + 4 * k);
+    }
+    merge_wave_store<SPL>(merge_gate(q, qts, t, h, d0, l), nh, t, h, ns, hv, ov, out, ots, d0, l);
+}
+
 template <int SPL>
 __global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __restrict__ q, int qts, int pos0,
                                                                 int nh, int nt, const float* __restrict__ part,
@@ -478,6 +546,103 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __r
     }
     combine_wave_row<SPL>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots, row,
                           16 * (4 * quarter + (threadIdx.x >> 6)), threadIdx.x & 63);
+}
+
+// One wave merges mailbox unit (row th, dim block db): lane l polls its pieces of splits l + 64j
+// until every word has arrived (bounded by a deadline on the real-time counter), merges as
+// combine_wave_row does, and clears the pieces it read. A poisoned mailbox, or a wait that ran out
+// (which poisons it), gives NaN outputs.
+template <int SPL>
+__device__ __forceinline__ void mailbox_merge(const float* __restrict__ q, int qts, int pos0, int nh, int chunk,
+                                              int smax, MbRsrc r, float* __restrict__ out, int ots, int th, int db,
+                                              int l) {
+    const int t = th / nh, h = th - t * nh, d0 = 16 * db;
+    const int ns = (pos0 + t + chunk) / chunk;
+    f2 hv[SPL];
+    f4 ov[SPL][4];
+    bool ok[SPL];
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        ok[j] = l + 64 * j >= ns;
+        hv[j] = f2{-INFINITY, 0.f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ov[j][k] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float gv = merge_gate(q, qts, t, h, d0, l);   // issued before the wait, used after it
+    bool bad = mb_load2(r, 0)[0] != 0u;
+    const uint64_t deadline = __builtin_amdgcn_s_memrealtime() + MB_SPIN_TICKS;
+    while (!bad) {
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            if (ok[j]) continue;
+            const int base = mb_piece(th, db, l + 64 * j, smax);
+            u4 w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) w[k] = mb_load4(r, base + 4 * k);
+            const u2 hw = mb_load2(r, base + 16);
+            bool full = hw[0] != MB_EMPTY && hw[1] != MB_EMPTY;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) full = full && w[k][e] != MB_EMPTY;
+            if (full) {
+                ok[j] = true;
+                hv[j] = __builtin_bit_cast(f2, hw);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) ov[j][k] = __builtin_bit_cast(f4, w[k]);
+            }
+        }
+        bool mine = true;
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) mine = mine && ok[j];
+        if (__all(mine)) break;
+        if (__builtin_amdgcn_s_memrealtime() > deadline) {
+            bad = true;
+            if (l == 0) mb_store2(r, 0, f2{1.f, 1.f});
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (bad) {
+        if (l < 16) out[(size_t)t * ots + (size_t)h * HD + d0 + l] = __builtin_nanf("");
+        return;
+    }
+    // clear the pieces for the next call, then merge (clearing first measured faster: the clears
+    // are issued before the merge and drain while it runs)
+    const u4 empty = u4{MB_EMPTY, MB_EMPTY, MB_EMPTY, MB_EMPTY};
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        if (l + 64 * j >= ns) continue;
+        const int base = mb_piece(th, db, l + 64 * j, smax);
+#pragma unroll
+        for (int k = 0; k < 5; ++k) mb_store4(r, base + 4 * k, empty);
+    }
+    merge_wave_store<SPL>(gv, nh, t, h, ns, hv, ov, out, ots, d0, l);
+}
+
+// Decode / verify attention in one launch: the split-K partials of decode_partial (one 64-key tile
+// per split) into the mailbox, then every wave merges its share of the (row, 16-dim block) units.
+// The host launches it only when the whole grid is co-resident, so every piece a merge waits for is
+// being produced.
+template <int NB, int SPL>
+__global__ __launch_bounds__(256) void attn_decode_mailbox_kernel(const float* __restrict__ q, int qts,
+                                                                  const uint16_t* __restrict__ kc,
+                                                                  const uint16_t* __restrict__ vc, int kvd, int pos0,
+                                                                  int nh, int nkv, int nt, float scale, int chunk,
+                                                                  int smax, float* mb, uint32_t mbb,
+                                                                  float* __restrict__ out, int ots) {
+    decode_partial<NB, false, true>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, nullptr, chunk, smax, blockIdx.x,
+                                    blockIdx.y, blockIdx.z, mb, mbb);
+    const int nwg = gridDim.x * gridDim.y * gridDim.z;
+    const int wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const MbRsrc r = mb_rsrc(mb, mbb);
+    for (int u = wg + nwg * (threadIdx.x >> 6); u < nt * nh * 16; u += 4 * nwg)
+        mailbox_merge<SPL>(q, qts, pos0, nh, chunk, smax, r, out, ots, u >> 4, u & 15, threadIdx.x & 63);
+}
+
+__global__ __launch_bounds__(256) void mailbox_fill_kernel(uint32_t* p, size_t words) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (size_t)gridDim.x * 256)
+        p[i] = i < (size_t)MB_HEAD ? 0u : MB_EMPTY;
 }
 
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
@@ -505,6 +670,68 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
         default: IT_DECODE_LAUNCH(4); break;
     }
 #undef IT_DECODE_LAUNCH
+    return hipGetLastError();
+}
+
+size_t mailbox_bytes(long ctx, int nt, int nh) {
+    const long smax = (ctx + TK - 1) / TK;
+    return 4 * ((size_t)MB_HEAD + (size_t)nt * nh * 16 * smax * MB_PIECE);
+}
+
+namespace {
+// workgroups of one mailbox kernel instantiation that fit the device at once (cached per device)
+template <int NB, int SPL>
+int mailbox_capacity() {
+    static std::atomic<int> cap[64];   // 0 = not yet queried
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int c = cap[dev].load(std::memory_order_relaxed);
+    if (c) return c;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_decode_mailbox_kernel<NB, SPL>, 256, 0) !=
+            hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    c = per_cu * cus > 0 ? per_cu * cus : -1;
+    cap[dev].store(c, std::memory_order_relaxed);
+    return c;
+}
+}  // namespace
+
+hipError_t launch_attn_decode_mailbox(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
+                                      int pos0, int nh, int nkv, int nt, float scale, float* out, int ots, float* mb,
+                                      size_t mbb, hipStream_t st, bool* launched, bool dry_run) {
+    *launched = false;
+    const int G = nh / nkv, R = nt * G;
+    const long total = (long)pos0 + nt;
+    const int smax = (int)((total + TK - 1) / TK);
+    const size_t need = mailbox_bytes(total, nt, nh);
+    // one group of at most 8 rows (decode): with more rows the merging waves wait beside
+    // workgroups still computing, and two launches measured faster (nt = 2: 12.1 against 13.8 us,
+    // nt = 4: 18.5 against 21.3 at ctx 8192)
+    if (smax > 256 || R > 8 || need > mbb || need >= (1u << 31) || !mb) return hipSuccess;
+    const int rows = 8;
+    const dim3 grid(smax, nkv, (R + rows - 1) / rows);
+    const long wgs = (long)grid.x * grid.y * grid.z;
+    const int spl = smax <= 64 ? 1 : smax <= 128 ? 2 : 4;
+#define IT_MB_CASE(SPL_)                                                                                            \
+    if (spl == SPL_) {                                                                                              \
+        if (mailbox_capacity<1, SPL_>() < wgs) return hipSuccess;                                                   \
+        *launched = true;                                                                                           \
+        if (dry_run) return hipSuccess;                                                                             \
+        attn_decode_mailbox_kernel<1, SPL_><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale,    \
+                                                                  TK, smax, mb, (uint32_t)need, out, ots);          \
+        return hipGetLastError();                                                                                   \
+    }
+    IT_MB_CASE(1) IT_MB_CASE(2) IT_MB_CASE(4)
+#undef IT_MB_CASE
+    return hipSuccess;
+}
+
+hipError_t launch_mailbox_fill(void* mb, size_t bytes, hipStream_t st) {
+    const size_t words = bytes / 4;
+    const unsigned blocks = (unsigned)std::min<size_t>((words + 255) / 256, 2048);
+    mailbox_fill_kernel<<<blocks, 256, 0, st>>>((uint32_t*)mb, words);
     return hipGetLastError();
 }
 

@@ -23,6 +23,16 @@ hipError_t launch_attn_combine(const float* q, int qts, const float* part, int p
 hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                               int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
                               hipStream_t st);
+// Decode attention in one launch through a mailbox (see decode.hip). Returns hipSuccess with
+// *launched = false, having enqueued nothing, when the geometry does not qualify (splits of 64
+// keys, at most 256 splits, at most 8 query rows per KV head, mailbox_bytes(pos0 + nt, nt, nh)
+// bytes, the whole grid co-resident on the device); with dry_run, only reports whether it would
+// launch.
+size_t mailbox_bytes(long ctx, int nt, int nh);
+hipError_t launch_attn_decode_mailbox(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
+                                      int pos0, int nh, int nkv, int nt, float scale, float* out, int ots, float* mb,
+                                      size_t mbb, hipStream_t st, bool* launched, bool dry_run = false);
+hipError_t launch_mailbox_fill(void* mb, size_t bytes, hipStream_t st);
 hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                              int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st);
 

@@ -5,6 +5,8 @@ torch's current stream. Buffer layouts and semantics are those of include/it_att
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from ._lib import call, lib
@@ -150,6 +152,55 @@ def attn_f16(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int, nh:
     nbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
     call("it_attn_f16_ex", q.data_ptr(), nh * 2 * hd, kc.data_ptr(), vc.data_ptr(), kvd, pos0, hd, nh, nkv, nt,
          float(scale), out.data_ptr(), nh * hd, _ptr(scratch), nbytes, kernel, chunk, _stream())
+    return out
+
+
+def attn_mailbox(ctx: int, nt: int, nh: int, device) -> torch.Tensor:
+    """A mailbox for attn_f16_mailbox (decode / verify rows up to nt at context up to ctx, nh
+    heads), initialised on the current stream. Keep one per stream of calls."""
+    nbytes = lib().it_attn_mailbox_bytes(ctx, nt, nh)
+    mb = torch.empty(nbytes, device=device, dtype=torch.uint8)
+    call("it_attn_mailbox_init", mb.data_ptr(), nbytes, _stream())
+    return mb
+
+
+def attn_mailbox_poisoned(mb: torch.Tensor) -> bool:
+    """True if a one-launch merge in this mailbox ever gave up waiting (synchronises the stream)."""
+    flag = ctypes.c_int(0)
+    call("it_attn_mailbox_poisoned", mb.data_ptr(), ctypes.addressof(flag), _stream())
+    return bool(flag.value)
+
+
+def attn_mailbox_would_launch(pos0: int, nt: int, nh: int, nkv: int, mailbox: torch.Tensor, hd: int = 256) -> bool:
+    """Whether attn_f16_mailbox takes the one-launch form for this geometry and mailbox."""
+    return bool(lib().it_attn_mailbox_would_launch(pos0, nt, hd, nh, nkv, mailbox.numel()))
+
+
+def attn_f16_mailbox(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int, nh: int, nkv: int,
+                     mailbox: torch.Tensor, scale: float | None = None, out: torch.Tensor | None = None,
+                     scratch: torch.Tensor | None = None) -> torch.Tensor:
+    """attn_f16 with decode in one launch through `mailbox` (attn_mailbox) where the
+    geometry allows it; otherwise the same as attn_f16 with `scratch`."""
+    _need(q, torch.float32, "q")
+    nt = q.shape[0]
+    hd = q.shape[-1] // (2 * nh)
+    kvd = nkv * hd
+    if scale is None:
+        scale = 1.0 / hd ** 0.5
+    for c in (kc, vc):
+        if c.dtype not in (torch.float16, torch.int16) or not c.is_contiguous() or c.shape[-1] != kvd:
+            raise ValueError("kc/vc must be contiguous [ctx, nkv*hd] f16")
+        if c.shape[0] < pos0 + nt:
+            raise ValueError("cache shorter than pos0 + nt")
+    if out is None:
+        out = torch.empty(nt, nh * hd, device=q.device, dtype=torch.float32)
+    _need(out, torch.float32, "out")
+    if scratch is None:
+        need = attn_scratch_bytes(pos0, nt, nh, nkv, hd)
+        scratch = torch.empty(max(need, 1), device=q.device, dtype=torch.uint8)
+    call("it_attn_f16_mailbox", q.data_ptr(), nh * 2 * hd, kc.data_ptr(), vc.data_ptr(), kvd, pos0, hd, nh, nkv, nt,
+         float(scale), out.data_ptr(), nh * hd, mailbox.data_ptr(), mailbox.numel(), scratch.data_ptr(),
+         scratch.numel(), _stream())
     return out
 
 
