@@ -126,5 +126,15 @@ __device__ __forceinline__ float sigmoid_hw(float x) {
 }
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+// SiLU, softplus and e^x on the hardware exp2 / log2 / reciprocal (a few ulp): for short serial
+// chains with one wave per SIMD, where every instruction is on the critical path.
+__device__ __forceinline__ float silu_hw(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+__device__ __forceinline__ float softplus_hw(float x) {
+    return x > 20.0f ? x : __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(x * 1.4426950408889634f)) *
+                               0.6931471805599453f;
+}
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
 }  // namespace it

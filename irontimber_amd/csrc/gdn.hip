@@ -279,13 +279,29 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
     f4 s0 = ld_f4(sb + (size_t)i0 * S + j0), s1 = ld_f4(sb + (size_t)(i0 + 1) * S + j0);
     const float scale = 1.0f / sqrtf((float)S);
     const float dth = dt[h], ah = A[h];
-    for (int t = 0; t < nt; ++t) {
+    // token inputs one token ahead: token t + 1's loads are issued before token t's barriers, so a
+    // run of tokens waits for memory once instead of once per token
+    struct Tok { float q0, q1, k0, k1; f4 v; float b, a; };
+    auto load_tok = [&](int t) {
         const float* c = co + (size_t)t * cts;
-        const float q0 = c[kh * S + i0], q1 = c[kh * S + i0 + 1];
-        const float k0 = c[qk + kh * S + i0], k1 = c[qk + kh * S + i0 + 1];
-        const f4 v = ld_f4(c + 2 * qk + h * S + j0);
-        const float beta = sigmoidf_(br[(size_t)t * bts + h]);
-        const float eg = expf(softplusf_(ar[(size_t)t * bts + h] + dth) * ah);
+        Tok r;
+        r.q0 = c[kh * S + i0];
+        r.q1 = c[kh * S + i0 + 1];
+        r.k0 = c[qk + kh * S + i0];
+        r.k1 = c[qk + kh * S + i0 + 1];
+        r.v = ld_f4(c + 2 * qk + h * S + j0);
+        r.b = br[(size_t)t * bts + h];
+        r.a = ar[(size_t)t * bts + h];
+        return r;
+    };
+    Tok nx = load_tok(0);
+    for (int t = 0; t < nt; ++t) {
+        const Tok cur = nx;
+        if (t + 1 < nt) nx = load_tok(t + 1);
+        const float q0 = cur.q0, q1 = cur.q1, k0 = cur.k0, k1 = cur.k1;
+        const f4 v = cur.v;
+        const float beta = sigmoid_hw(cur.b);
+        const float eg = exp_hw(softplus_hw(cur.a + dth) * ah);
         s0 *= eg; s1 *= eg;
         f4 p = s0 * k0 + s1 * k1;
 #pragma unroll
@@ -323,8 +339,10 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
 // cover 16 distinct rows per wave, then the 4 waves through LDS). The new conv state goes to a
 // separate buffer (reading and rewriting one buffer would race between workgroups): q/k channels
 // by the first column block of the QK head's first V head, v channels by row pair 0 of each
-// workgroup. Arithmetic order of the conv and of the step as in gdn_conv_l2_kernel and
-// gdn_step_kernel; the norms' sums are added in another order (last-bit differences).
+// workgroup. With one wave per SIMD every instruction is on the critical path, so the activations
+// use the hardware exp2 / log2 / reciprocal (a few ulp), and the q/k norms, being per-head scalars,
+// are applied after the S k and S^T q sums: their sums of squares share the S k exchange (two
+// barriers a token instead of three). Results agree with conv + L2 + gdn_step_kernel to rounding.
 constexpr int FUSED_TMAX = 4;
 
 template <int K>
@@ -390,6 +408,13 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
         wnk[i] = *(const f2*)(cst_in + (size_t)i * cd + ck);
         wnv[i] = ld_f4(cst_in + (size_t)i * cd + cv);
     }
+    // the gate inputs too: loaded inside the loop they would wait behind the norm barrier
+    float brt[FUSED_TMAX], art[FUSED_TMAX];
+#pragma unroll
+    for (int t = 0; t < FUSED_TMAX; ++t) {
+        brt[t] = br[(size_t)min(t, nt - 1) * bts + h];
+        art[t] = ar[(size_t)min(t, nt - 1) * bts + h];
+    }
     const float scale = 1.0f / sqrtf((float)S);
     const float dth = dt[h], ah = A[h];
 #pragma unroll
@@ -405,8 +430,8 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
             for (int i = 0; i < K - 1; ++i) { a += wnq[i][e] * wq[e][i]; b += wnk[i][e] * wk[e][i]; }
             a += xq[t][e] * wq[e][K - 1];
             b += xk[t][e] * wk[e][K - 1];
-            q[e] = siluf_(a);
-            k[e] = siluf_(b);
+            q[e] = silu_hw(a);
+            k[e] = silu_hw(b);
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -414,31 +439,31 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
 #pragma unroll
             for (int i = 0; i < K - 1; ++i) a += wnv[i][e] * wv[e][i];
             a += xv[t][e] * wv[e][K - 1];
-            v[e] = siluf_(a);
+            v[e] = silu_hw(a);
         }
 #pragma unroll
         for (int i = 0; i + 1 < K - 1; ++i) { wnq[i] = wnq[i + 1]; wnk[i] = wnk[i + 1]; wnv[i] = wnv[i + 1]; }
         wnq[K - 2] = xq[t];
         wnk[K - 2] = xk[t];
         wnv[K - 2] = xv[t];
-        // ---- L2 norms of the q and k heads
+        // ---- recurrence (gdn_step_kernel) with the q/k L2 norms folded in: the head norms are
+        // scalars, so S k = |k| * S k_raw-hat and S^T q likewise; their sums of squares ride in the
+        // same LDS exchange as S k (one barrier fewer than normalising first)
+        const float beta = sigmoid_hw(brt[t]);
+        const float eg = exp_hw(softplus_hw(art[t] + dth) * ah);
+        s0 *= eg; s1 *= eg;
+        f4 p = s0 * k[0] + s1 * k[1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = sum_lanes_stride4(p[j]);
         const float sq = sum_lanes_stride4(q[0] * q[0] + q[1] * q[1]);
         const float sk2 = sum_lanes_stride4(k[0] * k[0] + k[1] * k[1]);
+        if (l < 4) red1[w][l] = p;
         if (l == 0) nrm[t & 1][w] = f2{sq, sk2};
         __syncthreads();
         const f2 n = (nrm[t & 1][0] + nrm[t & 1][1]) + (nrm[t & 1][2] + nrm[t & 1][3]);
         const float fq = 1.0f / fmaxf(sqrtf(n[0]), eps), fk = 1.0f / fmaxf(sqrtf(n[1]), eps);
         const float q0 = q[0] * fq, q1 = q[1] * fq, k0 = k[0] * fk, k1 = k[1] * fk;
-        // ---- recurrence (gdn_step_kernel)
-        const float beta = sigmoidf_(br[(size_t)t * bts + h]);
-        const float eg = expf(softplusf_(ar[(size_t)t * bts + h] + dth) * ah);
-        s0 *= eg; s1 *= eg;
-        f4 p = s0 * k0 + s1 * k1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = sum_lanes_stride4(p[j]);
-        if (l < 4) red1[w][l] = p;
-        __syncthreads();
-        const f4 skv = red1[0][cg] + red1[1][cg] + red1[2][cg] + red1[3][cg];
+        const f4 skv = (red1[0][cg] + red1[1][cg] + red1[2][cg] + red1[3][cg]) * fk;
         const f4 delta = (v - skv) * beta;
         s0 += k0 * delta; s1 += k1 * delta;
         f4 o = s0 * q0 + s1 * q1;
@@ -546,18 +571,31 @@ __global__ __launch_bounds__(256) void gdn_step_head_kernel(
     const float* zb = z ? z : co;
     const int zstride = z ? zts : 0;
     const f4 wv = ld_f4((z ? nw : co) + j0);
-    for (int t = 0; t < nt; ++t) {
+    // token inputs one token ahead (issued before the previous token's barriers)
+    struct Tok { f4 q[R / 4], k[R / 4], v, z; float b, a; };
+    auto load_tok = [&](int t) {
         const float* c = co + (size_t)t * cts;
-        f4 q[R / 4], k[R / 4];
+        Tok r;
 #pragma unroll
-        for (int r = 0; r < R / 4; ++r) {
-            q[r] = ld_f4(c + kh * S + i0 + 4 * r);
-            k[r] = ld_f4(c + qk + kh * S + i0 + 4 * r);
+        for (int i = 0; i < R / 4; ++i) {
+            r.q[i] = ld_f4(c + kh * S + i0 + 4 * i);
+            r.k[i] = ld_f4(c + qk + kh * S + i0 + 4 * i);
         }
-        const f4 v = ld_f4(c + 2 * qk + h * S + j0);
-        const f4 zv = ld_f4(zb + (size_t)t * zstride + (z ? (size_t)h * S : 0) + j0);   // issued with the token's loads
-        const float beta = sigmoidf_(br[(size_t)t * bts + h]);
-        const float eg = expf(softplusf_(ar[(size_t)t * bts + h] + dth) * ah);
+        r.v = ld_f4(c + 2 * qk + h * S + j0);
+        r.z = ld_f4(zb + (size_t)t * zstride + (z ? (size_t)h * S : 0) + j0);
+        r.b = br[(size_t)t * bts + h];
+        r.a = ar[(size_t)t * bts + h];
+        return r;
+    };
+    Tok nx = load_tok(0);
+    for (int t = 0; t < nt; ++t) {
+        const Tok cur = nx;
+        if (t + 1 < nt) nx = load_tok(t + 1);
+        const f4 (&q)[R / 4] = cur.q;
+        const f4 (&k)[R / 4] = cur.k;
+        const f4 v = cur.v, zv = cur.z;
+        const float beta = sigmoid_hw(cur.b);
+        const float eg = exp_hw(softplus_hw(cur.a + dth) * ah);
         f4 p = {};
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -588,7 +626,7 @@ __global__ __launch_bounds__(256) void gdn_step_head_kernel(
                 const float ss = wave_sum(ot[0] * ot[0] + ot[1] * ot[1] + ot[2] * ot[2] + ot[3] * ot[3]) * 0.5f;
                 const float sc = 1.0f / sqrtf(ss * (1.0f / S) + eps);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) res[j] = (ot[j] * sc) * wv[j] * siluf_(zv[j]);
+                for (int j = 0; j < 4; ++j) res[j] = (ot[j] * sc) * wv[j] * silu_hw(zv[j]);
             }
             if (l < 32) *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = res;
         }
