@@ -81,15 +81,15 @@ template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
 }  // namespace
 
 // ------------------------------------------------------------------------------------------------
-// Mailbox for decode in one launch. The split records go, per 16-dim block, into pieces
-// {o[16], m, l, -, -} of a caller-owned buffer whose words all hold MB_EMPTY between calls (an f32
+// Mailbox for decode in one launch. The split records go, per 16-dim block, into 96-byte pieces
+// {o[16], m, l, unused} of a caller-owned buffer whose words all hold MB_EMPTY between calls (an f32
 // NaN pattern no arithmetic produces: generated NaNs are the canonical quiet NaN, and an f16 NaN
 // widened keeps its low 13 bits zero). Pieces are written and read device-coherently (past the
 // per-XCD L2), and each word is checked on its own, so no flag, fence or store ordering is needed:
 // a piece is complete when none of its 18 words is MB_EMPTY. The merging wave then writes
 // MB_EMPTY back, which leaves the buffer ready for the next call. Word 0 of the buffer is the
 // poison flag, set by a merge that gave up waiting.
-constexpr int MB_PIECE = 20;        // floats per piece
+constexpr int MB_PIECE = 24;        // floats per piece: o[16], {m, l}, unused; whole 32-byte sectors
 constexpr int MB_HEAD = 64;         // floats before the first piece
 constexpr uint32_t MB_EMPTY = 0xFFFFFFFFu;
 constexpr int MB_COHERENT = 16;     // buffer cache-policy bit: device-coherent access
@@ -615,7 +615,8 @@ __device__ __forceinline__ void mailbox_merge(const float* __restrict__ q, int q
         if (l + 64 * j >= ns) continue;
         const int base = mb_piece(th, db, l + 64 * j, smax);
 #pragma unroll
-        for (int k = 0; k < 5; ++k) mb_store4(r, base + 4 * k, empty);
+        for (int k = 0; k < 4; ++k) mb_store4(r, base + 4 * k, empty);
+        mb_store2(r, base + 16, __builtin_bit_cast(f2, u2{MB_EMPTY, MB_EMPTY}));
     }
     merge_wave_store<SPL>(gv, nh, t, h, ns, hv, ov, out, ots, d0, l);
 }
