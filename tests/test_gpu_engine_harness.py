@@ -1,8 +1,8 @@
 """The C++ engine-shaped caller (tests/csrc/engine_harness.cpp) drives the C ABI as the reference's
 engine would (one arena, prompt split by it_prefill_chunks, scratch = the arena's dispatch room,
-then token-by-token decode with the one-launch GDN layer) over one attention and one GDN layer; its
-outputs match the oracle: attention within 2e-3 with identical argmax, GDN outputs within 2e-3,
-the final state within 5e-3 and the conv state bit-exact."""
+then token-by-token decode with attention and the GDN layer each in one launch) over one attention
+and one GDN layer; its outputs match the oracle: attention within 2e-3 with identical argmax, GDN
+outputs within 2e-3, the final state within 5e-3 and the conv state bit-exact."""
 import os
 import subprocess
 
@@ -37,6 +37,7 @@ def test_engine_harness_matches_oracle(tmp_path, tp, td, ub):
     r = subprocess.run([EXE, str(tmp_path), str(tp), str(td), str(ub)], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stderr
+    assert f"({td} attention calls in one launch), mailbox clean" in r.stdout
     attn = np.fromfile(tmp_path / "attn_out.bin", np.float32).reshape(T, 16 * 256)
     gout = np.fromfile(tmp_path / "gdn_out.bin", np.float32).reshape(T, 32 * 128)
     st = np.fromfile(tmp_path / "state_out.bin", np.float32).reshape(32, 128, 128)
