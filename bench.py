@@ -27,11 +27,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per launch of the dominant decode kernel (attn_decode_kernel<1>, ctx 8192), from two
-# rocprofv3 --pmc runs of `bench.py --only decode` scaled by a 256 MiB copy's readings:
-# FETCH_SIZE 8,305.0 KiB x 2.0 + WRITE_SIZE 2,112 KiB x 1.0, re-measured on the current build (the
-# counter table of profiles/attn_decode_ctx8192.md; a --pmc run cannot share the timed process).
-DECODE_TRAFFIC_BYTES = int((8305.0 * 2.0 + 2112.0 * 1.0) * 1024)
+COPY_KIB = 262144   # the calibration copy: 256 MiB read and written
 F16_MFMA_PEAK_TFLOPS = 2500.0
 NH, NKV, HD = 16, 2, 256
 KVD = NKV * HD
@@ -86,6 +82,59 @@ def graph_time_ms(torch, fn, reps: int, warm: int = 3) -> float:
     return best
 
 
+def pmc_median(counter: str, bench_args: list, kernel: str, grid: str):
+    """Run bench.py once more, as a child process under `rocprofv3 --pmc <counter>` (counters cannot
+    be collected in the timed process), and return (median of the counter over the dispatches of
+    `kernel` at total grid size `grid`, None) or (None, reason)."""
+    import csv, glob, shutil, signal, statistics, subprocess, tempfile
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None, "rocprofv3 not found"
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        cmd = [prof, "--pmc", counter, "-d", d, "-o", "run", "--output-format", "csv", "--", sys.executable,
+               os.path.join(ROOT, "bench.py"), "--no-pmc"] + bench_args
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
+                                stderr=subprocess.DEVNULL, start_new_session=True)
+        try:
+            rc = proc.wait(timeout=150)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)   # the profiler and the program it runs
+            proc.wait()
+            return None, f"{counter} pass timed out"
+        if rc != 0:
+            return None, f"{counter} pass exited with {rc}"
+        vals = []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if (r.get("Counter_Name") == counter and r.get("Kernel_Name", "").startswith(kernel)
+                        and r.get("Grid_Size") == grid):
+                    vals.append(float(r["Counter_Value"]))
+        if not vals:
+            return None, f"{counter}: no dispatch of {kernel} at grid {grid}"
+        return statistics.median(vals), None
+
+
+def measure_decode_traffic():
+    """HBM bytes per launch of the ctx-8192 partial kernel: FETCH_SIZE and WRITE_SIZE medians, each
+    scaled by what the same counter reads for a plain 256 MiB device copy. Returns (bytes, note)."""
+    dec = ["--only", "decode", "--no-cpu", "--steps", "20", "--warmup", "2"]
+    kern, grid = "void it::attn_decode_kernel<1, false>", str(32768 * 2)
+    got = {}
+    for key, counter, args, k, g in (("fetch", "FETCH_SIZE", dec, kern, grid),
+                                     ("write", "WRITE_SIZE", dec, kern, grid),
+                                     ("cal_fetch", "FETCH_SIZE", ["--copy-calibration"], "__amd_rocclr_copyBuffer", "131072"),
+                                     ("cal_write", "WRITE_SIZE", ["--copy-calibration"], "__amd_rocclr_copyBuffer", "131072")):
+        v, why = pmc_median(counter, args, k, g)
+        if v is None or v <= 0:
+            return None, why or f"{counter}: zero reading"
+        got[key] = v
+    fetch = got["fetch"] * COPY_KIB / got["cal_fetch"]
+    write = got["write"] * COPY_KIB / got["cal_write"]
+    note = (f"rocprofv3 --pmc in this run: FETCH_SIZE {got['fetch']:.1f} KiB x {COPY_KIB / got['cal_fetch']:.3f} + "
+            f"WRITE_SIZE {got['write']:.1f} KiB x {COPY_KIB / got['cal_write']:.3f} (factors from a 256 MiB copy)")
+    return int(round((fetch + write) * 1024)), note
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -96,6 +145,8 @@ def main():
     ap.add_argument("--decode-chunk", type=int, default=0, help="keys per split for decode (0 = library policy)")
     ap.add_argument("--only", choices=["all", "decode", "prefill", "gdn", "prep", "mtp"], default="all",
                     help="run one section only (profiling runs); the JSON line then carries that section's figures")
+    ap.add_argument("--no-pmc", action="store_true",
+                    help="skip the rocprofv3 --pmc passes that measure roofline.traffic")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain device copies of 256 MiB (reference reading for the FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
@@ -570,6 +621,11 @@ def main():
                "configs": cpu_all}
         log(f"cpu baselines ({threads} threads of {hw}): " + json.dumps(cpu_all))
 
+    traffic, traffic_note = None, "not measured (--no-pmc or a section run)"
+    if args.only == "all" and not args.no_pmc and us_layer is not None:
+        log("roofline.traffic: four rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE; decode and a copy)")
+        traffic, traffic_note = measure_decode_traffic()
+        log(f"traffic: {traffic} bytes per launch ({traffic_note})")
     line = {
         "metric": "decode attn µs/layer + HBM GB/s @ctx 8192; prefill attn TFLOP/s @8192 tok",
         "value": rnd(value_gbs, 1),
@@ -591,7 +647,7 @@ def main():
         "results": res,
         "roofline": {"bound": "hbm", "achieved": rnd(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": rnd(None if part_gbs is None else part_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": DECODE_TRAFFIC_BYTES, "traffic_unit": "bytes per launch",
+                     "traffic": traffic, "traffic_unit": "bytes per launch", "traffic_source": traffic_note,
                      "kernel": "attn_decode_kernel<1, false>", "kernel_us": rnd(part_us, 3),
                      "bytes_per_launch": dbytes},
         "roofline_prefill": {"bound": "mfma", "achieved": prefill_tflops, "peak": F16_MFMA_PEAK_TFLOPS,
