@@ -134,7 +134,8 @@ int it_attn_f16_noalloc(const float* q, int q_tok_stride, const uint16_t* kc, co
  * device (other streams, concurrent graph replays) need one each. A merge that has waited 10 ms
  * (possible only if other work holds the device's compute units) gives up, writes NaN outputs and
  * poisons the mailbox: every later call then gives NaN at once until it_attn_mailbox_init runs
- * again; it_attn_mailbox_poisoned reports the flag. */
+ * again. A mailbox that was never initialised (or was overwritten) is treated as poisoned too;
+ * it_attn_mailbox_poisoned reports either. */
 size_t it_attn_mailbox_bytes(int ctx, int nt, int nh);
 int it_attn_mailbox_init(void* mailbox, size_t bytes, void* stream);
 int it_attn_mailbox_poisoned(const void* mailbox, int* poisoned, void* stream);   /* synchronises stream */

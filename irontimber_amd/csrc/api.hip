@@ -341,11 +341,11 @@ int it_attn_mailbox_init(void* mailbox, size_t bytes, void* stream) {
 
 int it_attn_mailbox_poisoned(const void* mailbox, int* poisoned, void* stream) {
     if (!mailbox || !poisoned) return fail("it_attn_mailbox_poisoned: null argument");
-    uint32_t w = 0;
+    uint32_t w[2] = {0, 0};
     hipStream_t st = (hipStream_t)stream;
-    if (check(hipMemcpyAsync(&w, mailbox, 4, hipMemcpyDeviceToHost, st), "it_attn_mailbox_poisoned")) return -1;
+    if (check(hipMemcpyAsync(w, mailbox, 8, hipMemcpyDeviceToHost, st), "it_attn_mailbox_poisoned")) return -1;
     if (check(hipStreamSynchronize(st), "it_attn_mailbox_poisoned")) return -1;
-    *poisoned = w != 0;
+    *poisoned = w[0] != 0 || w[1] != it::MAILBOX_MAGIC;   // gave up, or never initialised
     return 0;
 }
 

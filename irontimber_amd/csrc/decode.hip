@@ -88,7 +88,9 @@ template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
 // per-XCD L2), and each word is checked on its own, so no flag, fence or store ordering is needed:
 // a piece is complete when none of its 18 words is MB_EMPTY. The merging wave then writes
 // MB_EMPTY back, which leaves the buffer ready for the next call. Word 0 of the buffer is the
-// poison flag, set by a merge that gave up waiting.
+// poison flag, set by a merge that gave up waiting; word 1 holds MAILBOX_MAGIC once the buffer is
+// initialised, so a buffer that never was (or was overwritten) fails loudly instead of passing its
+// stale words off as records.
 constexpr int MB_PIECE = 24;        // floats per piece: o[16], {m, l}, unused; whole 32-byte sectors
 constexpr int MB_HEAD = 64;         // floats before the first piece
 constexpr uint32_t MB_EMPTY = 0xFFFFFFFFu;
@@ -569,7 +571,8 @@ __device__ __forceinline__ void mailbox_merge(const float* __restrict__ q, int q
         for (int k = 0; k < 4; ++k) ov[j][k] = f4{0.f, 0.f, 0.f, 0.f};
     }
     const float gv = merge_gate(q, qts, t, h, d0, l);   // issued before the wait, used after it
-    bool bad = mb_load2(r, 0)[0] != 0u;
+    const u2 hdr = mb_load2(r, 0);
+    bool bad = hdr[0] != 0u || hdr[1] != MAILBOX_MAGIC;
     const uint64_t deadline = __builtin_amdgcn_s_memrealtime() + MB_SPIN_TICKS;
     while (!bad) {
 #pragma unroll
@@ -643,7 +646,7 @@ __global__ __launch_bounds__(256) void attn_decode_mailbox_kernel(const float* _
 
 __global__ __launch_bounds__(256) void mailbox_fill_kernel(uint32_t* p, size_t words) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (size_t)gridDim.x * 256)
-        p[i] = i < (size_t)MB_HEAD ? 0u : MB_EMPTY;
+        p[i] = i == 1 ? MAILBOX_MAGIC : i < (size_t)MB_HEAD ? 0u : MB_EMPTY;
 }
 
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,

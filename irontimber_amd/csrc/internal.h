@@ -29,6 +29,8 @@ hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const
 // bytes, the whole grid co-resident on the device); with dry_run, only reports whether it would
 // launch.
 size_t mailbox_bytes(long ctx, int nt, int nh);
+// mailbox header: word 0 the poison flag (0 = clear), word 1 this value once initialised
+constexpr uint32_t MAILBOX_MAGIC = 0x4D424F58u;
 hipError_t launch_attn_decode_mailbox(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
                                       int pos0, int nh, int nkv, int nt, float scale, float* out, int ots, float* mb,
                                       size_t mbb, hipStream_t st, bool* launched, bool dry_run = false);

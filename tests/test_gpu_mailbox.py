@@ -22,9 +22,12 @@ def _inputs(dev, seed, ctx, nt, nh, nkv):
     return q, kb, vb, dev_f32(q.reshape(nt, -1), dev), dev_f16bits(kb, dev), dev_f16bits(vb, dev)
 
 
+MAGIC = np.uint32(0x4D424F58)
+
+
 def _clean(mb):
     words = host(mb).view(np.uint32)
-    return (words[:64] == 0).all() and (words[64:] == EMPTY).all()
+    return words[0] == 0 and words[1] == MAGIC and (words[2:64] == 0).all() and (words[64:] == EMPTY).all()
 
 
 # (ctx, nt, nh, nkv, one launch expected): decode at the BASELINE geometries, short and ragged
@@ -131,3 +134,14 @@ def test_poisoned_mailbox_fails_loudly(dev):
     got = host(ops.attn_f16_mailbox(qd, kc, vc, ctx - 1, nh, nkv, mb))
     np.testing.assert_array_equal(got, host(ops.attn_f16(qd, kc, vc, ctx - 1, nh, nkv)))
     assert _clean(mb)
+
+
+def test_uninitialised_mailbox_fails_loudly(dev):
+    """A mailbox that it_attn_mailbox_init never filled (here zeroed device memory, whose words
+    would otherwise pass for records) is treated as poisoned: NaN outputs, the flag reported."""
+    nh, nkv, ctx = 16, 2, 8192
+    q, kb, vb, qd, kc, vc = _inputs(dev, 11, ctx, 1, nh, nkv)
+    mb = torch.zeros(ops.lib().it_attn_mailbox_bytes(ctx, 1, nh), device=dev, dtype=torch.uint8)
+    assert ops.attn_mailbox_poisoned(mb)
+    got = host(ops.attn_f16_mailbox(qd, kc, vc, ctx - 1, nh, nkv, mb))
+    assert np.isnan(got).all()
