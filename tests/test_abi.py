@@ -211,3 +211,36 @@ def test_prefill_chunks_brute_force():
                 want.append((s, s + m))
                 s += m
             assert prefill_chunks(n, batch) == want
+
+
+def test_mailbox_host_side():
+    """The mailbox entry points' host-side rules, with no device work: the size formula (64 header
+    words, then 96-byte pieces per token, head, 16-dim block and 64-key split), argument checks of
+    the initialiser and the call before any launch, and the eligibility query declining every
+    geometry that is not a decode step (no device query for those)."""
+    lib = _lib.lib()
+    for ctx, nt, nh in [(1, 1, 16), (8192, 1, 16), (8192, 4, 16), (16384, 1, 32), (65, 2, 8)]:
+        smax = (ctx + 63) // 64
+        assert lib.it_attn_mailbox_bytes(ctx, nt, nh) == 4 * (64 + nt * nh * 16 * smax * 24)
+    assert lib.it_attn_mailbox_bytes(0, 1, 16) == 0 and lib.it_attn_mailbox_bytes(8192, 0, 16) == 0
+    fake = ctypes.c_void_p(1 << 20)   # never dereferenced
+    assert lib.it_attn_mailbox_init(None, 1 << 20, None) != 0
+    assert lib.it_attn_mailbox_init(fake, 16, None) != 0                       # below one header
+    assert lib.it_attn_mailbox_init(ctypes.c_void_p((1 << 20) + 4), 1 << 20, None) != 0   # misaligned
+    assert b"16-byte" in lib.it_last_error()
+    assert lib.it_attn_mailbox_poisoned(None, None, None) != 0
+    # misaligned mailbox: refused before any device work
+    rc = lib.it_attn_f16_mailbox(fake, 8192, fake, fake, 512, 8191, 256, 16, 2, 1, 0.0625, fake, 4096,
+                                 ctypes.c_void_p((1 << 20) + 8), 1 << 22, None, 0, None)
+    assert rc != 0 and b"16-byte" in lib.it_last_error()
+    # bad geometry: the same validation as it_attn_f16
+    rc = lib.it_attn_f16_mailbox(fake, 8192, fake, fake, 512, 0, 256, 15, 2, 1, 0.0625, fake, 4096, fake, 1 << 22,
+                                 None, 0, None)
+    assert rc != 0
+    # not a decode step, too many splits, too small a mailbox, bad geometry: declined without a query
+    need = lib.it_attn_mailbox_bytes(8192, 1, 16)
+    assert lib.it_attn_mailbox_would_launch(8128, 64, 256, 16, 2, 1 << 30) == 0
+    assert lib.it_attn_mailbox_would_launch(8191, 4, 256, 16, 2, 1 << 30) == 0      # 32 rows per KV head
+    assert lib.it_attn_mailbox_would_launch(16384, 1, 256, 16, 2, 1 << 30) == 0     # 257 splits
+    assert lib.it_attn_mailbox_would_launch(8191, 1, 256, 16, 2, need - 4) == 0
+    assert lib.it_attn_mailbox_would_launch(8191, 1, 128, 16, 2, need) == 0
