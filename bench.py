@@ -526,6 +526,17 @@ def main():
         io = T5 * (2 * nk + nv) * S * 4 + T5 * nv * S * 4 + 2 * 2 * nv * S * S * 4 + 2 * T5 * nv * 4
         res["gdn_prefill_8192_scan_io_GBs"] = round(io / (ms_s * 1e-3) / 1e9, 1)
         log(f"gdn prefill 8192: layer {ms:.3f} ms, scan {ms_s:.3f} ms ({res['gdn_prefill_8192_scan_TFLOPs']} TF/s chunked)")
+        # the same layer in one call, the conv output kept as f16 (config 5's f16 activations)
+        scr1 = torch.empty(_l().it_gdn_prefill_scratch_bytes(T5, nv, nk, S), device=dev, dtype=torch.uint8)
+
+        def gdn_prefill_one():
+            call("it_gdn_prefill", x5.data_ptr(), d5["cd"], w5.data_ptr(), 4, cs5.data_ptr(), br5.data_ptr(),
+                 ar5.data_ptr(), nv, dt5.data_ptr(), a5.data_ptr(), st5.data_ptr(), o5.data_ptr(), nv * S, T5, nv,
+                 nk, S, 1e-6, scr1.data_ptr(), scr1.numel(), stream_of())
+        ms1 = graph_time_ms(torch, gdn_prefill_one, reps=3)
+        res["gdn_prefill_8192_layer_one_call_ms"] = round(ms1, 4)
+        log(f"gdn prefill 8192 in one call (f16 conv output): layer {ms1:.3f} ms")
+        del scr1
         z5 = torch.randn(T5, nv * S, device=dev)
         nw5 = torch.ones(S, device=dev)
 

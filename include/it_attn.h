@@ -328,6 +328,21 @@ int it_gdn_chunked(const float* co, int co_tok_stride, const float* beta_raw, co
                    int out_tok_stride, int nt, int nv, int nk, int S, void* scratch,
                    size_t scratch_bytes, void* stream);
 
+/* The GDN layer over a prompt chunk in one call: replaces the conv (src/vk/mod.rs:803), rmsnorm
+ * mode 2 on the q/k heads (804) and gdn_p (806) dispatches of a prefill chunk. Conv + SiLU + q/k
+ * L2 norm (as it_gdn_conv_l2norm with nnorm = 2*nk), its output kept in `scratch` as f16 (the
+ * "f16 activations" of the chunked-prefill benchmark: half the bytes for the conv's write and the
+ * scan's read; rounding it moves outputs by ~7e-5 and the final state by ~6e-4 at 8192 tokens),
+ * then the chunk-64 scan of it_gdn_chunked. x [nt][x_tok_stride] f32 with cd = (2*nk+nv)*S
+ * channels; w, conv_state, beta_raw, alpha_raw, dt, a, state and out as it_gdn_conv and
+ * it_gdn_chunked (S = 128); conv_state and state are updated in place. scratch: 16-byte aligned,
+ * it_gdn_prefill_scratch_bytes(nt, nv, nk, S) bytes. */
+size_t it_gdn_prefill_scratch_bytes(int nt, int nv, int nk, int S);
+int it_gdn_prefill(const float* x, int x_tok_stride, const float* conv_w, int K, float* conv_state,
+                   const float* beta_raw, const float* alpha_raw, int ba_tok_stride, const float* dt,
+                   const float* a, float* state, float* out, int out_tok_stride, int nt, int nv, int nk, int S,
+                   float eps, void* scratch, size_t scratch_bytes, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Reference-shaped dispatch policy (pure host functions, no device access).
  * ---------------------------------------------------------------------------------------------- */

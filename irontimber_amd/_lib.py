@@ -54,6 +54,9 @@ SIGNATURES = {
     "it_attention_chunk": (c_int, [c_uint32, c_uint32, c_uint32, c_size_t]),
     "it_validate_geometry": (c_int, [c_int] * 9),
     "it_attn_f16_noalloc": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int, P]),
+    "it_gdn_prefill_scratch_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "it_gdn_prefill": (c_int, [P, c_int, P, c_int, P, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int,
+                               c_float, P, c_size_t, P]),
     "it_attn_mailbox_bytes": (c_size_t, [c_int, c_int, c_int]),
     "it_attn_mailbox_init": (c_int, [P, c_size_t, P]),
     "it_attn_mailbox_would_launch": (c_int, [c_int, c_int, c_int, c_int, c_int, c_size_t]),

@@ -610,6 +610,43 @@ int it_gdn_chunked(const float* co, int cts, const float* br, const float* ar, i
                  "it_gdn_chunked");
 }
 
+static size_t gdn_prefill_co_bytes(int nt, int nv, int nk, int S) {
+    return ((size_t)nt * (size_t)(2 * nk + nv) * S * 2 + 255) / 256 * 256;
+}
+
+size_t it_gdn_prefill_scratch_bytes(int nt, int nv, int nk, int S) {
+    if (nt <= 0 || nv <= 0 || nk <= 0 || S != 128) return 0;
+    return gdn_prefill_co_bytes(nt, nv, nk, S) + it::gdn_chunked_scratch_bytes(nt, nv, S);
+}
+
+int it_gdn_prefill(const float* x, int xts, const float* w, int K, float* conv_state, const float* br, const float* ar,
+                   int bts, const float* dt, const float* a, float* state, float* out, int ots, int nt, int nv,
+                   int nk, int S, float eps, void* scratch, size_t scratch_bytes, void* stream) {
+    const char* who = "it_gdn_prefill";
+    if (K < 2 || K > 4) return fail("%s: kernel size %d unsupported (2..4)", who, K);
+    if (S != 128) return fail("%s: state size %d unsupported (128)", who, S);
+    if (nv <= 0 || nk <= 0 || nv % nk != 0) return fail("%s: nv %d / nk %d invalid", who, nv, nk);
+    if (nt < 0) return fail("%s: nt %d invalid", who, nt);
+    if (!x || !w || !conv_state || !br || !ar || !dt || !a || !state || !out) return fail("%s: null buffer", who);
+    const int cd = (2 * nk + nv) * S;
+    if (nt > 1 && (xts < cd || ots < nv * S || bts < nv)) return fail("%s: token strides overlap rows", who);
+    if (!aligned16(state) || !aligned16(out) || ots % 4 != 0)
+        return fail("%s: state/out must be 16-byte aligned, the out token stride a multiple of 4", who);
+    if (nt == 0) { g_err.clear(); return 0; }
+    const size_t need = it_gdn_prefill_scratch_bytes(nt, nv, nk, S);
+    if (scratch_bytes < need || !scratch)
+        return fail("%s: scratch of %zu bytes < %zu required (it_gdn_prefill_scratch_bytes)", who, scratch_bytes, need);
+    if (!aligned16(scratch)) return fail("%s: scratch must be 16-byte aligned", who);
+    // the conv + SiLU + q/k L2 output goes to the front of the scratch as f16 (token stride cd),
+    // the chunk records after it
+    _Float16* co = (_Float16*)scratch;
+    void* rec = (char*)scratch + gdn_prefill_co_bytes(nt, nv, nk, S);
+    hipStream_t st = (hipStream_t)stream;
+    if (check(it::launch_gdn_conv_l2(x, xts, w, conv_state, co, cd, cd, nt, K, 2 * nk, eps, nullptr, 0, st), who))
+        return -1;
+    return check(it::launch_gdn_chunked(co, cd, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, rec, st), who);
+}
+
 // ---- reference-shaped policy (src/vk/mod.rs:130-220) -------------------------------------------
 size_t it_attention_scratch_words(size_t ctx, size_t heads) { return 64 * heads * (ctx > 260 ? ctx : 260); }
 

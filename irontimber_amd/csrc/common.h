@@ -41,6 +41,18 @@ __device__ __forceinline__ h8 cat_h4(h4 a, h4 b) { return h8{a[0], a[1], a[2], a
 
 __device__ __forceinline__ h8 ld_h8(const void* p) { return __builtin_bit_cast(h8, *(const u4*)p); }
 __device__ __forceinline__ f4 ld_f4(const float* p) { return *(const f4*)p; }
+// 8 consecutive activations as two f4, from f32 or (16-byte aligned) f16 storage
+__device__ __forceinline__ void ld8(const float* p, f4& a, f4& b) { a = ld_f4(p); b = ld_f4(p + 4); }
+__device__ __forceinline__ void ld8(const _Float16* p, f4& a, f4& b) {
+    const h8 h = ld_h8(p);
+    a = f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+    b = f4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]};
+}
+// store 4 activations as f32 or f16 (round to nearest even)
+__device__ __forceinline__ void st4(float* p, f4 y) { *(f4*)p = y; }
+__device__ __forceinline__ void st4(_Float16* p, f4 y) {
+    *(h4*)p = h4{(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+}
 
 // Split 8 f32 values into f16 hi + f16 lo with hi + lo == x to ~2^-22 relative: two MFMAs with
 // the halves reproduce an f32-accurate dot product against exact f16 operands.

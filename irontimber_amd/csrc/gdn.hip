@@ -81,10 +81,10 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __rest
 // 128hb + 64 + l, so a token's head vector is the whole wave and its sum of squares one DPP
 // reduction. Head blocks hb < nnorm (the q and k heads) are normalised, x / max(||x||, eps); the
 // rest (v) pass through. State and checkpoint handling as in gdn_conv_kernel.
-template <int K>
+template <int K, typename OutT>
 __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restrict__ x, int xts,
                                                           const float* __restrict__ w, float* __restrict__ state,
-                                                          float* __restrict__ out, int ots, int cd, int nt, int TT,
+                                                          OutT* __restrict__ out, int ots, int cd, int nt, int TT,
                                                           int nnorm, float eps, float* __restrict__ ck, int ck_after) {
     constexpr int TMAX = 16;   // tokens per run (the host passes TT <= TMAX)
     const int hb = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restric
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            out[(size_t)(t0 + j) * ots + ch[c]] = y[c];
+            out[(size_t)(t0 + j) * ots + ch[c]] = (OutT)y[c];
 #pragma unroll
             for (int i = 0; i + 1 < K - 1; ++i) win[c][i] = win[c][i + 1];
             win[c][K - 2] = xs[c][j];
@@ -155,10 +155,10 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restric
 // holds channels 256*wb + 4l .. 4l+3 of wave block wb, so lanes 0-31 and 32-63 each hold one
 // 128-channel head and a head's sum of squares is a reduction over its 32 lanes (DPP within the
 // 16-lane rows, then a row swap). A quarter of the memory instructions of the scalar form.
-template <int K>
+template <int K, typename OutT>
 __global__ __launch_bounds__(256) void gdn_conv_l2_v4_kernel(const float* __restrict__ x, int xts,
                                                              const float* __restrict__ w, float* __restrict__ state,
-                                                             float* __restrict__ out, int ots, int cd, int nt, int TT,
+                                                             OutT* __restrict__ out, int ots, int cd, int nt, int TT,
                                                              int nnorm, float eps, float* __restrict__ ck,
                                                              int ck_after) {
     constexpr int TMAX = 16;   // tokens per run (the host passes TT <= TMAX)
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_v4_kernel(const float* __rest
         ss += dppc<0x140>(ss);   // row_mirror
         ss = sum_xor16(ss);      // rows 0+1 and 2+3: the two heads' sums
         if (norm) y *= 1.0f / fmaxf(sqrtf(ss), eps);
-        *(f4*)(out + (size_t)(t0 + j) * ots + ch) = y;
+        st4(out + (size_t)(t0 + j) * ots + ch, y);
 #pragma unroll
         for (int i = 0; i + 1 < K - 1; ++i) win[i] = win[i + 1];
         win[K - 2] = xs[j];
@@ -661,7 +661,8 @@ hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state
     return hipGetLastError();
 }
 
-hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd,
+template <typename OutT>
+hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* state, OutT* out, int ots, int cd,
                               int nt, int K, int nnorm, float eps, float* ck, int ck_after, hipStream_t st) {
     const int TT = nt <= 16 ? nt : 16;
     const dim3 grid((cd / 128 + 3) / 4, (nt + TT - 1) / TT);
@@ -674,10 +675,11 @@ hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* st
     if (ck && grid.y > 1)                                                                                           \
         gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, ck, cd, ck_after + 1);          \
     if (v4)                                                                                                         \
-        gdn_conv_l2_v4_kernel<KK><<<grid4, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck,    \
-                                                         ck_after);                                                  \
+        gdn_conv_l2_v4_kernel<KK, OutT><<<grid4, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps,  \
+                                                               ck, ck_after);                                       \
     else                                                                                                            \
-        gdn_conv_l2_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck, ck_after); \
+        gdn_conv_l2_kernel<KK, OutT><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck,  \
+                                                           ck_after);                                               \
     if (grid.y > 1) gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, state, cd, nt);
     switch (K) {
         case 2: IT_CONVL2(2) break;
@@ -687,6 +689,10 @@ hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* st
 #undef IT_CONVL2
     return hipGetLastError();
 }
+template hipError_t launch_gdn_conv_l2<float>(const float*, int, const float*, float*, float*, int, int, int, int,
+                                                int, float, float*, int, hipStream_t);
+template hipError_t launch_gdn_conv_l2<_Float16>(const float*, int, const float*, float*, _Float16*, int, int, int,
+                                                   int, int, float, float*, int, hipStream_t);
 
 hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps, hipStream_t st) {
     const int rows = nheads * nt;

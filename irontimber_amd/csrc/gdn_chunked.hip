@@ -80,7 +80,8 @@ __device__ __forceinline__ void prep_wg(int id, int nch, int nv, int nk, int& c,
     }
 }
 
-__global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void gdn_chunk_prep(const float* __restrict__ co, int cts,
+template <typename CoT>
+__global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void gdn_chunk_prep(const CoT* __restrict__ co, int cts,
                                                                const float* __restrict__ br, const float* __restrict__ ar,
                                                                int bts, const float* __restrict__ dt,
                                                                const float* __restrict__ A, int nt, int nv, int nk,
@@ -91,6 +92,9 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
     static_assert(2 * C * KP * 2 >= C * SD * 4, "the V rows fit in the K tile");
 
+    // an f16 conv output is exact in f16, so its hi/lo splits have lo == 0 and the K K^T / Q K^T
+    // products need only the hi x hi term (bit-identical to the three-term form)
+    constexpr bool F16 = sizeof(CoT) == 2;
     const int nch = (nt + C - 1) / C;
     int c, h;
     prep_wg(blockIdx.x, nch, nv, nk, c, h);
@@ -116,9 +120,12 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     for (int it = 0; it < C * SD / 8 / PREP_THREADS; ++it) {
         const int idx = tid + it * PREP_THREADS;
         const int t = idx >> 4, d8 = 8 * (idx & 15);
-        const float* row = co + (size_t)(t0 + min(t, L - 1)) * cts + qk + kh * SD + d8;
+        const CoT* row = co + (size_t)(t0 + min(t, L - 1)) * cts + qk + kh * SD + d8;
         const float m = t < L ? 1.f : 0.f;
-        const f4 k0 = ld_f4(row) * m, k1 = ld_f4(row + 4) * m;
+        f4 k0, k1;
+        ld8(row, k0, k1);
+        k0 *= m;
+        k1 *= m;
         h8 hi, lo;
         split_hi_lo(k0, k1, hi, lo);
         *(h8*)&Kx[0][t][d8] = hi; *(h8*)&Kx[1][t][d8] = lo;
@@ -133,12 +140,13 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         for (int b = 0; b < 2; ++b) {
             if (b >= nb) break;   // uniform
             const int ta = 16 * (mb0 - b) + li;
-            const float* qr = qrow(ta);
+            const CoT* qr = qrow(ta);
             const float qm = ta < L ? 1.f : 0.f;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                qv[b][2 * ks] = ld_f4(qr + 32 * ks + 8 * g) * qm;
-                qv[b][2 * ks + 1] = ld_f4(qr + 32 * ks + 8 * g + 4) * qm;
+                ld8(qr + 32 * ks + 8 * g, qv[b][2 * ks], qv[b][2 * ks + 1]);
+                qv[b][2 * ks] *= qm;
+                qv[b][2 * ks + 1] *= qm;
             }
         }
     }
@@ -195,10 +203,13 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     const int d = 32 * ks + 8 * g;
-                    const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
+                    const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]);
                     acc = mfma16x16x32(ah[ks], bh, acc);
-                    acc = mfma16x16x32(ah[ks], bl, acc);
-                    acc = mfma16x16x32(al[ks], bh, acc);
+                    if constexpr (!F16) {
+                        const h8 bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
+                        acc = mfma16x16x32(ah[ks], bl, acc);
+                        acc = mfma16x16x32(al[ks], bh, acc);
+                    }
                 }
                 store_tile(true, mt, nt_, acc);
             }
@@ -214,11 +225,13 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const int d = 32 * ks + 8 * g;
-                const h8 ah = ld_h8(&Kx[0][ta][d]), al = ld_h8(&Kx[1][ta][d]);
-                const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
+                const h8 ah = ld_h8(&Kx[0][ta][d]), bh = ld_h8(&Kx[0][16 * nt_ + li][d]);
                 acc = mfma16x16x32(ah, bh, acc);
-                acc = mfma16x16x32(ah, bl, acc);
-                acc = mfma16x16x32(al, bh, acc);
+                if constexpr (!F16) {
+                    const h8 al = ld_h8(&Kx[1][ta][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
+                    acc = mfma16x16x32(ah, bl, acc);
+                    acc = mfma16x16x32(al, bh, acc);
+                }
             }
             store_tile(false, mt, nt_, acc);
         }
@@ -270,9 +283,9 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     // beta = 0. (The other workgroup on the CU covers their latency.)
     f4 vreg[4];
     {
-        const float* src = co + (size_t)(t0 + min(tid >> 3, L - 1)) * cts + 2 * qk + h * SD + 16 * (tid & 7);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) vreg[j] = ld_f4(src + 4 * j);
+        const CoT* src = co + (size_t)(t0 + min(tid >> 3, L - 1)) * cts + 2 * qk + h * SD + 16 * (tid & 7);
+        ld8(src, vreg[0], vreg[1]);
+        ld8(src + 8, vreg[2], vreg[3]);
     }
     // right-hand sides of this lane's 16 (row, column) cells: W from the K tile, U from V
     float rhs[2][4][4];
@@ -583,7 +596,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
 }
 
 // ------------------------------------------------------------------------------------------------
-hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+template <typename CoT>
+hipError_t launch_gdn_chunked(const CoT* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
                               hipStream_t st) {
     const int nch = (nt + C - 1) / C;
@@ -594,5 +608,9 @@ hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const f
     gdn_chunk_scan<<<dim3(8 * NCB * ((nv + 7) / 8)), SCAN_THREADS, 0, st>>>((const char*)scratch, nch, state, out, ots, nt, nv);
     return hipGetLastError();
 }
+template hipError_t launch_gdn_chunked<float>(const float*, int, const float*, const float*, int, const float*,
+                                              const float*, float*, float*, int, int, int, int, void*, hipStream_t);
+template hipError_t launch_gdn_chunked<_Float16>(const _Float16*, int, const float*, const float*, int, const float*,
+                                                 const float*, float*, float*, int, int, int, int, void*, hipStream_t);
 
 }  // namespace it

@@ -46,7 +46,9 @@ hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, 
 // ck / ck_after: optional checkpoint of the state after token ck_after (null = none).
 hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,
                            int K, float* ck, int ck_after, hipStream_t st);
-hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd,
+// OutT float or _Float16 (the conv output as f16 for the one-call GDN prefill)
+template <typename OutT>
+hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* state, OutT* out, int ots, int cd,
                               int nt, int K, int nnorm, float eps, float* ck, int ck_after, hipStream_t st);
 hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps, hipStream_t st);
 hipError_t launch_gdn_decode_fused(const float* x, int xts, const float* cw, int K, const float* cst_in, float* cst_out,
@@ -63,7 +65,9 @@ hipError_t launch_gdn_step_head(const float* co, int cts, const float* br, const
 hipError_t launch_gdn_gated_norm(const float* o, int ots, const float* z, int zts, const float* w, float eps,
                                  float* out, int outs, int nv, int nt, hipStream_t st);
 size_t gdn_chunked_scratch_bytes(int nt, int nv, int S);
-hipError_t launch_gdn_chunked(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
+// CoT float (it_gdn_chunked) or _Float16 (the conv output of the one-call GDN prefill)
+template <typename CoT>
+hipError_t launch_gdn_chunked(const CoT* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
                               hipStream_t st);
 

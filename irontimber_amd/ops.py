@@ -311,6 +311,28 @@ def gdn_step(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, out=None, 
     return out
 
 
+def gdn_prefill(x, w, conv_state, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, eps: float = 1e-6, out=None,
+                scratch=None):
+    """The GDN layer over a prompt chunk in one call (it_gdn_prefill): conv + SiLU + q/k L2 kept as
+    f16 in scratch, then the chunk-64 scan. x [nt, cd] f32, w [cd, K], conv_state [K-1, cd] and
+    state [nv, S, S] updated in place -> out [nt, nv*S]."""
+    for t, n in ((x, "x"), (w, "w"), (conv_state, "conv_state"), (beta_raw, "beta_raw"), (alpha_raw, "alpha_raw"),
+                 (dt, "dt"), (a, "a"), (state, "state")):
+        _need(t, torch.float32, n)
+    nt = x.shape[0]
+    S = state.shape[-1]
+    if out is None:
+        out = torch.empty(nt, nv * S, device=x.device, dtype=torch.float32)
+    need = lib().it_gdn_prefill_scratch_bytes(nt, nv, nk, S)
+    if scratch is None and need:
+        scratch = torch.empty(need, device=x.device, dtype=torch.uint8)
+    nbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
+    call("it_gdn_prefill", x.data_ptr(), x.shape[1], w.data_ptr(), w.shape[1], conv_state.data_ptr(),
+         beta_raw.data_ptr(), alpha_raw.data_ptr(), beta_raw.shape[1], dt.data_ptr(), a.data_ptr(), state.data_ptr(),
+         out.data_ptr(), out.shape[1], nt, nv, nk, S, float(eps), _ptr(scratch), nbytes, _stream())
+    return out
+
+
 def gdn_gated_rmsnorm(o: torch.Tensor, z: torch.Tensor, w: torch.Tensor, nv: int, eps: float = 1e-6,
                       out: torch.Tensor | None = None) -> torch.Tensor:
     """o, z [nt, nv*128], w [128] -> o / rms(o) * w * silu(z) per 128-wide head row (out may be o)."""

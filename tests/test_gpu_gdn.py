@@ -392,3 +392,53 @@ def test_conv_kparity_geometry(dev):
     got2 = host(ops.gdn_conv(dev_f32(x2, dev), dev_f32(w, dev), st))
     assert np.abs(got2 - want2).max() <= 1e-6
     np.testing.assert_array_equal(host(st), wst2)
+
+
+@pytest.mark.parametrize("nt,nv,nk,K", [(1, 4, 2, 4), (5, 4, 2, 3), (64, 8, 4, 4), (65, 4, 2, 2), (200, 32, 16, 4),
+                                        (130, 8, 8, 4)])
+def test_prefill_one_call_equals_f16_conv_output_two_calls(dev, nt, nv, nk, K):
+    """it_gdn_prefill (conv + L2 kept as f16, then the chunk-64 scan) equals, bit for bit, the two
+    f32 calls it_gdn_conv_l2norm + it_gdn_chunked fed with that conv output rounded to f16 (RNE):
+    the f16 prep's single hi x hi product is the three-term hi/lo form with exact zero lo terms.
+    Conv state identical; outputs also within the GDN bars of the float64 recurrence."""
+    announce(f"gdn prefill one call nt={nt} nv={nv} nk={nk} K={K}")
+    d = gdn_inputs(17 + nt, nt=nt, nv=nv, nk=nk, K=K)
+    x, w = dev_f32(d["x"], dev), dev_f32(d["w"], dev)
+    args = [dev_f32(d["beta_raw"], dev), dev_f32(d["alpha_raw"], dev), dev_f32(d["dt"], dev), dev_f32(d["a"], dev)]
+    cs1, st1 = dev_f32(d["conv_state"], dev), dev_f32(d["state"], dev)
+    got = host(ops.gdn_prefill(x, w, cs1, *args, st1, nv, nk))
+    cs2, st2 = dev_f32(d["conv_state"], dev), dev_f32(d["state"], dev)
+    co = ops.gdn_conv_l2norm(x, w, cs2, 2 * nk).half().float()
+    want = host(ops.gdn_step(co, *args, st2, nv, nk, chunked=True))
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(host(st1), host(st2))
+    np.testing.assert_array_equal(host(cs1), host(cs2))
+    o64, s64 = gdn_seq_f64(host(co), d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
+    assert np.abs(got - o64).max() <= OUT_TOL and np.abs(host(st1) - s64).max() <= STATE_TOL
+
+
+def test_prefill_one_call_config5(dev):
+    """BASELINE config 5 (seed 4, f16 activations) through it_gdn_prefill: against 8192 sequential
+    steps of the cpu.rs restatement on the f32 layer input, the output and final-state bars,
+    the conv state bit-exact, and the last token's argmax identical."""
+    nv, nk, S, nt = 32, 16, 128, 8192
+    d = gdn_inputs(4, nt=nt, nv=nv, nk=nk)
+    announce("gdn config5 one-call oracle (cpu)")
+    co_ref = np.zeros((nt, d["cd"]), np.float32)
+    cst, sst = d["conv_state"].copy(), d["state"].copy()
+    out_ref = np.zeros((nt, nv * S), np.float32)
+    P = lambda a: a.ctypes.data
+    oracle.lib().it_ref_gdn_layer(P(d["x"]), d["cd"], P(d["w"]), P(cst), 4, P(d["beta_raw"]), P(d["alpha_raw"]), nv,
+                                  P(d["dt"]), P(d["a"]), P(sst), P(out_ref), nv * S, P(co_ref), nt, nv, nk, S, 1e-6,
+                                  oracle.hardware_threads())
+    announce("gdn config5 one call gpu")
+    cs, st = dev_f32(d["conv_state"], dev), dev_f32(d["state"], dev)
+    args = [dev_f32(d["beta_raw"], dev), dev_f32(d["alpha_raw"], dev), dev_f32(d["dt"], dev), dev_f32(d["a"], dev)]
+    out = host(ops.gdn_prefill(dev_f32(d["x"], dev), dev_f32(d["w"], dev), cs, *args, st, nv, nk))
+    eo, es = np.abs(out - out_ref).max(), np.abs(host(st) - sst).max()
+    print(f"config5 one call vs oracle: out max_abs={eo:.3g} state max_abs={es:.3g}")
+    assert eo <= OUT_TOL and es <= STATE_TOL
+    np.testing.assert_array_equal(host(cs), cst)
+    assert assert_argmax_agrees(out[-1:], out_ref[-1:]) == 0
+    near = assert_argmax_agrees(out, out_ref)
+    print(f"config5 one call: {near} near-tie argmax rows of {nt} over the whole prompt")
