@@ -536,7 +536,6 @@ def main():
         ms1 = graph_time_ms(torch, gdn_prefill_one, reps=3)
         res["gdn_prefill_8192_layer_one_call_ms"] = round(ms1, 4)
         log(f"gdn prefill 8192 in one call (f16 conv output): layer {ms1:.3f} ms")
-        del scr1
         z5 = torch.randn(T5, nv * S, device=dev)
         nw5 = torch.ones(S, device=dev)
 
@@ -558,14 +557,15 @@ def main():
         vp = torch.from_numpy(vbp.view(np.int16)).to(dev)
         outp = torch.empty(T, NH * HD, device=dev)
 
-        def hybrid():
+        def hybrid():   # each GDN layer in one call (it_gdn_prefill)
             for _ in range(3):
-                gdn_prefill()
+                gdn_prefill_one()
             call("it_attn_f16", qp.data_ptr(), NH * 2 * HD, kp.data_ptr(), vp.data_ptr(), KVD, 0, HD, NH, NKV, T, scale,
                  outp.data_ptr(), NH * HD, None, 0, stream_of())
         ms = graph_time_ms(torch, hybrid, reps=2)
         res["hybrid_3gdn_1attn_prefill_8192_ms"] = round(ms, 3)
-        del qp, kp, vp, outp, co5, o5, scr5
+        log(f"hybrid 3 GDN + 1 attention prefill layers, 8192 tokens: {ms:.3f} ms")
+        del qp, kp, vp, outp, co5, o5, scr5, scr1
 
     # ------------------------------------------------------------------ CPU baselines (oracle, host cores)
     # The C++ restatement of src/cpu.rs timed on this box's host cores, one bounded sample per
