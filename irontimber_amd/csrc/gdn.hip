@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restric
 #pragma unroll
             for (int i = 0; i < K - 1; ++i) s += win[c][i] * wt[c][i];
             s += xs[c][j] * wt[c][K - 1];
-            y[c] = siluf_(s);
+            y[c] = silu_hw(s);
         }
         if (norm) {
             const float sc = 1.0f / fmaxf(sqrtf(wave_sum(y[0] * y[0] + y[1] * y[1])), eps);
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void gdn_conv_l2_v4_kernel(const float* __rest
 #pragma unroll
             for (int i = 0; i < K - 1; ++i) acc += win[i][e] * wt[i][e];
             acc += xs[j][e] * wt[K - 1][e];
-            y[e] = siluf_(acc);
+            y[e] = silu_hw(acc);
         }
         float ss = y[0] * y[0] + y[1] * y[1] + y[2] * y[2] + y[3] * y[3];
         ss += dppc<0xB1>(ss);    // quad_perm [1,0,3,2]
