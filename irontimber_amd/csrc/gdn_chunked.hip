@@ -176,7 +176,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = 16 * mt + 4 * g + i, s = 16 * nt_ + li;
-            const float d = expf(fminf(sG[t] - sG[s], 0.f));
+            const float d = exp_hw(fminf(sG[t] - sG[s], 0.f));
             if (!isq) Ap[t][s] = s < t ? sB[t] * d * acc[i] : 0.f;
             else aqk[t * C + s] = (_Float16)(s <= t ? d * acc[i] : 0.f);
         }
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             // e^G q of these rows (token-major f16) straight from the registers
             {
                 const int t = 16 * mt + li;
-                const float e = t < L ? expf(sG[t]) : 0.f;
+                const float e = t < L ? exp_hw(sG[t]) : 0.f;
                 u4* QG = (u4*)(rec + OFF_QG);
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
@@ -254,11 +254,11 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int t = t8 + j;
-                r[j] = (_Float16)(expf(fminf(glast - sG[t], 0.f)) * ((float)Kx[0][t][d] + (float)Kx[1][t][d]));
+                r[j] = (_Float16)(exp_hw(fminf(glast - sG[t], 0.f)) * ((float)Kx[0][t][d] + (float)Kx[1][t][d]));
             }
             KT[idx] = __builtin_bit_cast(u4, r);
         }
-        if (tid < 4) ((float*)(rec + OFF_GC))[tid] = expf(glast);   // 4 copies: read per lane
+        if (tid < 4) ((float*)(rec + OFF_GC))[tid] = exp_hw(glast);   // 4 copies: read per lane
     }
     __syncthreads();   // A' complete
     // ---- (I + A') [W | U] = diag(beta) [e^G K | V], blocked by 16 rows:
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int t = 16 * i + 4 * g + e;
-            rhs[0][i][e] = sB[t] * (expf(sG[t]) * ((float)Kx[0][t][col] + (float)Kx[1][t][col]));
+            rhs[0][i][e] = sB[t] * (exp_hw(sG[t]) * ((float)Kx[0][t][col] + (float)Kx[1][t][col]));
         }
     __syncthreads();   // the K tile is dead: V passes through it to its solve lanes
     float* const Vs = (float*)&Kx[0][0][0];   // [C][SD] f32, 32 KB of the 36 KB tile
