@@ -244,3 +244,27 @@ def test_mailbox_host_side():
     assert lib.it_attn_mailbox_would_launch(16384, 1, 256, 16, 2, 1 << 30) == 0     # 257 splits
     assert lib.it_attn_mailbox_would_launch(8191, 1, 256, 16, 2, need - 4) == 0
     assert lib.it_attn_mailbox_would_launch(8191, 1, 128, 16, 2, need) == 0
+
+
+def test_gdn_prefill_host_side():
+    """it_gdn_prefill: scratch size = f16 conv output (256-byte rounded) + the chunk records, and
+    every argument error reported before device work."""
+    lib = _lib.lib()
+    for nt, nv, nk in [(1, 32, 16), (64, 4, 2), (8192, 32, 16), (77, 8, 8)]:
+        co = (nt * (2 * nk + nv) * 128 * 2 + 255) // 256 * 256
+        assert lib.it_gdn_prefill_scratch_bytes(nt, nv, nk, 128) == co + lib.it_gdn_chunked_scratch_bytes(nt, nv, 128)
+    assert lib.it_gdn_prefill_scratch_bytes(0, 32, 16, 128) == 0 and lib.it_gdn_prefill_scratch_bytes(8, 32, 16, 64) == 0
+    fake = ctypes.c_void_p(1 << 20)
+    need = lib.it_gdn_prefill_scratch_bytes(64, 32, 16, 128)
+
+    def call(K=4, S=128, nv=32, nk=16, nt=64, scratch=fake, nbytes=need, xts=8192, ots=4096):
+        return lib.it_gdn_prefill(fake, xts, fake, K, fake, fake, fake, nv, fake, fake, fake, fake, ots, nt, nv, nk, S,
+                                  1e-6, scratch, nbytes, None)
+    assert call(K=5) != 0
+    assert call(S=64) != 0
+    assert call(nv=30) != 0                       # nv not a multiple of nk
+    assert call(xts=4096) != 0                    # token stride below cd = 8192
+    assert call(ots=4098) != 0                    # out stride not a multiple of 4
+    assert call(nbytes=need - 16) != 0 and b"scratch" in lib.it_last_error()
+    assert call(scratch=ctypes.c_void_p((1 << 20) + 8)) != 0 and b"16-byte" in lib.it_last_error()
+    assert call(nt=0) == 0                        # nothing to do, no device work
