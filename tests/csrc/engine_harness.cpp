@@ -63,7 +63,7 @@ void write_file(const std::string& path, const float* d, size_t n) {
 
 // Word offsets into the arena (f32 words; the f16 KV caches take kvd/2 words a position).
 struct Layout {
-    size_t q, k, v, kc, vc, aout, scr, mbox, x, w, cst0, cst1, st, br, ar, dt, a, co, gout, gscr, words;
+    size_t q, k, v, kc, vc, aout, scr, mbox, x, w, cst0, cst1, st, br, ar, dt, a, gout, gscr, words;
 };
 
 }  // namespace
@@ -100,9 +100,8 @@ int main(int argc, char** argv) {
     L.ar = take((size_t)T * NV);
     L.dt = take(NV);
     L.a = take(NV);
-    L.co = take((size_t)ub * CD);
     L.gout = take((size_t)T * NV * S);
-    L.gscr = take((it_gdn_chunked_scratch_bytes(ub, NV, S) + 3) / 4);
+    L.gscr = take((it_gdn_prefill_scratch_bytes(ub, NV, NK, S) + 3) / 4);   // f16 conv output + chunk records
     L.words = o;
 
     float* arena = nullptr;
@@ -129,7 +128,7 @@ int main(int argc, char** argv) {
     ITCHECK(it_attn_mailbox_init(a(L.mbox), mbox_bytes, s));
     uint16_t* kc = (uint16_t*)(arena + L.kc);
     uint16_t* vc = (uint16_t*)(arena + L.vc);
-    const size_t gscr_bytes = it_gdn_chunked_scratch_bytes(ub, NV, S);
+    const size_t gscr_bytes = it_gdn_prefill_scratch_bytes(ub, NV, NK, S);
 
     // one attention layer call for tokens [t0, t0 + nt): every call goes through the mailbox entry
     // point, which runs a decode step in one launch and anything else as it_attn_f16 with the
@@ -151,16 +150,11 @@ int main(int argc, char** argv) {
     for (long i = 0; i < nr; ++i) {
         const int t0 = (int)starts[i], nt = (int)lens[i];
         attention(t0, nt);
-        // GDN layer: conv + q/k L2 (vk/mod.rs:803-804), then the recurrence (806): the chunk-64 scan
-        // for full chunks, the token-sequential kernel for short ones
-        ITCHECK(it_gdn_conv_l2norm(a(L.x + (size_t)t0 * CD), CD, a(L.w), a(L.cst0), a(L.co), CD, CD, nt, KC, 2 * NK, EPS,
-                                   s));
-        if (nt >= 64)
-            ITCHECK(it_gdn_chunked(a(L.co), CD, a(L.br + (size_t)t0 * NV), a(L.ar + (size_t)t0 * NV), NV, a(L.dt), a(L.a),
-                                   a(L.st), a(L.gout + (size_t)t0 * NV * S), NV * S, nt, NV, NK, S, a(L.gscr), gscr_bytes, s));
-        else
-            ITCHECK(it_gdn_step(a(L.co), CD, a(L.br + (size_t)t0 * NV), a(L.ar + (size_t)t0 * NV), NV, a(L.dt), a(L.a),
-                                a(L.st), a(L.gout + (size_t)t0 * NV * S), NV * S, nt, NV, NK, S, s));
+        // GDN layer: conv + q/k L2 (vk/mod.rs:803-804) and the recurrence (806) in one call, the conv
+        // output kept as f16 in the layer's scratch slot
+        ITCHECK(it_gdn_prefill(a(L.x + (size_t)t0 * CD), CD, a(L.w), KC, a(L.cst0), a(L.br + (size_t)t0 * NV),
+                               a(L.ar + (size_t)t0 * NV), NV, a(L.dt), a(L.a), a(L.st), a(L.gout + (size_t)t0 * NV * S),
+                               NV * S, nt, NV, NK, S, EPS, a(L.gscr), gscr_bytes, s));
     }
     // ---- decode: one token per call; the GDN layer in one launch with the conv state alternating
     // between two arena slots

@@ -1,6 +1,7 @@
 """The C++ engine-shaped caller (tests/csrc/engine_harness.cpp) drives the C ABI as the reference's
 engine would (one arena, prompt split by it_prefill_chunks, scratch = the arena's dispatch room,
-then token-by-token decode with attention and the GDN layer each in one launch) over one attention
+each chunk's GDN layer through it_gdn_prefill, then token-by-token decode with attention and the
+GDN layer each in one launch) over one attention
 and one GDN layer; its outputs match the oracle: attention within 2e-3 with identical argmax, GDN
 outputs within 2e-3, the final state within 5e-3 and the conv state bit-exact."""
 import os
