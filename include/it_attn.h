@@ -123,7 +123,9 @@ int it_attn_f16_noalloc(const float* q, int q_tok_stride, const uint16_t* kc, co
  * writes its record to a caller-owned mailbox, per 16 output dims, and the waves that merge a
  * (token, head, 16 dims) unit wait for exactly the pieces they read. Results are bit-identical to
  * it_attn_f16's. Taken when the geometry qualifies: a split-K call (nt < 16) with at most 8 query
- * rows per KV head (nt * nh / nkv <= 8: decode), at most 256 splits of 64 keys (pos0 + nt <= 16384),
+ * rows per KV head (nt * nh / nkv <= 8: decode), at most 256 splits of 64 keys (pos0 + nt <= 16384)
+ * and enough of them to give every (token, head, 16-dim block) merge a wave of its own (nt * nh *
+ * 16 <= 4 * splits * nkv * row groups: with fewer, as at ctx 512, two launches are faster),
  * a mailbox of at least it_attn_mailbox_bytes(pos0 + nt, nt, nh) bytes, and a grid the device
  * holds at once (so every piece a merge waits for is being produced). Any other call runs
  * it_attn_f16 with `scratch` / `scratch_bytes`; it_attn_mailbox_would_launch reports which.

@@ -25,9 +25,9 @@ hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const
                               hipStream_t st);
 // Decode attention in one launch through a mailbox (see decode.hip). Returns hipSuccess with
 // *launched = false, having enqueued nothing, when the geometry does not qualify (splits of 64
-// keys, at most 256 splits, at most 8 query rows per KV head, mailbox_bytes(pos0 + nt, nt, nh)
-// bytes, the whole grid co-resident on the device); with dry_run, only reports whether it would
-// launch.
+// keys, at most 256 splits, at most 8 query rows per KV head, a wave per (row, 16-dim block) merge
+// unit, mailbox_bytes(pos0 + nt, nt, nh) bytes, the whole grid co-resident on the device); with
+// dry_run, only reports whether it would launch.
 size_t mailbox_bytes(long ctx, int nt, int nh);
 // mailbox header: word 0 the poison flag (0 = clear), word 1 this value once initialised
 constexpr uint32_t MAILBOX_MAGIC = 0x4D424F58u;

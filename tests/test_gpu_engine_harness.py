@@ -19,7 +19,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "tests", "csrc", "engine_harness")
 
 
-@pytest.mark.parametrize("tp,td,ub", [(200, 3, 64), (150, 2, 128), (600, 2, 512)])
+@pytest.mark.parametrize("tp,td,ub", [(200, 3, 64), (150, 2, 128), (600, 2, 512), (2100, 2, 512)])
 def test_engine_harness_matches_oracle(tmp_path, tp, td, ub):
     if not os.path.exists(EXE):
         pytest.fail(f"{EXE} is not built (__graft_entry__.build() runs make -C tests/csrc)")
@@ -38,7 +38,12 @@ def test_engine_harness_matches_oracle(tmp_path, tp, td, ub):
     r = subprocess.run([EXE, str(tmp_path), str(tp), str(td), str(ub)], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stderr
-    assert f"({td} attention calls in one launch), mailbox clean" in r.stdout
+    # decode steps whose geometry takes the one-launch form (enough splits for a wave per merge)
+    from irontimber_amd._lib import lib
+    mb_bytes = lib().it_attn_mailbox_bytes(T, 1, 16)
+    one = sum(lib().it_attn_mailbox_would_launch(t, 1, 256, 16, 2, mb_bytes) for t in range(tp, T))
+    assert one == (td if tp >= 2048 else 0)
+    assert f"({one} attention calls in one launch), mailbox clean" in r.stdout
     attn = np.fromfile(tmp_path / "attn_out.bin", np.float32).reshape(T, 16 * 256)
     gout = np.fromfile(tmp_path / "gdn_out.bin", np.float32).reshape(T, 32 * 128)
     st = np.fromfile(tmp_path / "state_out.bin", np.float32).reshape(32, 128, 128)

@@ -30,15 +30,17 @@ def _clean(mb):
     return words[0] == 0 and words[1] == MAGIC and (words[2:64] == 0).all() and (words[64:] == EMPTY).all()
 
 
-# (ctx, nt, nh, nkv, one launch expected): decode at the BASELINE geometries, short and ragged
-# contexts, other GQA groups, 256 splits (ctx 16384), verify rows whose last split is invisible to
-# the first token (pos0 % 64 == 63) with 8 rows per KV head, and geometries with more rows per KV
-# head, or a grid larger than the device holds at once (8 KV heads x 128 splits), which take the
-# two-launch path
-SHAPES = [(512, 1, 16, 2, True), (8192, 1, 16, 2, True), (1, 1, 16, 2, True), (65, 1, 16, 2, True),
-          (64, 1, 24, 4, True), (300, 5, 8, 8, True), (129, 2, 4, 1, True), (16384, 1, 16, 2, True),
-          (64 * 20 + 63 + 4, 4, 8, 8, True), (2000, 1, 32, 4, True), (8192, 8, 8, 8, False),
-          (8192, 4, 16, 2, False), (100, 3, 16, 2, False)]
+# (ctx, nt, nh, nkv, one launch expected): decode at the BASELINE geometry (ctx 8192), 256 splits
+# (ctx 16384), a one-key last split (ctx 2049), other GQA groups, verify rows whose last split is
+# invisible to the first token (pos0 % 64 == 63) with 8 rows per KV head; and geometries that take
+# the two-launch path: short contexts with fewer waves than merge units (ctx
+# 512, among them), more rows per KV head, or a grid larger than the device holds at once (8 KV
+# heads x 128 splits)
+SHAPES = [(8192, 1, 16, 2, True), (16384, 1, 16, 2, True), (2049, 1, 16, 2, True), (2000, 1, 32, 4, True),
+          (64 * 20 + 63 + 4, 4, 8, 8, True), (4096 + 1, 2, 8, 8, True), (8192 + 3, 3, 4, 2, True),
+          (512, 1, 16, 2, False), (1, 1, 16, 2, False), (65, 1, 16, 2, False), (64, 1, 24, 4, False),
+          (300, 5, 8, 8, False), (129, 2, 4, 1, False), (8192, 8, 8, 8, False), (8192, 4, 16, 2, False),
+          (100, 3, 16, 2, False)]
 
 
 @pytest.mark.parametrize("ctx,nt,nh,nkv,one", SHAPES)
@@ -64,7 +66,7 @@ def test_mailbox_sequence_and_baseline_argmax(dev):
     would use it): every result equals the two-launch path and the mailbox stays clean."""
     nh, nkv = 16, 2
     mb = ops.attn_mailbox(8192, 4, nh, dev)
-    for i, (ctx, nt) in enumerate([(8192, 1), (8192, 4), (37, 1), (8192, 1), (5000, 1), (8192, 4), (512, 1)]):
+    for i, (ctx, nt) in enumerate([(8192, 1), (8192, 4), (37, 1), (8192, 1), (5000, 1), (8192, 4), (3000, 1)]):
         announce(f"mailbox sequence step {i} ctx={ctx} nt={nt}")
         q, kb, vb, qd, kc, vc = _inputs(dev, 100 + i, ctx, nt, nh, nkv)
         got = host(ops.attn_f16_mailbox(qd, kc, vc, ctx - nt, nh, nkv, mb))
