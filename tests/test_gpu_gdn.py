@@ -376,6 +376,8 @@ def test_conv_kparity_geometry(dev):
     continues from that state."""
     MB = 1 << 20
     arena, params = oracle.kparity_draws(5 << 20, 1 << 16)
+    params = params.copy()
+    params[16:20] = -np.abs(params[16:20]) - 0.1     # set before every case (kparity.rs:63)
     cd, nt, K = 1000, 5, 4
     x = arena[:nt * cd].reshape(nt, cd)
     w = params[:cd * K].reshape(cd, K)
