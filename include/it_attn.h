@@ -149,6 +149,9 @@ int it_attn_f16_mailbox(const float* q, int q_tok_stride, const uint16_t* kc, co
 /* The choice it_attn_f16 makes for this geometry and scratch budget: *kernel 1 (split-K) or 2
  * (flash), *chunk keys per split (0 = flash in one pass, no scratch), *bytes of scratch used.
  * Returns nonzero if no split fits (only possible for nt < 16 with fewer than nt*nh*1040 bytes).
+ * Scratch per split: the split-K kernel's records are 260 f32 words per (token, head); the flash
+ * kernel's key-split records are 132 words per (token, head): {m, l, k, 0} and O as int16 in
+ * units of k = max|O| / 32767 (an error of at most max|O| / 65534 per value before the merge).
  * Host-only; the chunk loop is the reference's, src/vk/mod.rs:714-716. */
 int it_attn_plan(int pos0, int nt, int hd, int nh, int nkv, size_t scratch_bytes, int* kernel, int* chunk,
                  size_t* bytes);

@@ -58,6 +58,13 @@ size_t splitk_scratch(int pos0, int nt, int nh, int chunk) {
     return (size_t)nt * nh * smax * PART_WORDS * sizeof(float);
 }
 
+// Scratch of the flash kernel's key-split records: it::FLASH_REC words (16-byte header and O as
+// int16) per (token, head, split), half the split-K kernel's 260-word f32 records.
+size_t flash_scratch(int pos0, int nt, int nh, int chunk) {
+    const size_t smax = ((size_t)pos0 + nt + chunk - 1) / chunk;
+    return (size_t)nt * nh * smax * it::FLASH_REC * sizeof(float);
+}
+
 // Kernel and keys per split for an automatic call that must fit `budget` bytes of scratch. The
 // library's preferred split is kept when it fits; otherwise the split doubles until the records
 // fit, which is the reference's rule for its fixed arena (src/vk/mod.rs:714-716: C doubles from 64
@@ -72,9 +79,9 @@ bool plan_attn(int pos0, int nt, int nh, int nkv, int kernel, size_t budget, Att
     p.kernel = kernel;
     if (kernel == KERNEL_FLASH) {
         int c = flash_chunk(pos0, nt, nh, nkv, 0);
-        while (c && splitk_scratch(pos0, nt, nh, c) > budget) c = (2L * c >= total) ? 0 : 2 * c;
+        while (c && flash_scratch(pos0, nt, nh, c) > budget) c = (2L * c >= total) ? 0 : 2 * c;
         p.chunk = c;
-        p.bytes = c ? splitk_scratch(pos0, nt, nh, c) : 0;
+        p.bytes = c ? flash_scratch(pos0, nt, nh, c) : 0;
         return true;
     }
     int c = auto_chunk(pos0, nt, nh, nkv);
@@ -238,7 +245,7 @@ size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int k
     if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
     if (kernel == KERNEL_FLASH) {
         const int c = flash_chunk(pos0, nt, nh, nkv, chunk);
-        return c ? splitk_scratch(pos0, nt, nh, c) : 0;
+        return c ? flash_scratch(pos0, nt, nh, c) : 0;
     }
     if (kernel != KERNEL_SPLITK) return 0;
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
@@ -290,7 +297,7 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
         if (!c)
             return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st),
                          "it_attn_f16 (flash)");
-        const size_t need = splitk_scratch(pos0, nt, nh, c);
+        const size_t need = flash_scratch(pos0, nt, nh, c);
         if (scratch_bytes < need || !scratch)
             return fail("it_attn_f16: scratch of %zu bytes < %zu required (it_attn_scratch_bytes)", scratch_bytes, need);
         if (!aligned16(scratch)) return fail("it_attn_f16: scratch must be 16-byte aligned");

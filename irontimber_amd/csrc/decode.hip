@@ -97,7 +97,6 @@ constexpr uint32_t MB_EMPTY = 0xFFFFFFFFu;
 constexpr int MB_COHERENT = 16;     // buffer cache-policy bit: device-coherent access
 constexpr uint64_t MB_SPIN_TICKS = 1000000;   // 10 ms of the 100 MHz real-time counter
 typedef __amdgpu_buffer_rsrc_t MbRsrc;
-typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ MbRsrc mb_rsrc(float* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(p, 0, (int)bytes, 0x00020000);
@@ -364,10 +363,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
 // of them; the maxima and sums reduce through LDS.
 //   SL = 16: a quarter of the dims per workgroup (4 per row), for rows with many splits (decode).
 //   SL = 4 : the whole row per workgroup, for rows with at most 32 splits (chunked prefill).
-template <int SL>
+//   Q16: the flash key-split records ({m, l, k, 0}, then O as int16 in units of k; FLASH_REC words).
+template <int SL, bool Q16 = false>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ q, int qts, int pos0, int nh,
                                                           const float* __restrict__ part, int chunk, int smax,
                                                           float* __restrict__ out, int ots) {
+    constexpr int RW = Q16 ? FLASH_REC : PART;   // record words
     constexpr int DLN = 256 / SL;            // dim lanes, 4 dims each
     constexpr int DW = 4 * DLN;              // dims per workgroup
     __shared__ float red_m[SL];
@@ -376,7 +377,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     const int dq = blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int sg = tid / DLN, dl = tid % DLN, d0 = DW * dq + 4 * dl;
     const int n = pos0 + t + 1, ns = (n + chunk - 1) / chunk;
-    const float* base = part + (size_t)(t * nh + h) * smax * PART;
+    const float* base = part + (size_t)(t * nh + h) * smax * RW;
     const f4 gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + d0);
     float M = -INFINITY, den = 0.f;
     f4 o = {0.f, 0.f, 0.f, 0.f};
@@ -384,6 +385,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
         const int nb = min(COMB_SPL, (ns - s0 - sg + SL - 1) / SL);   // this lane's splits in the batch
         f2 hv[COMB_SPL];
         f4 ov[COMB_SPL];
+        float kv[COMB_SPL];
+        u2 qv[COMB_SPL];
         // branch-free batch: slots past the lane's count reload its last split and are masked after.
         // Headers load as {m, l} only: a wider load with dead lanes lets the register allocator
         // reuse them while the load is in flight, which costs a wait per load.
@@ -391,9 +394,22 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
         for (int j = 0; j < COMB_SPL; ++j) {
             // a lane with no split left in the batch (nb <= 0) reloads split ns - 1: every index
             // stays inside this row's records, so a buffer sized exactly for them is never overrun
-            const float* rec = base + (size_t)min(s0 + sg + SL * max(0, min(j, nb - 1)), ns - 1) * PART;
+            const float* rec = base + (size_t)min(s0 + sg + SL * max(0, min(j, nb - 1)), ns - 1) * RW;
             hv[j] = *(const f2*)rec;
-            ov[j] = ld_f4(rec + 4 + d0);
+            if (Q16) {
+                kv[j] = rec[2];
+                qv[j] = *((const u2*)(rec + 4) + (d0 >> 2));
+            } else {
+                ov[j] = ld_f4(rec + 4 + d0);
+            }
+        }
+        if (Q16) {
+#pragma unroll
+            for (int j = 0; j < COMB_SPL; ++j) {
+                // int16 pairs, low half first: sign-extend, convert, scale by k
+                const int32_t a = (int32_t)qv[j][0], b = (int32_t)qv[j][1];
+                ov[j] = f4{(float)((a << 16) >> 16), (float)(a >> 16), (float)((b << 16) >> 16), (float)(b >> 16)} * kv[j];
+            }
         }
         float mloc = M;
 #pragma unroll
@@ -760,6 +776,16 @@ hipError_t launch_attn_combine(const float* q, int qts, const float* part, int p
         attn_combine_wave_kernel<4><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
     else
         attn_combine_kernel<16><<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_combine_q16(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
+                                   float* out, int ots, hipStream_t st) {
+    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    if (smax <= 32)
+        attn_combine_kernel<4, true><<<dim3(1, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
+    else
+        attn_combine_kernel<16, true><<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
     return hipGetLastError();
 }
 

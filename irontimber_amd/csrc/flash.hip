@@ -18,10 +18,10 @@
 // no registers): tile t+1 streams in while tile t is computed, one barrier per tile.
 //
 // Key-split form (part != null): workgroup (row tile, KV head, split s) covers keys
-// [s*chunk, (s+1)*chunk) only and writes the partial records {m, l, 0, 0, o[256]} of its rows
-// (same layout as the decode partials, kernels/src/lib.rs:753-798) for the merge kernel. Used when
-// one pass would leave most CUs idle: a 64-token chunk after a long context has only
-// 2 * ceil(64*G/128) row tiles.
+// [s*chunk, (s+1)*chunk) only and writes a partial record of each of its rows for the merge
+// kernel: the {m, l} of the decode partials (kernels/src/lib.rs:753-798) plus a scale k, then O as
+// int16 in units of k (FLASH_REC words). Used when one pass would leave most CUs idle: a 64-token
+// chunk after a long context has only 2 * ceil(64*G/128) row tiles.
 #include "common.h"
 #include "internal.h"
 
@@ -286,27 +286,46 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     IT_WAIT_VMCNT(0);  // the loads issued past the end land in the buffers staged below
     __syncthreads();   // every wave is done with the last tile
     float* os = (float*)(w == 0 ? K0 : w == 1 ? K1 : w == 2 ? V0 : V1);
+    float amax = 0.f;   // max |O| over the lane's 128 dims of its row (the int16 record scale)
 #pragma unroll
     for (int db = 0; db < 8; ++db)
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
             const int ch = (32 * db + 8 * i4 + 4 * hh) >> 2;   // 16-byte chunk of the row
-            *(f4*)(os + c * HD + 4 * (ch ^ c)) = f4{o[db][4 * i4], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
+            const f4 v = f4{o[db][4 * i4], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
+            *(f4*)(os + c * HD + 4 * (ch ^ c)) = v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(v[j]));
         }
-    __shared__ float ml[4][2][32];   // per wave: running max and sum of its 32 queries
+    __shared__ float ml[4][3][32];   // per wave: running max, sum and max |O| of its 32 queries
     l_run = sum_xor32(l_run);
-    if (hh == 0) { ml[w][0][c] = m_run; ml[w][1][c] = l_run; }
+    amax = max_xor32(amax);
+    if (hh == 0) { ml[w][0][c] = m_run; ml[w][1][c] = l_run; ml[w][2][c] = amax; }
     const int rw = rt * BM + 32 * w;
     const int nrow = min(32, R - rw);
     int tq = rw / G, gq = rw - tq * G;   // (token, q-head) of row rw + i, walked as in the prologue
     if (part) {
-        // partial records of (token, head, split): m in natural-log units of the scaled score;
-        // stored non-temporally (34 MB per 64-token chunk at 8192: measured 154 -> 158 TFLOP/s)
+        // partial records of (token, head, split), FLASH_REC words each: {m, l, k, 0} with m in
+        // natural-log units of the scaled score and k = max|O| / 32767, then O as int16 in units of
+        // k (v_cvt_pk_norm_i16_f32 of O / max|O|): error <= max|O| / 65534 per value, half the
+        // bytes of an f32 record (over the 128 chunks of an 8192-token prompt: 158 -> 162 TFLOP/s,
+        // and the reference's arena holds the preferred split at twice as many chunk positions).
+        // Stored non-temporally (154 -> 158 TFLOP/s with the f32 records).
 #pragma unroll 4
         for (int i = 0; i < nrow; ++i) {
-            float* rec = part + ((size_t)(tq * nh + kh * G + gq) * smax + split) * 260;
-            if (l == 0) __builtin_nontemporal_store(f4{ml[w][0][i] * 0.6931471805599453f, ml[w][1][i], 0.f, 0.f}, (f4*)rec);
-            __builtin_nontemporal_store(*(const f4*)(os + i * HD + 4 * (l ^ i)), (f4*)(rec + 4 + 4 * l));
+            float* rec = part + ((size_t)(tq * nh + kh * G + gq) * smax + split) * FLASH_REC;
+            const float am = ml[w][2][i];
+            if (l == 0)
+                __builtin_nontemporal_store(f4{ml[w][0][i] * 0.6931471805599453f, ml[w][1][i], am * (1.0f / 32767.0f), 0.f},
+                                            (f4*)rec);
+            const f4 ov = *(const f4*)(os + i * HD + 4 * (l ^ i));
+            const float inv = am > 0.f ? __builtin_amdgcn_rcpf(am) : 0.f;
+            const auto p0 = __builtin_amdgcn_cvt_pknorm_i16(ov[0] * inv, ov[1] * inv);
+            const auto p1 = __builtin_amdgcn_cvt_pknorm_i16(ov[2] * inv, ov[3] * inv);
+            u2 pk;
+            pk[0] = __builtin_bit_cast(uint32_t, p0);
+            pk[1] = __builtin_bit_cast(uint32_t, p1);
+            __builtin_nontemporal_store(pk, (u2*)(rec + 4) + l);
             if (++gq == G) { gq = 0; ++tq; }
         }
         return;
@@ -359,7 +378,7 @@ hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, 
     attn_flash_kernel<<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, part, chunk, smax);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
+    return launch_attn_combine_q16(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
 }
 
 }  // namespace it

@@ -20,6 +20,10 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
                                 int nh, int nkv, int nt, float scale, float* part, int chunk, hipStream_t st);
 hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                float* out, int ots, hipStream_t st);
+// Key-split flash records in the compact form: {m, l, k, 0} + 256 int16 (O in units of k).
+constexpr int FLASH_REC = 4 + 128;
+hipError_t launch_attn_combine_q16(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
+                                   float* out, int ots, hipStream_t st);
 hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                               int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
                               hipStream_t st);

@@ -115,11 +115,12 @@ def test_scratch_bytes_policy():
     assert lib.it_attn_scratch_bytes(8188, 4, 256, 16, 2) == 4 * 16 * 128 * 260 * 4
     # whole-prompt prefill: flash, no scratch
     assert lib.it_attn_scratch_bytes(0, 8192, 256, 16, 2) == 0
-    # a 64-token chunk after 4096 positions: 8 flash row tiles, keys split 192 per split (22 splits)
-    assert lib.it_attn_scratch_bytes(4096, 64, 256, 16, 2) == 64 * 16 * 22 * 260 * 4
+    # a 64-token chunk after 4096 positions: 8 flash row tiles, keys split 192 per split (22
+    # splits); the flash kernel's records are 132 words (16-byte header, 256 int16)
+    assert lib.it_attn_scratch_bytes(4096, 64, 256, 16, 2) == 64 * 16 * 22 * 132 * 4
     # forced one-pass flash (chunk >= keys) and forced splits
     assert lib.it_attn_scratch_bytes_ex(4096, 64, 256, 16, 2, 2, 8192) == 0
-    assert lib.it_attn_scratch_bytes_ex(4096, 64, 256, 16, 2, 2, 1024) == 64 * 16 * 5 * 260 * 4
+    assert lib.it_attn_scratch_bytes_ex(4096, 64, 256, 16, 2, 2, 1024) == 64 * 16 * 5 * 132 * 4
 
 
 @pytest.mark.parametrize("nh,nkv", [(16, 2), (24, 4)])
