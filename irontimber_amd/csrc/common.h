@@ -101,6 +101,19 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (a + b) + (c + d);
 }
 
+// An offset that is the same in every lane, moved into scalar registers: arithmetic on it stays on
+// the scalar unit, and a kernel-argument pointer plus it plus a lane offset needs no 64-bit vector
+// arithmetic (each wave64 vector instruction costs 4 cycles, a 64-bit multiply several). The
+// pointer itself is not passed through an integer, which would lose its global address space.
+__device__ __forceinline__ size_t uniform_off(size_t v) {
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return ((size_t)hi << 32) | lo;
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
 // s_waitcnt immediate that waits until at most N vector-memory operations of this wave are still
 // outstanding, leaving the other counters alone. gfx9-family simm16 layout (gfx950 included):
 // bits [3:0] vmcnt[3:0], [6:4] expcnt (7 = no wait), [11:8] lgkmcnt (15 = no wait),

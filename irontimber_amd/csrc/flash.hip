@@ -92,7 +92,8 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     const int nrt = (R + BM - 1) / BM;
     const int rt = nrt - 1 - (int)blockIdx.x;          // heaviest row tile first
     const int kh = blockIdx.y;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, hh = l >> 5, c = l & 31;
+    // the wave index as a scalar: row counts, row walks and branches on them stay in SGPRs
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, hh = l >> 5, c = l & 31;
     const int r = rt * BM + 32 * w + c;                 // this lane's query row
     const bool rvalid = r < R;
     const int t = rvalid ? r / G : 0;
@@ -118,16 +119,18 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     h8 qb[16];
     {
         f4 qx[32];
-        const int rw = rt * BM + 32 * w;
+        const int rw = __builtin_amdgcn_readfirstlane(rt * BM + 32 * w);
         // row rr = token rr / G, q-head kh*G + rr % G: one division, then a walk over the 32 rows
-        // (a division per row costs ~40 instructions, ~10k cycles over the unrolled loop)
-        int tq = rw / G, gq = rw - tq * G;
-        const float* qlast = q + (size_t)((R - 1) / G) * qts + (size_t)(kh * G + (R - 1) % G) * 2 * HD + 4 * l;
+        // (a division per row costs ~40 instructions, ~10k cycles over the unrolled loop). The
+        // row offsets are scalar (uniform_off): per-row 64-bit vector address arithmetic cost
+        // ~60 cycles a row.
+        int tq = __builtin_amdgcn_readfirstlane(rw / G), gq = rw - tq * G;
+        const float* qlast = q + uniform_off((size_t)((R - 1) / G) * qts + (size_t)(kh * G + (R - 1) % G) * 2 * HD);
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
             // rows past R: any valid row (the last), zeroed below
-            const float* src = rw + i < R ? q + (size_t)tq * qts + (size_t)(kh * G + gq) * 2 * HD + 4 * l : qlast;
-            qx[i] = ld_f4(src);
+            const float* src = rw + i < R ? q + uniform_off((size_t)tq * qts + (size_t)(kh * G + gq) * 2 * HD) : qlast;
+            qx[i] = ld_f4(src + 4 * l);
             if (++gq == G) { gq = 0; ++tq; }
         }
         tile_to_lds(kc, kvd, kb0, kend, cj, K0, w, l);
@@ -297,13 +300,13 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
 #pragma unroll
             for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(v[j]));
         }
-    __shared__ float ml[4][3][32];   // per wave: running max, sum and max |O| of its 32 queries
+    __shared__ __align__(16) float ml[4][3][32];   // per wave: running max, sum and max |O| of its 32 queries
     l_run = sum_xor32(l_run);
     amax = max_xor32(amax);
     if (hh == 0) { ml[w][0][c] = m_run; ml[w][1][c] = l_run; ml[w][2][c] = amax; }
-    const int rw = rt * BM + 32 * w;
+    const int rw = __builtin_amdgcn_readfirstlane(rt * BM + 32 * w);
     const int nrow = min(32, R - rw);
-    int tq = rw / G, gq = rw - tq * G;   // (token, q-head) of row rw + i, walked as in the prologue
+    int tq = __builtin_amdgcn_readfirstlane(rw / G), gq = rw - tq * G;   // (token, q-head) of row rw + i
     if (part) {
         // partial records of (token, head, split), FLASH_REC words each: {m, l, k, 0} with m in
         // natural-log units of the scaled score and k = max|O| / 32767, then O as int16 in units of
@@ -311,22 +314,46 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         // bytes of an f32 record (over the 128 chunks of an 8192-token prompt: 158 -> 162 TFLOP/s,
         // and the reference's arena holds the preferred split at twice as many chunk positions).
         // Stored non-temporally (154 -> 158 TFLOP/s with the f32 records).
-#pragma unroll 4
-        for (int i = 0; i < nrow; ++i) {
-            float* rec = part + ((size_t)(tq * nh + kh * G + gq) * smax + split) * FLASH_REC;
-            const float am = ml[w][2][i];
-            if (l == 0)
-                __builtin_nontemporal_store(f4{ml[w][0][i] * 0.6931471805599453f, ml[w][1][i], am * (1.0f / 32767.0f), 0.f},
-                                            (f4*)rec);
-            const f4 ov = *(const f4*)(os + i * HD + 4 * (l ^ i));
-            const float inv = am > 0.f ? __builtin_amdgcn_rcpf(am) : 0.f;
-            const auto p0 = __builtin_amdgcn_cvt_pknorm_i16(ov[0] * inv, ov[1] * inv);
-            const auto p1 = __builtin_amdgcn_cvt_pknorm_i16(ov[2] * inv, ov[3] * inv);
+        // All 32 staged rows are read before any store (the accumulators are dead, so the
+        // registers are free): one row per iteration waited on each LDS read in turn (4.3 -> 3.4 us
+        // per workgroup for the 32 rows). Lane i < nrow writes row i's header. Each row's record
+        // base is scalar and its 1 / max|O| comes from the lane that owns the row (lanes c and
+        // c + 32 both hold row c's maximum), so a row costs a few vector instructions.
+        if (l < nrow) {
+            const int tl = (rw + l) / G, gl = rw + l - tl * G;
+            float* rec = part + ((size_t)(tl * nh + kh * G + gl) * smax + split) * FLASH_REC;
+            __builtin_nontemporal_store(f4{ml[w][0][l] * 0.6931471805599453f, ml[w][1][l], ml[w][2][l] * (1.0f / 32767.0f), 0.f},
+                                        (f4*)rec);
+        }
+        const float inv_c = amax > 0.f ? __builtin_amdgcn_rcpf(amax) : 0.f;   // row c
+        f4 ov[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) ov[i] = *(const f4*)(os + i * HD + 4 * (l ^ i));
+        // record index of row rw + i, walked in scalar registers: +smax within a token, and past
+        // the other KV heads' q-heads at a token boundary
+        size_t ridx = (size_t)(tq * nh + kh * G + gq) * smax + split;
+        const size_t rnext = (size_t)(nh - G + 1) * smax;
+        auto put = [&](int i) {
+            u2* dst = (u2*)(part + uniform_off(ridx * FLASH_REC + 4));
+            const float inv = readlane_f(inv_c, i);
             u2 pk;
-            pk[0] = __builtin_bit_cast(uint32_t, p0);
-            pk[1] = __builtin_bit_cast(uint32_t, p1);
-            __builtin_nontemporal_store(pk, (u2*)(rec + 4) + l);
-            if (++gq == G) { gq = 0; ++tq; }
+            pk[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_i16(ov[i][0] * inv, ov[i][1] * inv));
+            pk[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_i16(ov[i][2] * inv, ov[i][3] * inv));
+            __builtin_nontemporal_store(pk, dst + l);
+            if (++gq == G) { gq = 0; ridx += rnext; } else { ridx += smax; }
+        };
+        // a full 32-row wave (every wave when the row count is a multiple of 128) runs the rows
+        // as one straight block, so their conversions and stores interleave (a branch per row
+        // serialised each row's dependent chain). Two rows per 16-byte store instead measured
+        // slower (173.7 against 177.0 TFLOP/s over the 128 chunks): the phase is bound by how
+        // fast the CU's writes drain (~25 GB/s a CU), not by the instructions.
+        if (nrow == 32) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) put(i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (i < nrow) put(i);
         }
         return;
     }
