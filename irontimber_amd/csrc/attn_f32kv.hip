@@ -30,30 +30,40 @@ __device__ __forceinline__ f4 mfma16x16x4f32(float a, float b, f4 c) {
 
 }  // namespace
 
-// Workgroup = (key split s, KV head kh, group of tpw tokens); 4 waves. Query rows: r = lt*G + g for
-// the group's token lt and the KV head's q-head g (G = nh/nkv, tpw*G <= 16). Wave w takes keys
-// 16w..16w+15 of every 64-key tile of the split and runs its own online softmax; the four waves
-// are merged through LDS at the end and one record per (token, q-head) row is written:
-// part[((t*nh + h)*smax + s)*260] = {m, l, 0, 0, o[256]}, m in natural-log units.
+// Workgroup = (key split s, KV head kh, group of tpw tokens); 4 waves; RB blocks of 16 query rows
+// (rows r = lt*G + g for the group's token lt and the KV head's q-head g, G = nh/nkv,
+// tpw*G <= 16*RB). Per 64-key tile:
+//   scores  wave w: keys 16w .. 16w+15 against every row (its own 16 K rows, staged by itself);
+//   softmax the rows' tile maximum across the four waves through LDS (barrier 1); each wave
+//           writes its P (16 keys x rows) and its partial row sums to LDS (barrier 2, after which
+//           every wave's V rows have landed too);
+//   P.V     wave w: output dims 64w .. 64w+63 over all 64 keys (A = V^T from every wave's V rows,
+//           B = P^T from LDS).
+// Every wave then holds the same running max and sum and its own quarter of the dims, so the
+// record part[((t*nh + h)*smax + s)*260] = {m, l, 0, 0, o[256]} (m in natural-log units) goes out
+// straight from the accumulators, with no merge of the waves. RB = 2 (multi-token calls) makes
+// each K/V tile serve 32 rows: the 64-token catch-up reads the cache 16 times instead of 32.
 //
 // Each wave stages its own 16 K rows and 16 V rows in LDS with global_load_lds (one coalesced
 // 1 KB row per instruction, nothing held in VGPRs while in flight); rows are padded to 260 floats
-// so the 16 lanes of a quarter-wave reading 16 rows at one column hit distinct banks. No other
-// wave reads them, so a wave-local wait replaces a barrier.
+// so the 16 lanes of a quarter-wave reading 16 rows at one column hit distinct banks.
 constexpr int F32KV_ROW = F32KV_HD + 4;                 // padded LDS row (floats)
-constexpr int F32KV_WAVE = 2 * 16 * F32KV_ROW;          // K then V rows of one wave
 #define IT_F32KV_WAIT_VMCNT0() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
 #define IT_F32KV_WAIT_VMCNT16() asm volatile("s_waitcnt vmcnt(16)" ::: "memory")
 
+template <int RB>
 __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict__ q, int qts,
                                                          const float* __restrict__ kc, const float* __restrict__ vc,
                                                          int kvd, int pos0, int nh, int nkv, int nt, int tpw,
                                                          float qscale, float* __restrict__ part, int chunk, int smax) {
     typedef __attribute__((address_space(3))) void lds_void;
-    __shared__ float ml[4][2][16];
-    __shared__ __attribute__((aligned(16))) float smem[4 * F32KV_WAVE];   // tile staging, then the merge
+    constexpr int NR = 16 * RB;                                   // query rows per workgroup
+    __shared__ __attribute__((aligned(16))) float Ks[F32KV_KEYS * F32KV_ROW];
+    __shared__ __attribute__((aligned(16))) float Vs[F32KV_KEYS * F32KV_ROW];
+    __shared__ float Ps[F32KV_KEYS][NR];                          // P of the tile, [key][row]
+    __shared__ float mxs[4][NR], pss[4][NR];                      // per wave: row max, row sum
     const int s = blockIdx.x, kh = blockIdx.y, t0 = blockIdx.z * tpw;
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
     const int G = nh / nkv;
     const int ntg = min(tpw, nt - t0);
     const int rows = ntg * G;
@@ -61,8 +71,8 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
     const int kend = min(kb0 + chunk, pos0 + t0 + ntg);   // keys the group's last token sees
     if (kb0 >= kend) return;   // whole workgroup: no token of the group sees this split
     const int total = pos0 + nt;
-    float* Kw = smem + w * F32KV_WAVE;
-    float* Vw = Kw + 16 * F32KV_ROW;
+    float* Kw = Ks + 16 * w * F32KV_ROW;
+    float* Vw = Vs + 16 * w * F32KV_ROW;
 
     // This wave's 16 K and V rows of tile kt (keys kt + 16w + r), lane l bringing dims 4l .. 4l+3.
     // K rows first, V rows after: the scores and the softmax only wait for the K rows (16 loads
@@ -84,120 +94,133 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
     stage_k(kb0);   // the first tile's K rows are in flight while q loads below
 
     // Score product j = 4*jj + c contracts dims {16*jj + 4*lg + c : lg = 0..3}: lane l holds dims
-    // 16*jj + 4*lg .. +3 of its key row (A) and of its query row (B).
-    const bool rv = lr < rows;
-    const int tq = t0 + (rv ? lr / G : 0), hq = kh * G + (rv ? lr % G : 0);
-    const int nvis = pos0 + tq + 1;   // keys visible to this row
-    const float* qp = q + (size_t)tq * qts + (size_t)hq * 2 * F32KV_HD + 4 * lg;
-    const float qs = rv ? qscale : 0.f;   // padding rows: a valid row's load, scaled to zero
-    f4 qv[16];
+    // 16*jj + 4*lg .. +3 of its key row (A) and of its query row (B), for each row block.
+    int nvis[RB];
+    f4 qv[RB][16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) qv[j] = ld_f4(qp + 16 * j) * qs;
+    for (int rb = 0; rb < RB; ++rb) {
+        const int r = 16 * rb + lr;
+        const bool rv = r < rows;
+        const int tq = t0 + (rv ? r / G : 0), hq = kh * G + (rv ? r % G : 0);
+        nvis[rb] = pos0 + tq + 1;   // keys visible to this row
+        const float* qp = q + (size_t)tq * qts + (size_t)hq * 2 * F32KV_HD + 4 * lg;
+        const float qs = rv ? qscale : 0.f;   // padding rows: a valid row's load, scaled to zero
+#pragma unroll
+        for (int j = 0; j < 16; ++j) qv[rb][j] = ld_f4(qp + 16 * j) * qs;
+    }
     stage_v(kb0);
 
-    float m_run = -1e30f, l_run = 0.f;   // log2 units; finite floor keeps fully masked blocks NaN-free
-    f4 acc[16];                          // O^T blocks (dq, e): dims 16*lg + 4*ii + 64*dq + e of row lr
+    float m_run[RB], l_run[RB];   // log2 units; a finite floor keeps fully masked rows NaN-free
+    f4 acc[RB][4];                // O^T block e of row block rb: dims 64w + 4*(4lg + i) + e of row lr
 #pragma unroll
-    for (int b = 0; b < 16; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < RB; ++rb) {
+        m_run[rb] = -1e30f;
+        l_run[rb] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[rb][e] = f4{0.f, 0.f, 0.f, 0.f};
+    }
 
     for (int kt = kb0; kt < kend; kt += F32KV_KEYS) {
         if (kt != kb0) {
+            __syncthreads();   // every wave is done with the previous tile's K, V and P
             stage_k(kt);
             stage_v(kt);
         }
         IT_F32KV_WAIT_VMCNT16();   // K rows (and q): the 16 V loads may still fly
-        // S^T block: element i = key kt + 16w + 4lg + i, query row lr (4 independent chains).
-        f4 sa[4] = {};
+        // S^T block: element i = key kt + 16w + 4lg + i, query row lr of block rb.
+        f4 sc[RB];
 #pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-            const f4 kf = *(const f4*)(Kw + lr * F32KV_ROW + 16 * jj + 4 * lg);
+        for (int rb = 0; rb < RB; ++rb) {
+            f4 sa[2] = {};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) sa[c] = mfma16x16x4f32(kf[c], qv[jj][c], sa[c]);
+            for (int jj = 0; jj < 16; ++jj) {
+                const f4 kf = *(const f4*)(Kw + lr * F32KV_ROW + 16 * jj + 4 * lg);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) sa[c & 1] = mfma16x16x4f32(kf[c], qv[rb][jj][c], sa[c & 1]);
+            }
+            sc[rb] = sa[0] + sa[1];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kt + 16 * w + 4 * lg + i;
+                sc[rb][i] = key < nvis[rb] ? sc[rb][i] : -INFINITY;
+                mx = fmaxf(mx, sc[rb][i]);
+            }
+            mx = max_xor32(max_xor16(mx));
+            if (lg == 0) mxs[w][16 * rb + lr] = mx;
         }
-        f4 sc = (sa[0] + sa[1]) + (sa[2] + sa[3]);
-        float mx = -INFINITY;
+        __syncthreads();   // the four waves' row maxima
+        float alpha[RB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = kt + 16 * w + 4 * lg + i;
-            sc[i] = key < nvis ? sc[i] : -INFINITY;
-            mx = fmaxf(mx, sc[i]);
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = 16 * rb + lr;
+            const float mt = fmaxf(fmaxf(mxs[0][r], mxs[1][r]), fmaxf(mxs[2][r], mxs[3][r]));
+            const float m_new = fmaxf(m_run[rb], mt);
+            alpha[rb] = exp2f(m_run[rb] - m_new);
+            m_run[rb] = m_new;
+            float ps = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = exp2f(sc[rb][i] - m_new);
+                ps += p;
+                Ps[16 * w + 4 * lg + i][r] = p;
+            }
+            ps = sum_xor32(sum_xor16(ps));
+            if (lg == 0) pss[w][r] = ps;
         }
-        mx = max_xor32(max_xor16(mx));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = exp2f(m_run - m_new);
-        f4 p;
-        float ps = 0.f;
+        IT_F32KV_WAIT_VMCNT0();   // this wave's V rows
+        __syncthreads();          // every wave's P, row sums and V rows
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            p[i] = exp2f(sc[i] - m_new);
-            ps += p[i];
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = 16 * rb + lr;
+            l_run[rb] = l_run[rb] * alpha[rb] + ((pss[0][r] + pss[1][r]) + (pss[2][r] + pss[3][r]));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[rb][e] *= alpha[rb];
         }
-        l_run = l_run * alpha + sum_xor32(sum_xor16(ps));
-        m_run = m_new;
-        IT_F32KV_WAIT_VMCNT0();   // V rows
-        // O^T += V^T P^T: MFMA i takes key 4lg + i of the block (its A element from V, its B element
-        // this lane's p[i]); output block b = (dq, e) holds dims 16lg + 4ii + 64dq + e.
+        // O^T += V^T P^T, key quad kq: MFMA A element = V[4kq + lg][64w + 4lr + e] (one f4 read
+        // gives the four blocks e), B element = P[4kq + lg][row lr of block rb].
 #pragma unroll
-        for (int dq = 0; dq < 4; ++dq) {
-            f4 vv[4];
+        for (int kq = 0; kq < 16; ++kq) {
+            const f4 vv = *(const f4*)(Vs + (4 * kq + lg) * F32KV_ROW + 64 * w + 4 * lr);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) vv[i] = *(const f4*)(Vw + (4 * lg + i) * F32KV_ROW + 4 * lr + 64 * dq);
+            for (int rb = 0; rb < RB; ++rb) {
+                const float pb = Ps[4 * kq + lg][16 * rb + lr];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                f4 o = acc[4 * dq + e] * alpha;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) o = mfma16x16x4f32(vv[i][e], p[i], o);
-                acc[4 * dq + e] = o;
+                for (int e = 0; e < 4; ++e) acc[rb][e] = mfma16x16x4f32(vv[e], pb, acc[rb][e]);
             }
         }
-        // The next tile's DMA overwrites this wave's rows: every lane's LDS reads must be done.
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 
-    // Merge the four waves (each saw a different quarter of every tile) and write the records.
-    if (lg == 0) {
-        ml[w][0][lr] = m_run;
-        ml[w][1][lr] = l_run;
+    // Records straight from the accumulators: lane (lr, lg) holds dims 64w + 16lg + 4i + e
+    // (e = 0..3 contiguous) of row 16rb + lr; wave 0 adds the headers.
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int r = 16 * rb + lr;
+        if (r >= rows) continue;
+        const int tr = t0 + r / G, hr = kh * G + r % G;
+        float* rec = part + ((size_t)(tr * nh + hr) * smax + s) * 260;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *(f4*)(rec + 4 + 64 * w + 16 * lg + 4 * i) = f4{acc[rb][0][i], acc[rb][1][i], acc[rb][2][i], acc[rb][3][i]};
+        if (w == 0 && lg == 0) *(f4*)rec = f4{m_run[rb] * 0.69314718055994530942f, l_run[rb], 0.f, 0.f};
     }
-    __syncthreads();   // also: every wave is done with its staging rows, which Os reuses
-    f4* Os = (f4*)smem;   // [4][16][65] f4: +1 per row staggers the rows across banks
-    const float M = fmaxf(fmaxf(ml[0][0][lr], ml[1][0][lr]), fmaxf(ml[2][0][lr], ml[3][0][lr]));
-    const float f = exp2f(m_run - M);
-#pragma unroll
-    for (int dq = 0; dq < 4; ++dq)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            // block (dq, e) element ii: dim 16lg + 4ii + 64dq + e, e = 0..3 -> one f4
-            const f4 o = f4{acc[dq * 4 + 0][ii], acc[dq * 4 + 1][ii], acc[dq * 4 + 2][ii], acc[dq * 4 + 3][ii]} * f;
-            Os[(w * 16 + lr) * 65 + (16 * lg + 4 * ii + 64 * dq) / 4] = o;
-        }
-    __syncthreads();
-    // Thread -> (row r = tid >> 4, dims 16*(tid & 15) .. +15).
-    const int r = threadIdx.x >> 4, c4 = (threadIdx.x & 15) * 4;
-    if (r >= rows) return;
-    const float Mr = fmaxf(fmaxf(ml[0][0][r], ml[1][0][r]), fmaxf(ml[2][0][r], ml[3][0][r]));
-    float L = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) L += ml[ww][1][r] * exp2f(ml[ww][0][r] - Mr);
-    const int tr = t0 + r / G, hr = kh * G + r % G;
-    float* rec = part + ((size_t)(tr * nh + hr) * smax + s) * 260;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const f4 o = Os[(0 * 16 + r) * 65 + c4 + c] + Os[(1 * 16 + r) * 65 + c4 + c] + Os[(2 * 16 + r) * 65 + c4 + c] +
-                     Os[(3 * 16 + r) * 65 + c4 + c];
-        *(f4*)(rec + 4 + 4 * (c4 + c)) = o;
-    }
-    if ((threadIdx.x & 15) == 0) *(f4*)rec = f4{Mr * 0.69314718055994530942f, L, 0.f, 0.f};
 }
 
 hipError_t launch_attn_f32kv(const float* q, int qts, const float* kc, const float* vc, int kvd, int pos0, int nh,
                              int nkv, int nt, float scale, float* out, int ots, float* part, int chunk, hipStream_t st) {
     const int G = nh / nkv;
-    const int tpw = 16 / G;
     const int smax = (pos0 + nt + chunk - 1) / chunk;
-    const dim3 grid((unsigned)smax, (unsigned)nkv, (unsigned)((nt + tpw - 1) / tpw));
-    attn_f32kv_kernel<<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw,
-                                            scale * 1.44269504088896340736f, part, chunk, smax);
+    const float qs = scale * 1.44269504088896340736f;
+    // two 16-row blocks per workgroup once a call has more rows than one block holds
+    if (nt * G > 16) {
+        const int tpw = 32 / G;
+        const dim3 grid((unsigned)smax, (unsigned)nkv, (unsigned)((nt + tpw - 1) / tpw));
+        attn_f32kv_kernel<2><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk, smax);
+    } else {
+        const int tpw = 16 / G;
+        const dim3 grid((unsigned)smax, (unsigned)nkv, (unsigned)((nt + tpw - 1) / tpw));
+        attn_f32kv_kernel<1><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk, smax);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
