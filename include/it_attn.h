@@ -103,8 +103,8 @@ int it_attn_f16_ex(const float* q, int q_tok_stride, const uint16_t* kc, const u
 
 /* it_attn_f16 that allocates nothing and takes no scratch argument. No counterpart in the reference:
  * it is for callers that cannot allocate device memory or hand over a workspace (code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc). The split-K partial
- * records go to a file-scope device array of IT_NOALLOC_SCRATCH_BYTES (16 MiB) that each GPU the
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The partial records (split-K,
+ * or the flash kernel's int16 key-split records) go to a file-scope device array of IT_NOALLOC_SCRATCH_BYTES (16 MiB) that each GPU the
  * library runs on holds until the process ends; the split is fitted to that size as for a caller
  * buffer of the same size (it_attn_plan(..., IT_NOALLOC_SCRATCH_BYTES, ...) gives the choice), and
  * a geometry whose records cannot fit (split-K with nt*nh*1040 bytes above the maximum) is rejected
