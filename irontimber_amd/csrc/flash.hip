@@ -289,7 +289,11 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     IT_WAIT_VMCNT(0);  // the loads issued past the end land in the buffers staged below
     __syncthreads();   // every wave is done with the last tile
     float* os = (float*)(w == 0 ? K0 : w == 1 ? K1 : w == 2 ? V0 : V1);
-    float amax = 0.f;   // max |O| over the lane's 128 dims of its row (the int16 record scale)
+    // max |O| over the lane's 128 dims of its row (the int16 record scale), taken on the bit
+    // patterns of |O|: NaN patterns sort above infinity, so a NaN or infinite O (from a NaN or
+    // infinite V) reaches the record's scale and the merged output instead of being quantised
+    // away (a float maximum would skip a NaN)
+    uint32_t abits = 0u;
 #pragma unroll
     for (int db = 0; db < 8; ++db)
 #pragma unroll
@@ -298,11 +302,20 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
             const f4 v = f4{o[db][4 * i4], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
             *(f4*)(os + c * HD + 4 * (ch ^ c)) = v;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(v[j]));
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t b = __builtin_bit_cast(u4, v)[j] & 0x7fffffffu;
+                abits = b > abits ? b : abits;
+            }
         }
     __shared__ __align__(16) float ml[4][3][32];   // per wave: running max, sum and max |O| of its 32 queries
     l_run = sum_xor32(l_run);
-    amax = max_xor32(amax);
+    {
+        float a = __builtin_bit_cast(float, abits), b = a;
+        swap32(a, b);   // a, b: this lane's and its partner's (other half of the row), in some order
+        const uint32_t ua = __builtin_bit_cast(uint32_t, a), ub = __builtin_bit_cast(uint32_t, b);
+        abits = ua > ub ? ua : ub;
+    }
+    const float amax = __builtin_bit_cast(float, abits);
     if (hh == 0) { ml[w][0][c] = m_run; ml[w][1][c] = l_run; ml[w][2][c] = amax; }
     const int rw = __builtin_amdgcn_readfirstlane(rt * BM + 32 * w);
     const int nrow = min(32, R - rw);

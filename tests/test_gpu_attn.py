@@ -217,3 +217,30 @@ def test_reference_room_is_enough(dev, pos0, nt, cap):
     print(f"max_abs={err:.3g}")
     assert np.isfinite(got).all() and err <= TOL
     assert assert_argmax_agrees(got, want) == 0
+
+
+@pytest.mark.parametrize("kernel,chunk", [(ops.KERNEL_SPLITK, 0), (ops.KERNEL_FLASH, 0), (ops.KERNEL_FLASH, 64),
+                                          (ops.KERNEL_FLASH, 8192)])
+@pytest.mark.parametrize("bad", [float("nan"), float("inf")])
+def test_nonfinite_value_row_propagates(dev, kernel, chunk, bad):
+    """A NaN or infinite value in V (one key's row of one KV head) reaches every output row that
+    sees that key, as in the reference's arithmetic (cpu.rs:266-270 sums e_p v_p): no path may
+    quantise it away (the flash key-split records hold O as int16 against the row's max |O|, and
+    that maximum is taken so that NaN and infinity survive it). Rows of tokens whose visible keys
+    end before the key's 64-key tile, and the other KV head's rows, stay finite. (Rows that share
+    the key's tile but not the key may turn NaN too: their P is 0 there and the matrix product
+    computes 0 * NaN; cpu.rs never touches keys a row cannot see.)"""
+    nh, nkv, nt, pos0 = 16, 2, 64, 1000
+    ctx = pos0 + nt
+    announce(f"nonfinite V kernel={kernel} chunk={chunk} bad={bad}")
+    q, kb, vb = attn_inputs(5, ctx=ctx, nt=nt, nh=nh, nkv=nkv)
+    key = pos0 + 40                       # seen by tokens 40.. of the chunk; its tile starts at 1024
+    vb = vb.copy()
+    vb[key, 3] = np.float16(bad).view(np.uint16)   # dim 3 of KV head 0
+    got = host(ops.attn_f16(dev_f32(q.reshape(nt, -1), dev), dev_f16bits(kb, dev), dev_f16bits(vb, dev), pos0, nh,
+                            nkv, kernel=kernel, chunk=chunk))
+    g = got.reshape(nt, nh, 256)
+    head0 = slice(0, nh // nkv)
+    assert not np.isfinite(g[40:, head0, 3]).any()          # every row that sees the key
+    assert np.isfinite(g[:1024 - pos0]).all()                 # tokens whose keys end before its tile
+    assert np.isfinite(g[:, nh // nkv:]).all()                # the other KV head
