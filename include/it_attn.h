@@ -72,7 +72,8 @@ size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv);
  *   Token t attends keys 0..pos0+t (n = pos0+t+1, cpu.rs:260; kernels/src/lib.rs:764); q-head h
  *   reads KV head h/(nh/nkv) (cpu.rs:265).
  *   out  : f32 out[t*out_tok_stride + h*hd + d] = softmax(scale*q.K) V * sigmoid(gate).
- *   scratch: device buffer for the split-K partial records. it_attn_scratch_bytes(...) bytes give the
+ *   scratch: device buffer for the partial records (split-K: 260 f32 words per token, head and split;
+ *          flash key splits: 132 words, O as int16). it_attn_scratch_bytes(...) bytes give the
  *          library's preferred split; with fewer bytes the keys per split double until the records
  *          fit (the reference's rule for its fixed arena, src/vk/mod.rs:714-716), and the prefill
  *          kernel falls back to one pass with no scratch. The reference's own room,
@@ -91,7 +92,8 @@ int it_attn_f16(const float* q, int q_tok_stride, const uint16_t* kc, const uint
  *   kernel 0 = automatic (what it_attn_f16 does), 1 = split-K partials + combine,
  *          2 = flash prefill (needs nt >= 16): one pass with no scratch, or, when one pass would
  *          leave most of the GPU idle (a short chunk after a long context), key splits whose
- *          partial records are merged like kernel 1's.
+ *          partial records (132 words: {m, l, k, 0} and O as int16 in units of k) are merged like
+ *          kernel 1's.
  *   chunk  = keys per split (multiple of 64), 0 = automatic. For kernel 2 a chunk of at least
  *          pos0 + nt means one pass.
  * it_attn_scratch_bytes_ex gives the scratch for the same choice. With chunk = 0 the split is fitted
