@@ -61,7 +61,7 @@ __device__ __forceinline__ void split_hi_lo4(f4 x, h4& hi, h4& lo) {
 // diagonal-block inverses. Q never enters LDS: the Q K^T operands and e^G q are read from global
 // (the chunk's q rows stay in L2). The triangular solve runs in registers.
 constexpr int PREP_THREADS = 512;
-constexpr int KP = SD + 16;    // f16 row pitch of the K tile (288 B, 32-byte multiple)
+constexpr int KP = SD + 8;     // f16 row pitch of the K tile (272 B: 16 rows at one column hit distinct bank groups)
 
 // Workgroup id -> (chunk c, V head h) of the prep grid, launched 1-D. The nv / nk V heads that
 // share a QK head read the same q and k rows; they get ids 8 apart (one XCD, under the
