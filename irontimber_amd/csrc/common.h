@@ -138,6 +138,12 @@ __device__ __forceinline__ void swap16(float& a, float& b) {
 __device__ __forceinline__ void swap32(float& a, float& b) {
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
+// Two values reduced by one swap: fold16(a, b) returns, in the even 16-lane rows, a summed over
+// the row pair (rows 0+1, 2+3) and, in the odd rows, b summed likewise; fold32(a, b) returns a
+// summed over lanes l and l ^ 32 in the lower half and b in the upper half. Halves the swaps of a
+// reduction of several values whose results may end up in different lanes.
+__device__ __forceinline__ float fold16(float a, float b) { swap16(a, b); return a + b; }
+__device__ __forceinline__ float fold32(float a, float b) { swap32(a, b); return a + b; }
 // max / sum over lanes l and l ^ 32, and over l and l ^ 16
 __device__ __forceinline__ float max_xor32(float v) { float a = v, b = v; swap32(a, b); return fmaxf(a, b); }
 __device__ __forceinline__ float sum_xor32(float v) { float a = v, b = v; swap32(a, b); return a + b; }

@@ -244,10 +244,22 @@ __global__ __launch_bounds__(256) void l2norm_kernel(float* __restrict__ x, int 
 // Sum over the 16 lanes of a wave that share l & 3 (lane bits 2-5), every lane receiving its
 // group's sum: two DPP row rotates (by 4 and 8) sum within each 16-lane row, then the rows are
 // added by swapping lane halves (v_permlane16_swap, then v_permlane32_swap). No LDS traffic.
-__device__ __forceinline__ float sum_lanes_stride4(float v) {
+__device__ __forceinline__ float rowsum_stride4(float v) {
     v += dppc<0x124>(v);   // row_ror:4
     v += dppc<0x128>(v);   // row_ror:8
-    return sum_xor32(sum_xor16(v));
+    return v;
+}
+__device__ __forceinline__ float sum_lanes_stride4(float v) { return sum_xor32(sum_xor16(rowsum_stride4(v))); }
+// The wave's column sums of p and r (4 columns each) with 6 swaps instead of 16: row sums, then
+// (p_j, r_j) folded over row pairs and (j, j + 1) over the wave halves. Lane l of row rho = l >> 4
+// ends with, for its column group l & 3, the sums of (rho & 1 ? r : p) elements rho >> 1 (u0) and
+// 2 + (rho >> 1) (u1).
+__device__ __forceinline__ void colsums_pr(f4 p, f4 r, float& u0, float& u1) {
+    float t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] = fold16(rowsum_stride4(p[j]), rowsum_stride4(r[j]));
+    u0 = fold32(t[0], t[1]);
+    u1 = fold32(t[2], t[3]);
 }
 
 // Workgroup id -> (16-column block cb, V head h) of the 8 x nv step grid, launched 1-D.
@@ -268,7 +280,9 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
                                                        float* __restrict__ out, int ots, int nt, int nv, int nk,
                                                        float* __restrict__ ck, int ck_after) {
     constexpr int S = 128;
-    __shared__ f4 red1[4][4], red2[4][4];
+    // per token parity: {S^T k, S^T q} column sums of each wave, and its k.q
+    __shared__ f4 red[2][4][2][4];
+    __shared__ float rkq[2][4];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
     int cb, h;
     step_wg(blockIdx.x, nv, cb, h);
@@ -303,22 +317,28 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
         const float beta = sigmoid_hw(cur.b);
         const float eg = exp_hw(softplus_hw(cur.a + dth) * ah);
         s0 *= eg; s1 *= eg;
-        f4 p = s0 * k0 + s1 * k1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = sum_lanes_stride4(p[j]);
-        if (l < 4) red1[w][l] = p;
+        // With S' = S + k delta^T (S already decayed), S'^T q = S^T q + (k.q) delta: S^T k, S^T q
+        // and k.q reduce together, one exchange and one barrier a token. The parity-indexed
+        // buffers are rewritten two tokens later, after every wave has passed the next barrier.
+        float u0, u1;
+        colsums_pr(s0 * k0 + s1 * k1, s0 * q0 + s1 * q1, u0, u1);
+        const float kq = sum_lanes_stride4(k0 * q0 + k1 * q1);
+        const int b = t & 1;
+        if ((l & 15) < 4) {
+            const int rho = l >> 4;
+            float* d = (float*)&red[b][w][rho & 1][cg];
+            d[rho >> 1] = u0;
+            d[2 + (rho >> 1)] = u1;
+        }
+        if (l == 0) rkq[b][w] = kq;
         __syncthreads();
-        const f4 sk = red1[0][cg] + red1[1][cg] + red1[2][cg] + red1[3][cg];
+        const f4 sk = (red[b][0][0][cg] + red[b][1][0][cg]) + (red[b][2][0][cg] + red[b][3][0][cg]);
         const f4 delta = (v - sk) * beta;
         s0 += k0 * delta; s1 += k1 * delta;
-        f4 o = s0 * q0 + s1 * q1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = sum_lanes_stride4(o[j]);
-        if (l < 4) red2[w][l] = o;
-        __syncthreads();
         if (tid < 4) {
-            const f4 ot = (red2[0][cg] + red2[1][cg] + red2[2][cg] + red2[3][cg]) * scale;
-            *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = ot;
+            const f4 sq = (red[b][0][1][cg] + red[b][1][1][cg]) + (red[b][2][1][cg] + red[b][3][1][cg]);
+            const float kqs = (rkq[b][0] + rkq[b][1]) + (rkq[b][2] + rkq[b][3]);
+            *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = (sq + kqs * delta) * scale;
         }
         if (ck && t == ck_after) {
             float* cb_ = ck + (size_t)h * S * S;
@@ -341,8 +361,8 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
 // by the first column block of the QK head's first V head, v channels by row pair 0 of each
 // workgroup. With one wave per SIMD every instruction is on the critical path, so the activations
 // use the hardware exp2 / log2 / reciprocal (a few ulp), and the q/k norms, being per-head scalars,
-// are applied after the S k and S^T q sums: their sums of squares share the S k exchange (two
-// barriers a token instead of three). Results agree with conv + L2 + gdn_step_kernel to rounding.
+// are applied after the S k and S^T q sums: their sums of squares share the one exchange of the
+// token (one barrier a token). Results agree with conv + L2 + gdn_step_kernel to rounding.
 constexpr int FUSED_TMAX = 4;
 
 template <int K>
@@ -353,8 +373,10 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     int ots, int nt, int nv, int nk, float eps, float* __restrict__ ck_state, float* __restrict__ ck_conv,
     int ck_after) {
     constexpr int S = 128;
-    __shared__ f4 red1[4][4], red2[4][4];
-    __shared__ f2 nrm[2][4];   // per wave: {sum q^2, sum k^2} of its 16 row pairs, per token parity
+    // per token parity, per wave: {S^T k, S^T q} column sums and {sum q^2, sum k^2, k.q} of its
+    // 16 row pairs (raw conv outputs, before the head norms)
+    __shared__ f4 red[2][4][2][4];
+    __shared__ f4 nrm[2][4];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
     int cb, h;
     step_wg(blockIdx.x, nv, cb, h);
@@ -446,34 +468,38 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
         wnq[K - 2] = xq[t];
         wnk[K - 2] = xk[t];
         wnv[K - 2] = xv[t];
-        // ---- recurrence (gdn_step_kernel) with the q/k L2 norms folded in: the head norms are
-        // scalars, so S k = |k| * S k_raw-hat and S^T q likewise; their sums of squares ride in the
-        // same LDS exchange as S k (one barrier fewer than normalising first)
+        // ---- recurrence (gdn_step_kernel) with the q/k L2 norms folded in. The head norms are
+        // scalars fq, fk, so with raw q, k: S^T k-hat = fk S^T k, and with S' = S + k-hat delta^T
+        // (S already decayed), S'^T q-hat = fq S^T q + fq fk (k.q) delta. The two column sums, the
+        // sums of squares and k.q all ride in one LDS exchange: one barrier a token. The parity-
+        // indexed buffers are rewritten two tokens later, after every wave has passed the next barrier.
         const float beta = sigmoid_hw(brt[t]);
         const float eg = exp_hw(softplus_hw(art[t] + dth) * ah);
         s0 *= eg; s1 *= eg;
-        f4 p = s0 * k[0] + s1 * k[1];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = sum_lanes_stride4(p[j]);
-        const float sq = sum_lanes_stride4(q[0] * q[0] + q[1] * q[1]);
-        const float sk2 = sum_lanes_stride4(k[0] * k[0] + k[1] * k[1]);
-        if (l < 4) red1[w][l] = p;
-        if (l == 0) nrm[t & 1][w] = f2{sq, sk2};
+        float u0, u1;
+        colsums_pr(s0 * k[0] + s1 * k[1], s0 * q[0] + s1 * q[1], u0, u1);
+        // the three scalars: sum q^2 ends in row 0, sum k^2 in row 1, k.q in rows 2 and 3
+        const float sn = fold32(fold16(rowsum_stride4(q[0] * q[0] + q[1] * q[1]),
+                                       rowsum_stride4(k[0] * k[0] + k[1] * k[1])),
+                                sum_xor16(rowsum_stride4(k[0] * q[0] + k[1] * q[1])));
+        const int b = t & 1;
+        if ((l & 15) < 4) {
+            const int rho = l >> 4;
+            float* d = (float*)&red[b][w][rho & 1][cg];
+            d[rho >> 1] = u0;
+            d[2 + (rho >> 1)] = u1;
+        }
+        if (l == 0 || l == 16 || l == 32) ((float*)&nrm[b][w])[l >> 4] = sn;
         __syncthreads();
-        const f2 n = (nrm[t & 1][0] + nrm[t & 1][1]) + (nrm[t & 1][2] + nrm[t & 1][3]);
+        const f4 n = (nrm[b][0] + nrm[b][1]) + (nrm[b][2] + nrm[b][3]);
         const float fq = 1.0f / fmaxf(sqrtf(n[0]), eps), fk = 1.0f / fmaxf(sqrtf(n[1]), eps);
-        const float q0 = q[0] * fq, q1 = q[1] * fq, k0 = k[0] * fk, k1 = k[1] * fk;
-        const f4 skv = (red1[0][cg] + red1[1][cg] + red1[2][cg] + red1[3][cg]) * fk;
+        const float k0 = k[0] * fk, k1 = k[1] * fk;
+        const f4 skv = ((red[b][0][0][cg] + red[b][1][0][cg]) + (red[b][2][0][cg] + red[b][3][0][cg])) * fk;
         const f4 delta = (v - skv) * beta;
         s0 += k0 * delta; s1 += k1 * delta;
-        f4 o = s0 * q0 + s1 * q1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = sum_lanes_stride4(o[j]);
-        if (l < 4) red2[w][l] = o;
-        __syncthreads();
         if (tid < 4) {
-            const f4 ot = (red2[0][cg] + red2[1][cg] + red2[2][cg] + red2[3][cg]) * scale;
-            *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = ot;
+            const f4 sq4 = (red[b][0][1][cg] + red[b][1][1][cg]) + (red[b][2][1][cg] + red[b][3][1][cg]);
+            *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = (sq4 * fq + (fq * fk * n[2]) * delta) * scale;
         }
         if (t == ck_after) {   // MTP verify checkpoint: both states after this token, from registers
             if (ck_state) {
@@ -556,7 +582,9 @@ __global__ __launch_bounds__(256) void gdn_step_head_kernel(
     int ots, int nt, int nk, const float* __restrict__ z, int zts, const float* __restrict__ nw, float eps,
     float* __restrict__ ck, int ck_after) {
     constexpr int S = 128, R = 16;
-    __shared__ f4 red1[4][32], red2[4][32];
+    // per token parity, per wave: {S^T k, S^T q} column sums and k.q
+    __shared__ f4 red[2][4][2][32];
+    __shared__ float rkq[2][4];
     const int h = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
     const int cq = tid & 31, rg = tid >> 5;
     const int kh = h % nk, qk = nk * S, j0 = 4 * cq, i0 = R * rg;
@@ -596,30 +624,34 @@ __global__ __launch_bounds__(256) void gdn_step_head_kernel(
         const f4 v = cur.v, zv = cur.z;
         const float beta = sigmoid_hw(cur.b);
         const float eg = exp_hw(softplus_hw(cur.a + dth) * ah);
-        f4 p = {};
+        // With S' = S + k delta^T (S already decayed), S'^T q = S^T q + (k.q) delta: S^T k, S^T q
+        // and k.q reduce together, one exchange and one barrier a token.
+        f4 p = {}, sq = {};
+        float kq = 0.f;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             s[r] *= eg;
             p += s[r] * k[r / 4][r & 3];
+            sq += s[r] * q[r / 4][r & 3];
+            kq += k[r / 4][r & 3] * q[r / 4][r & 3];
         }
+        // one swap per column: lanes 0-31 end with the wave's S^T k sums, lanes 32-63 with S^T q
+        f4 u;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = sum_xor32(p[j]);
-        if (l < 32) red1[w][cq] = p;
+        for (int j = 0; j < 4; ++j) u[j] = fold32(p[j], sq[j]);
+        kq = sum_xor32(kq);
+        const int b = t & 1;
+        red[b][w][l >> 5][cq] = u;
+        if (l == 0) rkq[b][w] = kq;
         __syncthreads();
-        const f4 sk = red1[0][cq] + red1[1][cq] + red1[2][cq] + red1[3][cq];
+        const f4 sk = (red[b][0][0][cq] + red[b][1][0][cq]) + (red[b][2][0][cq] + red[b][3][0][cq]);
         const f4 delta = (v - sk) * beta;
-        f4 o = {};
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            s[r] += k[r / 4][r & 3] * delta;
-            o += s[r] * q[r / 4][r & 3];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = sum_xor32(o[j]);
-        if (l < 32) red2[w][cq] = o;
-        __syncthreads();
+        for (int r = 0; r < R; ++r) s[r] += k[r / 4][r & 3] * delta;
         if (w == 0) {
-            const f4 ot = (red2[0][cq] + red2[1][cq] + red2[2][cq] + red2[3][cq]) * scale;
+            const f4 so = (red[b][0][1][cq] + red[b][1][1][cq]) + (red[b][2][1][cq] + red[b][3][1][cq]);
+            const float kqs = (rkq[b][0] + rkq[b][1]) + (rkq[b][2] + rkq[b][3]);
+            const f4 ot = (so + kqs * delta) * scale;
             f4 res = ot;
             if (z) {
                 // lanes 32..63 repeat lanes 0..31: the wave sum counts every column twice
@@ -635,8 +667,8 @@ __global__ __launch_bounds__(256) void gdn_step_head_kernel(
 #pragma unroll
             for (int r = 0; r < R; ++r) *(f4*)(cb_ + (size_t)(i0 + r) * S + j0) = s[r];
         }
-        // red1/red2 are rewritten by the next token only after its first barrier, which every
-        // wave reaches after finishing this token's reads.
+        // red[b] / rkq[b] are rewritten two tokens later, after the next token's barrier, which
+        // every wave reaches only after finishing this token's reads.
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) *(f4*)(sb + (size_t)(i0 + r) * S + j0) = s[r];
