@@ -295,9 +295,11 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
     }
 
     // ---- records {m (natural log units), l, 0, 0, o[256]} straight from registers: adding lanes l
-    // and l ^ 32 sums the P_hi and P_lo halves, after which lane (c, g < 2) holds rows 4g..4g+3 of
-    // each block at dims 64w + 16n + c (16 lanes store 64 contiguous bytes of a row), and the ones
-    // product gives every wave the full row sums. Wave 0 adds the headers.
+    // and l ^ 32 sums the P_hi and P_lo halves. One swap per pair of dim blocks (n, n + 1) leaves
+    // the sum of block n in the lower half-wave and of block n + 1 in the upper, so lane (c, g)
+    // holds row 4(g & 1) + i at dims 64w + 16(2k + (g >> 1)) + c for k = 0, 1 (16 lanes store 64
+    // contiguous bytes of a row), and the ones product gives every wave the full row sums. Wave 0's
+    // lower half adds the headers.
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         if (r0 + 8 * b >= R) continue;   // wave-uniform
@@ -307,13 +309,15 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
         float mh[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) mh[i] = __shfl(m_run[b], (4 * g + i) & 7);   // lane row = c & 7
+        // row sums of rows 4(g & 1) + i: rows i = 0, 2 in the lower half-wave, 1, 3 in the upper
+        const float lsp[2] = {fold32(lacc[b][0], lacc[b][1]), fold32(lacc[b][2], lacc[b][3])};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float v[4];
-#pragma unroll
-            for (int n = 0; n < 4; ++n) v[n] = sum_xor32(acc[b][n][i]);
-            const float ls = sum_xor32(lacc[b][i]);
-            if (l < 32 && rb + i < R) {
+            const int hi = l >> 5;
+            const float v[2] = {fold32(acc[b][0][i], acc[b][1][i]), fold32(acc[b][2][i], acc[b][3][i])};
+            const float ls = lsp[i >> 1];
+            const bool hdr = hi == (i & 1) && c == 0;   // the lanes that hold row 4(g & 1) + i's sum
+            if (rb + i < R) {
                 const int th = tq * nh + kh * G + gq;
                 if constexpr (MB) {
                     // mailbox pieces of dim blocks 4w .. 4w+3: dims from every lane, {m, l} from
@@ -322,8 +326,8 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
                     const MbRsrc mbr = mb_rsrc(mb, mbb);
                     if (p0 <= pos0 + tq) {
 #pragma unroll
-                        for (int n = 0; n < 4; ++n) mb_store1(mbr, mb_piece(th, 4 * w + n, s, smax) + c, v[n]);
-                        if (c < 4) mb_store2(mbr, mb_piece(th, 4 * w + c, s, smax) + 16, f2{mh[i] * LN2_F, ls});
+                        for (int k = 0; k < 2; ++k) mb_store1(mbr, mb_piece(th, 4 * w + 2 * k + hi, s, smax) + c, v[k]);
+                        if (hi == (i & 1) && c < 4) mb_store2(mbr, mb_piece(th, 4 * w + c, s, smax) + 16, f2{mh[i] * LN2_F, ls});
                     }
                 } else if constexpr (NB >= 2) {
                     // blocks of 16 or more rows (verify at nt = 4) store their records
@@ -331,13 +335,13 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
                     // decode (10.3 -> 11.1)
                     float* rec = part + ((size_t)th * smax + s) * PART;
 #pragma unroll
-                    for (int n = 0; n < 4; ++n) __builtin_nontemporal_store(v[n], rec + 4 + 64 * w + 16 * n + c);
-                    if (w == 0 && c == 0) __builtin_nontemporal_store(f4{mh[i] * LN2_F, ls, 0.f, 0.f}, (f4*)rec);
+                    for (int k = 0; k < 2; ++k) __builtin_nontemporal_store(v[k], rec + 4 + 64 * w + 16 * (2 * k + hi) + c);
+                    if (w == 0 && hdr) __builtin_nontemporal_store(f4{mh[i] * LN2_F, ls, 0.f, 0.f}, (f4*)rec);
                 } else {
                     float* rec = part + ((size_t)th * smax + s) * PART;
 #pragma unroll
-                    for (int n = 0; n < 4; ++n) rec[4 + 64 * w + 16 * n + c] = v[n];
-                    if (w == 0 && c == 0) *(f4*)rec = f4{mh[i] * LN2_F, ls, 0.f, 0.f};
+                    for (int k = 0; k < 2; ++k) rec[4 + 64 * w + 16 * (2 * k + hi) + c] = v[k];
+                    if (w == 0 && hdr) *(f4*)rec = f4{mh[i] * LN2_F, ls, 0.f, 0.f};
                 }
             }
             if (++gq == G) { gq = 0; ++tq; }
