@@ -225,21 +225,37 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
             }
         }
         // ---- hi + lo, scale to log2 units, mask; wave-local maxima
-        float x[NB][4];
+        float x[NB][4], mx[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const int lb = min(lim[b], pend);
-            float mx = -INFINITY;
+            mx[b] = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float v = sacc[b][i] + dpp_f<0x128>(sacc[b][i]);   // row_ror:8 -> column c ^ 8
                 const int key = kb + 16 * w + 4 * g + i;
                 x[b][i] = key < lb ? v * sc2 : -INFINITY;
-                mx = fmaxf(mx, x[b][i]);
+                mx[b] = fmaxf(mx[b], x[b][i]);
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            if (g == 0 && c < 8) Mx[w][8 * b + c] = mx;
+        }
+        // maxima over the four 16-lane rows by lane swaps (no LDS). With several blocks the swaps
+        // fold them: blocks (0, 1) and (2, 3) share a row-pair swap, the two results share the
+        // half-wave swap, and 16-lane row g ends with block g's maxima.
+        if constexpr (NB == 1) {
+            const float m1 = max_xor32(max_xor16(mx[0]));
+            if (g == 0 && c < 8) Mx[w][c] = m1;
+        } else {
+            float a0 = mx[0], b0 = mx[1];
+            swap16(a0, b0);
+            float t0 = fmaxf(a0, b0), t1 = t0;
+            if constexpr (NB > 2) {
+                float a1 = mx[2], b1 = NB > 3 ? mx[NB - 1] : -INFINITY;
+                swap16(a1, b1);
+                t1 = fmaxf(a1, b1);
+            }
+            swap32(t0, t1);
+            const float m = fmaxf(t0, t1);
+            if (g < NB && c < 8) Mx[w][8 * g + c] = m;
         }
         __syncthreads();   // A: tile maxima
 #pragma unroll

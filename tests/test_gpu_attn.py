@@ -41,7 +41,7 @@ def test_ragged_and_group_shapes(dev, ctx, nt, nh, nkv):
     assert np.abs(got - want).max() <= 1e-5
 
 
-@pytest.mark.parametrize("nt", [1, 4])
+@pytest.mark.parametrize("nt", [1, 3, 4])
 @pytest.mark.parametrize("chunk", [64, 128, 192, 256, 1024, 8192])
 def test_split_invariance(dev, chunk, nt):
     """The result does not depend on how the keys are split (invariant of the LSE merge); chunks
