@@ -523,20 +523,24 @@ __device__ __forceinline__ void merge_wave_store(float gv, int nh, int t, int h,
         swap16(a, b);
         r4[i] = a + b;
     }
+    // within each 16-lane row by DPP (no LDS): the partner of lane i is 15 - i (row_mirror, the
+    // other b3) and then 7 - i within its half (row_half_mirror, the other b2), so the partner
+    // sets of lanes i, i ^ 1, i ^ 2, i ^ 3 together cover the row; each lane keeps the half its own
+    // bits select, and the quad sums finish by quad_perm
     const bool b3 = (l >> 3) & 1, b2 = (l >> 2) & 1;
     float r2[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const float keep = b3 ? r4[2 + i] : r4[i], give = b3 ? r4[i] : r4[2 + i];
-        r2[i] = keep + __shfl_xor(give, 8);
+        r2[i] = keep + dppc<0x140>(give);   // row_mirror
     }
     float v;
     {
         const float keep = b2 ? r2[1] : r2[0], give = b2 ? r2[0] : r2[1];
-        v = keep + __shfl_xor(give, 4);
+        v = keep + dppc<0x141>(give);       // row_half_mirror
     }
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 1);
+    v += dppc<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dppc<0xB1>(v);   // quad_perm [1,0,3,2]
     if ((l & 3) == 0) {
         const int d = d0 + 8 * (l >> 5) + 4 * ((l >> 4) & 1) + 2 * ((l >> 3) & 1) + ((l >> 2) & 1);
         out[(size_t)t * ots + (size_t)h * HD + d] = v / den * sigmoidf_(gv);
