@@ -385,8 +385,9 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     const int j0 = cb * 16 + 4 * cg, i0 = 2 * rp;
     const int cq = kh * S + i0, ck = qk + kh * S + i0, cv = 2 * qk + h * S + j0;   // channel bases
     float* sb = state + (size_t)h * S * S;
-    // every load up front: state, tokens, weights, the conv window
-    f4 s0 = ld_f4(sb + (size_t)i0 * S + j0), s1 = ld_f4(sb + (size_t)(i0 + 1) * S + j0);
+    // every load up front: tokens, weights, the conv window, the gates, then the state. The
+    // vector-memory counter retires in order, so the conv inputs issued first can be used (the
+    // conv, SiLU and norm sums run) while the state slice is still landing.
     f2 xq[FUSED_TMAX], xk[FUSED_TMAX];
     f4 xv[FUSED_TMAX];
 #pragma unroll
@@ -437,8 +438,9 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
         brt[t] = br[(size_t)min(t, nt - 1) * bts + h];
         art[t] = ar[(size_t)min(t, nt - 1) * bts + h];
     }
-    const float scale = 1.0f / sqrtf((float)S);
     const float dth = dt[h], ah = A[h];
+    f4 s0 = ld_f4(sb + (size_t)i0 * S + j0), s1 = ld_f4(sb + (size_t)(i0 + 1) * S + j0);
+    const float scale = 1.0f / sqrtf((float)S);
 #pragma unroll
     for (int t = 0; t < FUSED_TMAX; ++t) {
         if (t >= nt) break;   // uniform
