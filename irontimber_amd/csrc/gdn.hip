@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------------
-// Decode layer in one launch: conv + SiLU + q/k L2 norm + recurrence for up to FUSED_TMAX tokens.
+// Decode layer in one launch: conv + SiLU + q/k L2 norm + recurrence for up to 4 tokens.
 // Same workgroup and thread layout as gdn_step_kernel; each thread also runs the conv of the
 // channels it consumes (q and k at rows i0, i0+1 of its QK head, v at columns j0..j0+3 of its V
 // head) from the old conv state, so no workgroup waits for another. The q/k head norms sum over
@@ -363,9 +363,9 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
 // use the hardware exp2 / log2 / reciprocal (a few ulp), and the q/k norms, being per-head scalars,
 // are applied after the S k and S^T q sums: their sums of squares share the one exchange of the
 // token (one barrier a token). Results agree with conv + L2 + gdn_step_kernel to rounding.
-constexpr int FUSED_TMAX = 4;
-
-template <int K>
+// TM: tokens the kernel is built for (1, 2 or 4; nt <= TM): every token's inputs are loaded up
+// front, so a decode step built for one token issues no loads for tokens it does not have.
+template <int K, int TM>
 __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     const float* __restrict__ x, int xts, const float* __restrict__ cw, const float* __restrict__ cst_in,
     float* __restrict__ cst_out, const float* __restrict__ br, const float* __restrict__ ar, int bts,
@@ -388,10 +388,10 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     // every load up front: tokens, weights, the conv window, the gates, then the state. The
     // vector-memory counter retires in order, so the conv inputs issued first can be used (the
     // conv, SiLU and norm sums run) while the state slice is still landing.
-    f2 xq[FUSED_TMAX], xk[FUSED_TMAX];
-    f4 xv[FUSED_TMAX];
+    f2 xq[TM], xk[TM];
+    f4 xv[TM];
 #pragma unroll
-    for (int t = 0; t < FUSED_TMAX; ++t) {
+    for (int t = 0; t < TM; ++t) {
         const float* xr = x + (size_t)min(t, nt - 1) * xts;
         xq[t] = *(const f2*)(xr + cq);
         xk[t] = *(const f2*)(xr + ck);
@@ -432,9 +432,9 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
         wnv[i] = ld_f4(cst_in + (size_t)i * cd + cv);
     }
     // the gate inputs too: loaded inside the loop they would wait behind the norm barrier
-    float brt[FUSED_TMAX], art[FUSED_TMAX];
+    float brt[TM], art[TM];
 #pragma unroll
-    for (int t = 0; t < FUSED_TMAX; ++t) {
+    for (int t = 0; t < TM; ++t) {
         brt[t] = br[(size_t)min(t, nt - 1) * bts + h];
         art[t] = ar[(size_t)min(t, nt - 1) * bts + h];
     }
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     f4 s0 = ld_f4(sb + (size_t)i0 * S + j0), s1 = ld_f4(sb + (size_t)(i0 + 1) * S + j0);
     const float scale = 1.0f / sqrtf((float)S);
 #pragma unroll
-    for (int t = 0; t < FUSED_TMAX; ++t) {
+    for (int t = 0; t < TM; ++t) {
         if (t >= nt) break;   // uniform
         // ---- conv + SiLU of this thread's channels
         float q[2], k[2];
@@ -544,11 +544,20 @@ hipError_t launch_gdn_decode_fused(const float* x, int xts, const float* cw, int
                                    float* state, float* out, int ots, int nt, int nv, int nk, float eps,
                                    float* ck_state, float* ck_conv, int ck_after, hipStream_t st) {
     const dim3 grid(8 * nv);
+#define IT_FUSED(KK, TT)                                                                                     \
+    gdn_decode_fused_kernel<KK, TT><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, \
+                                                          out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after)
+#define IT_FUSED_T(KK)                    \
+    if (nt <= 1) IT_FUSED(KK, 1);         \
+    else if (nt <= 2) IT_FUSED(KK, 2);    \
+    else IT_FUSED(KK, 4);
     switch (K) {
-        case 2: gdn_decode_fused_kernel<2><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after); break;
-        case 3: gdn_decode_fused_kernel<3><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after); break;
-        default: gdn_decode_fused_kernel<4><<<grid, 256, 0, st>>>(x, xts, cw, cst_in, cst_out, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after); break;
+        case 2: IT_FUSED_T(2) break;
+        case 3: IT_FUSED_T(3) break;
+        default: IT_FUSED_T(4) break;
     }
+#undef IT_FUSED_T
+#undef IT_FUSED
     return hipGetLastError();
 }
 
