@@ -15,13 +15,14 @@ namespace it {
 // ck (optional): with one run, the state after token ck_after is written there from the window
 // (the MTP verify checkpoint); with several runs the host launches gdn_conv_state_kernel for it
 // before this kernel instead.
-template <int K>
+// TMAX: the longest run the kernel is built for (1, 2, 4 or 16; the host passes TT <= TMAX), so a
+// decode or verify launch loads no inputs for tokens it does not have.
+template <int K, int TMAX>
 __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__ x, int xts, const float* __restrict__ w,
                                                        float* __restrict__ state, float* __restrict__ out, int ots,
                                                        int cd, int nt, int TT, float* __restrict__ ck, int ck_after) {
     const int ch = blockIdx.x * 256 + threadIdx.x;
     if (ch >= cd) return;
-    constexpr int TMAX = 16;   // tokens per run (the host passes TT <= TMAX)
     const int t0 = blockIdx.y * TT, n = min(nt, t0 + TT) - t0;
     // the run's inputs are all loaded before any is used: one memory round trip per run
     float xs[TMAX], wt[K], win[K - 1];
@@ -81,12 +82,11 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __rest
 // 128hb + 64 + l, so a token's head vector is the whole wave and its sum of squares one DPP
 // reduction. Head blocks hb < nnorm (the q and k heads) are normalised, x / max(||x||, eps); the
 // rest (v) pass through. State and checkpoint handling as in gdn_conv_kernel.
-template <int K, typename OutT>
+template <int K, typename OutT, int TMAX>   // TMAX as in gdn_conv_kernel
 __global__ __launch_bounds__(256) void gdn_conv_l2_kernel(const float* __restrict__ x, int xts,
                                                           const float* __restrict__ w, float* __restrict__ state,
                                                           OutT* __restrict__ out, int ots, int cd, int nt, int TT,
                                                           int nnorm, float eps, float* __restrict__ ck, int ck_after) {
-    constexpr int TMAX = 16;   // tokens per run (the host passes TT <= TMAX)
     const int hb = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
     if (hb >= cd / 128) return;   // whole waves
     const bool norm = hb < nnorm;
@@ -690,10 +690,15 @@ hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state
                            int K, float* ck, int ck_after, hipStream_t st) {
     const int TT = nt <= 16 ? nt : 16;
     const dim3 grid((cd + 255) / 256, (nt + TT - 1) / TT);
+    // the kernel built for the shortest run length that holds TT tokens
+#define IT_CONV_RUN(KK, TM) gdn_conv_kernel<KK, TM><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, ck, ck_after)
 #define IT_CONV(KK)                                                                                           \
     if (ck && grid.y > 1)                                                                                     \
         gdn_conv_state_kernel<KK><<<grid.x, 256, 0, st>>>(x, xts, state, ck, cd, ck_after + 1);              \
-    gdn_conv_kernel<KK><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, ck, ck_after);          \
+    if (TT <= 1) IT_CONV_RUN(KK, 1);                                                                          \
+    else if (TT <= 2) IT_CONV_RUN(KK, 2);                                                                     \
+    else if (TT <= 4) IT_CONV_RUN(KK, 4);                                                                     \
+    else IT_CONV_RUN(KK, 16);                                                                                 \
     if (grid.y > 1) gdn_conv_state_kernel<KK><<<grid.x, 256, 0, st>>>(x, xts, state, state, cd, nt);
     switch (K) {
         case 2: IT_CONV(2) break;
@@ -701,6 +706,7 @@ hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state
         default: IT_CONV(4) break;
     }
 #undef IT_CONV
+#undef IT_CONV_RUN
     return hipGetLastError();
 }
 
@@ -714,15 +720,19 @@ hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* st
     const bool v4 = nt > 16 && cd % 256 == 0 && xts % 4 == 0 && ots % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
                     ((uintptr_t)out & 15) == 0 && ((uintptr_t)state & 15) == 0 && (!ck || ((uintptr_t)ck & 15) == 0);
     const dim3 grid4((cd / 256 + 3) / 4, (nt + TT - 1) / TT);
+#define IT_L2_RUN(KK, TM)                                                                                           \
+    gdn_conv_l2_kernel<KK, OutT, TM><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck,     \
+                                                           ck_after)
 #define IT_CONVL2(KK)                                                                                               \
     if (ck && grid.y > 1)                                                                                           \
         gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, ck, cd, ck_after + 1);          \
     if (v4)                                                                                                         \
         gdn_conv_l2_v4_kernel<KK, OutT><<<grid4, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps,  \
                                                                ck, ck_after);                                       \
-    else                                                                                                            \
-        gdn_conv_l2_kernel<KK, OutT><<<grid, 256, 0, st>>>(x, xts, w, state, out, ots, cd, nt, TT, nnorm, eps, ck,  \
-                                                           ck_after);                                               \
+    else if (TT <= 1) IT_L2_RUN(KK, 1);                                                                             \
+    else if (TT <= 2) IT_L2_RUN(KK, 2);                                                                             \
+    else if (TT <= 4) IT_L2_RUN(KK, 4);                                                                             \
+    else IT_L2_RUN(KK, 16);                                                                                         \
     if (grid.y > 1) gdn_conv_state_kernel<KK><<<(cd + 255) / 256, 256, 0, st>>>(x, xts, state, state, cd, nt);
     switch (K) {
         case 2: IT_CONVL2(2) break;
@@ -730,6 +740,7 @@ hipError_t launch_gdn_conv_l2(const float* x, int xts, const float* w, float* st
         default: IT_CONVL2(4) break;
     }
 #undef IT_CONVL2
+#undef IT_L2_RUN
     return hipGetLastError();
 }
 template hipError_t launch_gdn_conv_l2<float>(const float*, int, const float*, float*, float*, int, int, int, int,
