@@ -276,7 +276,7 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
                 ph[i] = c < 8 ? hi : (_Float16)(p[i] - (float)hi);
             }
             *(h4*)&Ps[b][c][16 * w + 4 * g] = ph;
-            if (w == 0 && g == 0 && c < 8) Al[row] = a;
+            if (MULTI && w == 0 && g == 0 && c < 8) Al[row] = a;   // (one tile: nothing to rescale)
         }
         IT_WAIT_VMCNT(0);   // this tile's V
         __syncthreads();    // B: P planes, alpha, V tile
@@ -290,12 +290,14 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             if (r0 + 8 * b >= R) continue;   // wave-uniform
+            if constexpr (MULTI) {   // with one tile per split O and l are still zero here
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float a = Al[8 * b + ((4 * g + i) & 7)];
+                for (int i = 0; i < 4; ++i) {
+                    const float a = Al[8 * b + ((4 * g + i) & 7)];
 #pragma unroll
-                for (int n = 0; n < 4; ++n) acc[b][n][i] *= a;
-                lacc[b][i] *= a;
+                    for (int n = 0; n < 4; ++n) acc[b][n][i] *= a;
+                    lacc[b][i] *= a;
+                }
             }
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
