@@ -174,7 +174,7 @@ def main():
     stream_of = lambda: torch.cuda.current_stream().cuda_stream
     res = {}
     us_layer = value_gbs = part_gbs = part_us = prefill_tflops = None
-    chunk, NSETS, cpu = 64, 40, None
+    chunk, NSETS, cpu, head_reps = 64, 40, None, 1
     dbytes = decode_bytes(8192)
     scale = 1.0 / 16
     rnd = lambda v, n: None if v is None else round(v, n)
@@ -228,16 +228,20 @@ def main():
                 decode_step(i)
         g.replay()   # untimed replay (graph upload)
         torch.cuda.synchronize()
+        # the K-step graph is replayed back to back until at least 100 launches sit between the
+        # events (one replay when K >= 100), so a short --steps still times >= 100 layers
+        head_reps = -(-100 // K)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         with torch.cuda.stream(s):
             e0.record(s)
-            g.replay()
+            for _ in range(head_reps):
+                g.replay()
             e1.record(s)
         torch.cuda.synchronize()
         total_ms = e0.elapsed_time(e1)
         assert torch.equal(out[:1], ref_out), "graph replay changed the decode result"
-        us_layer = total_ms * 1000.0 / K
+        us_layer = total_ms * 1000.0 / (K * head_reps)
         dbytes = decode_bytes(ctx)
         value_gbs = dbytes / (us_layer * 1e-6) / 1e9
         res["decode_ctx8192_us_per_layer"] = round(us_layer, 3)
@@ -400,9 +404,21 @@ def main():
         res["mtp_f32kv_nt2_8192_us"] = round(ms * 1000 / K, 3)
         ms = graph_time_ms(torch, lambda: [mtp_attn(i, 64, 4096) for i in range(20)], reps=3)
         res["mtp_f32kv_catchup64_at4096_us"] = round(ms * 1000 / 20, 2)
+        # the same catch-up given exactly the reference arena's room (src/vk/mod.rs:148, 730-733):
+        # the split doubles from 64 to 256 keys to fit it
+        room = _lm().it_attention_dispatch_room(S8, NH, 64) * 4
+        scr_room = torch.empty(room, dtype=torch.uint8, device=dev)
+
+        def mtp_room(i):
+            call("it_attn_f32kv", qm.data_ptr(), NH * 2 * HD, kf[i % NMT].data_ptr(), vf[i % NMT].data_ptr(), KVD,
+                 4096, HD, NH, NKV, 64, scale, om.data_ptr(), NH * HD, scr_room.data_ptr(), room, stream_of())
+        ms = graph_time_ms(torch, lambda: [mtp_room(i) for i in range(20)], reps=3)
+        res["mtp_f32kv_catchup64_at4096_room_us"] = round(ms * 1000 / 20, 2)
         log(f"mtp f32-KV attention: decode 8192 slots {res['mtp_f32kv_decode_8192_us']} us "
             f"({res['mtp_f32kv_decode_8192_GBs']} GB/s), nt=2 {res['mtp_f32kv_nt2_8192_us']} us, "
-            f"64-token catch-up at 4096 {res['mtp_f32kv_catchup64_at4096_us']} us")
+            f"64-token catch-up at 4096 {res['mtp_f32kv_catchup64_at4096_us']} us, "
+            f"{res['mtp_f32kv_catchup64_at4096_room_us']} us within the reference room")
+        del scr_room
         del kf, vf, scm
 
     # ------------------------------------------------------------------ GDN decode step (config 4)
@@ -667,7 +683,10 @@ def main():
         "data": "synthetic (seeded splitmix64 N(0,1), BASELINE configs 1-4)",
         "config": {"workload": "decode attention, 1 layer, batch 1, 16 q / 2 KV heads, head_dim 256, "
                                "f16 KV cache 8192 positions (config 2, seed 1)",
-                   "kv_rotation_sets": NSETS, "split_keys": chunk, "timing": "hip graph replay, hip events"},
+                   "kv_rotation_sets": NSETS, "split_keys": chunk,
+                   "timing": (f"hip events around {head_reps} back-to-back replay(s) of a graph of the {K} timed "
+                              f"layers ({K * head_reps} launches of it_attn_f16 timed; value per layer)"
+                              if us_layer is not None else "hip graph replay, hip events")},
         "decode_us_per_layer": rnd(us_layer, 3),
         "prefill_attn_TFLOPs": prefill_tflops,
         "results": res,

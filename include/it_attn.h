@@ -93,9 +93,12 @@ int it_attn_f16(const float* q, int q_tok_stride, const uint16_t* kc, const uint
  *          2 = flash prefill (needs nt >= 16): one pass with no scratch, or, when one pass would
  *          leave most of the GPU idle (a short chunk after a long context), key splits whose
  *          partial records (132 words: {m, l, k, 0} and O as int16 in units of k) are merged like
- *          kernel 1's.
- *   chunk  = keys per split (multiple of 64), 0 = automatic. For kernel 2 a chunk of at least
- *          pos0 + nt means one pass.
+ *          kernel 1's,
+ *          3 = kernel 2 with lossless key-split records: the split-K kernel's 260-word f32 form
+ *          {m, l, 0, 0, o[256]} instead of int16 O (twice the scratch; the same result as one
+ *          pass up to f32 reassociation of the merge).
+ *   chunk  = keys per split (multiple of 64), 0 = automatic. For kernels 2 and 3 a chunk of at
+ *          least pos0 + nt means one pass.
  * it_attn_scratch_bytes_ex gives the scratch for the same choice. With chunk = 0 the split is fitted
  * to scratch_bytes as in it_attn_f16; an explicit chunk needs its full record set. */
 size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int kernel, int chunk);
@@ -188,13 +191,24 @@ int it_attn_prep_f32kv(float* q, int q_tok_stride, const float* k, const float* 
                        int pos0, int row0, int hd, int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0,
                        int sec1, int sec2, int sec3, void* stream);
 
-/* Bytes of scratch it_attn_f32kv needs (split-K partial records, same 260-float layout). */
+/* Bytes of scratch it_attn_f32kv prefers (split-K partial records of 64-key splits, same 260-float
+ * layout); any smaller scratch also works (it_attn_f32kv_plan). */
 size_t it_attn_f32kv_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv);
+
+/* The split it_attn_f32kv uses for a scratch of scratch_bytes: *chunk keys per split and *bytes of
+ * records, or *chunk = 0 and *bytes = 0 for the one-pass form that needs no scratch. The preferred
+ * split is kept when it fits; otherwise the split doubles until the records fit, the reference's
+ * rule for the MTP head's attention (src/vk/mod.rs:730-733, C doubling from 64 while
+ * nt*nh*ceil((pos0+nt)/C)*260 words exceed the room); when even one record per (token, head) does
+ * not fit it takes the one-pass form, as the reference falls back to its whole-context `attn`
+ * kernel (src/vk/mod.rs:740, kernels/src/lib.rs:83-116). Returns 0, or -1 for a bad geometry. */
+int it_attn_f32kv_plan(int pos0, int nt, int hd, int nh, int nkv, size_t scratch_bytes, int* chunk, size_t* bytes);
 
 /* Causal GQA attention with sigmoid gate over an f32 KV cache: it_attn_f16's semantics and
  * buffers with kc, vc as f32 [row][kvd]. Query t sees cache rows 0..pos0+t (for the MTP head pass
- * pos0 is the first query's slot, position - 1). hd == 256, at most 16 q heads per KV head; the
- * scratch (it_attn_f32kv_scratch_bytes) is required.
+ * pos0 is the first query's slot, position - 1). hd == 256, at most 16 q heads per KV head. The
+ * split fits whatever scratch the caller passes (it_attn_f32kv_plan); a null scratch or one too
+ * small for a record per (token, head) runs the one-pass form.
  * Replaces VkEngine::attention(..., f16 = false) for the MTP head, src/vk/mod.rs:707-709 and 942
  * (attn_s + attn_comb, kernels/src/lib.rs:682-740; CPU src/mtp.rs:122-130). */
 int it_attn_f32kv(const float* q, int q_tok_stride, const float* kc, const float* vc, int kvd, int pos0, int hd,

@@ -31,7 +31,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 constexpr int HD = 256;
 constexpr size_t PART_WORDS = 260;
-constexpr int KERNEL_AUTO = 0, KERNEL_SPLITK = 1, KERNEL_FLASH = 2;
+constexpr int KERNEL_AUTO = 0, KERNEL_SPLITK = 1, KERNEL_FLASH = 2, KERNEL_FLASH_F32 = 3;
 constexpr size_t AUTO_SCRATCH_CAP = size_t(256) << 20;   // keep automatic split-K scratch under 256 MiB
 
 // Keys per split for the split-K kernel when the caller leaves it to us: one 64-key tile per
@@ -60,9 +60,10 @@ size_t splitk_scratch(int pos0, int nt, int nh, int chunk) {
 
 // Scratch of the flash kernel's key-split records: it::FLASH_REC words (16-byte header and O as
 // int16) per (token, head, split), half the split-K kernel's 260-word f32 records.
-size_t flash_scratch(int pos0, int nt, int nh, int chunk) {
+// With f32 records (kernel 3) the records are the split-K kernel's 260 words instead.
+size_t flash_scratch(int pos0, int nt, int nh, int chunk, bool f32rec = false) {
     const size_t smax = ((size_t)pos0 + nt + chunk - 1) / chunk;
-    return (size_t)nt * nh * smax * it::FLASH_REC * sizeof(float);
+    return (size_t)nt * nh * smax * (f32rec ? PART_WORDS : (size_t)it::FLASH_REC) * sizeof(float);
 }
 
 // Kernel and keys per split for an automatic call that must fit `budget` bytes of scratch. The
@@ -77,11 +78,12 @@ bool plan_attn(int pos0, int nt, int nh, int nkv, int kernel, size_t budget, Att
     const long total = (long)pos0 + nt;
     if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
     p.kernel = kernel;
-    if (kernel == KERNEL_FLASH) {
+    if (kernel == KERNEL_FLASH || kernel == KERNEL_FLASH_F32) {
+        const bool f32 = kernel == KERNEL_FLASH_F32;
         int c = flash_chunk(pos0, nt, nh, nkv, 0);
-        while (c && flash_scratch(pos0, nt, nh, c) > budget) c = (2L * c >= total) ? 0 : 2 * c;
+        while (c && flash_scratch(pos0, nt, nh, c, f32) > budget) c = (2L * c >= total) ? 0 : 2 * c;
         p.chunk = c;
-        p.bytes = c ? flash_scratch(pos0, nt, nh, c) : 0;
+        p.bytes = c ? flash_scratch(pos0, nt, nh, c, f32) : 0;
         return true;
     }
     int c = auto_chunk(pos0, nt, nh, nkv);
@@ -89,6 +91,22 @@ bool plan_attn(int pos0, int nt, int nh, int nkv, int kernel, size_t budget, Att
     p.chunk = c;
     p.bytes = splitk_scratch(pos0, nt, nh, c);
     return p.bytes <= budget;
+}
+
+// Keys per split for the f32-KV (MTP head) attention that must fit `budget` bytes of scratch: the
+// library's preferred split when it fits, else the split doubles until the 260-word records fit
+// (the reference's rule for this call, src/vk/mod.rs:730-733). The kernel walks any number of
+// 64-key tiles per split, so the doubling may go on past the reference's 1024 keys up to one split
+// over every key. If even one record per (token, head) does not fit, chunk 0: one pass that
+// writes the output directly and needs no scratch (the reference falls back to its whole-context
+// `attn` kernel there, src/vk/mod.rs:740). Always succeeds.
+struct F32kvPlan { int chunk; size_t bytes; };
+F32kvPlan plan_f32kv(int pos0, int nt, int nh, int nkv, size_t budget) {
+    const long total = (long)pos0 + nt;
+    int c = auto_chunk(pos0, nt, nh, nkv);
+    while (splitk_scratch(pos0, nt, nh, c) > budget && c < total) c *= 2;
+    if (splitk_scratch(pos0, nt, nh, c) > budget) return {0, 0};
+    return {c, splitk_scratch(pos0, nt, nh, c)};
 }
 
 int validate_attn(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
@@ -216,6 +234,17 @@ size_t it_attn_f32kv_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv) {
     return splitk_scratch(pos0, nt, nh, auto_chunk(pos0, nt, nh, nkv));
 }
 
+int it_attn_f32kv_plan(int pos0, int nt, int hd, int nh, int nkv, size_t scratch_bytes, int* chunk, size_t* bytes) {
+    if (hd != HD || nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv || nh / nkv > 16 ||
+        (long)pos0 + nt > (1L << 22))
+        return fail("it_attn_f32kv_plan: bad geometry");
+    const F32kvPlan p = plan_f32kv(pos0, nt, nh, nkv, scratch_bytes);
+    if (chunk) *chunk = p.chunk;
+    if (bytes) *bytes = p.bytes;
+    g_err.clear();
+    return 0;
+}
+
 int it_attn_f32kv(const float* q, int qts, const float* kc, const float* vc, int kvd, int pos0, int hd, int nh,
                   int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes,
                   void* stream) {
@@ -230,12 +259,11 @@ int it_attn_f32kv(const float* q, int qts, const float* kc, const float* vc, int
         return fail("%s: q/kc/vc/out must be 16-byte aligned", who);
     if (qts % 4 != 0 || ots % 4 != 0) return fail("%s: token strides must be multiples of 4", who);
     if (nt > 1 && (qts < 2 * nh * hd || ots < nh * hd)) return fail("%s: token strides overlap rows", who);
-    const int chunk = auto_chunk(pos0, nt, nh, nkv);
-    const size_t need = splitk_scratch(pos0, nt, nh, chunk);
-    if (!scratch || scratch_bytes < need || !aligned16(scratch))
-        return fail("%s: scratch of %zu bytes needed (got %zu, 16-byte aligned)", who, need, scratch_bytes);
-    return check(it::launch_attn_f32kv(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, (float*)scratch, chunk,
-                                       (hipStream_t)stream),
+    if (scratch && !aligned16(scratch)) return fail("%s: scratch must be 16-byte aligned", who);
+    // fit the caller's scratch; no scratch (or too little for one record per row) = one pass
+    const F32kvPlan p = plan_f32kv(pos0, nt, nh, nkv, scratch ? scratch_bytes : 0);
+    return check(it::launch_attn_f32kv(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, (float*)scratch,
+                                       p.chunk, (hipStream_t)stream),
                  who);
 }
 
@@ -243,9 +271,9 @@ size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int k
     (void)hd;
     if (nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv) return 0;
     if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
-    if (kernel == KERNEL_FLASH) {
+    if (kernel == KERNEL_FLASH || kernel == KERNEL_FLASH_F32) {
         const int c = flash_chunk(pos0, nt, nh, nkv, chunk);
-        return c ? flash_scratch(pos0, nt, nh, c) : 0;
+        return c ? flash_scratch(pos0, nt, nh, c, kernel == KERNEL_FLASH_F32) : 0;
     }
     if (kernel != KERNEL_SPLITK) return 0;
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
@@ -273,9 +301,10 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
                    int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes, int kernel,
                    int chunk, void* stream) {
     if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, out, ots)) return -1;
-    if (kernel != KERNEL_AUTO && kernel != KERNEL_SPLITK && kernel != KERNEL_FLASH)
+    if (kernel != KERNEL_AUTO && kernel != KERNEL_SPLITK && kernel != KERNEL_FLASH && kernel != KERNEL_FLASH_F32)
         return fail("it_attn_f16: unknown kernel %d", kernel);
-    if (kernel == KERNEL_FLASH && nt < 16) return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
+    if ((kernel == KERNEL_FLASH || kernel == KERNEL_FLASH_F32) && nt < 16)
+        return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
     if (chunk == 0) {
         // automatic split: fit the caller's scratch (the reference's arena rule), never refuse a
         // geometry for which a smaller record set exists
@@ -284,12 +313,13 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
             return fail("it_attn_f16: scratch of %zu bytes cannot hold even one partial record per (token, head) "
                         "(%zu bytes)", scratch_bytes, p.bytes);
         kernel = p.kernel;
-        if (kernel == KERNEL_FLASH && p.chunk == 0) chunk = 1 << 30;   // one pass
+        if ((kernel == KERNEL_FLASH || kernel == KERNEL_FLASH_F32) && p.chunk == 0) chunk = 1 << 30;   // one pass
         else chunk = p.chunk;
     }
     if (kernel == KERNEL_AUTO) kernel = auto_kernel(nt);
     hipStream_t st = (hipStream_t)stream;
-    if (kernel == KERNEL_FLASH) {
+    if (kernel == KERNEL_FLASH || kernel == KERNEL_FLASH_F32) {
+        const bool f32 = kernel == KERNEL_FLASH_F32;
         if (nt < 16) return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
         if (chunk < 0 || chunk % 64 != 0) return fail("it_attn_f16: flash chunk %d must be a multiple of 64", chunk);
         // (chunk is never 0 here: the automatic plan above has replaced it)
@@ -297,12 +327,12 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
         if (!c)
             return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st),
                          "it_attn_f16 (flash)");
-        const size_t need = flash_scratch(pos0, nt, nh, c);
+        const size_t need = flash_scratch(pos0, nt, nh, c, f32);
         if (scratch_bytes < need || !scratch)
             return fail("it_attn_f16: scratch of %zu bytes < %zu required (it_attn_scratch_bytes)", scratch_bytes, need);
         if (!aligned16(scratch)) return fail("it_attn_f16: scratch must be 16-byte aligned");
         return check(it::launch_attn_flash_split(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots,
-                                                 (float*)scratch, c, st),
+                                                 (float*)scratch, c, st, f32),
                      "it_attn_f16 (flash, key splits)");
     }
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);

@@ -51,11 +51,18 @@ constexpr int F32KV_ROW = F32KV_HD + 4;                 // padded LDS row (float
 #define IT_F32KV_WAIT_VMCNT0() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
 #define IT_F32KV_WAIT_VMCNT16() asm volatile("s_waitcnt vmcnt(16)" ::: "memory")
 
-template <int RB>
+//
+// DIRECT (one pass, no scratch): the grid has one split covering every key, so instead of a record
+// each row's final output o / l * sigmoid(gate) is written straight to out[t*ots + h*256 + d]. This
+// is the fallback for a caller whose scratch cannot hold even one record per (token, head), the
+// role of the reference's whole-context `attn` kernel (kernels/src/lib.rs:83-116, chosen at
+// src/vk/mod.rs:740).
+template <int RB, bool DIRECT>
 __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict__ q, int qts,
                                                          const float* __restrict__ kc, const float* __restrict__ vc,
                                                          int kvd, int pos0, int nh, int nkv, int nt, int tpw,
-                                                         float qscale, float* __restrict__ part, int chunk, int smax) {
+                                                         float qscale, float* __restrict__ part, int chunk, int smax,
+                                                         float* __restrict__ out, int ots) {
     typedef __attribute__((address_space(3))) void lds_void;
     constexpr int NR = 16 * RB;                                   // query rows per workgroup
     __shared__ __attribute__((aligned(16))) float Ks[F32KV_KEYS * F32KV_ROW];
@@ -198,6 +205,22 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
         const int r = 16 * rb + lr;
         if (r >= rows) continue;
         const int tr = t0 + r / G, hr = kh * G + r % G;
+        if constexpr (DIRECT) {
+            // every visible row has seen at least key 0, so l_run > 0
+            const float inv = 1.0f / l_run[rb];
+            const float* gate = q + (size_t)tr * qts + (size_t)hr * 2 * F32KV_HD + F32KV_HD;
+            float* orow = out + (size_t)tr * ots + (size_t)hr * F32KV_HD;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 64 * w + 16 * lg + 4 * i;
+                const f4 g = ld_f4(gate + d);
+                f4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = acc[rb][e][i] * inv * sigmoidf_(g[e]);
+                *(f4*)(orow + d) = o;
+            }
+            continue;
+        }
         float* rec = part + ((size_t)(tr * nh + hr) * smax + s) * 260;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -209,20 +232,28 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
 hipError_t launch_attn_f32kv(const float* q, int qts, const float* kc, const float* vc, int kvd, int pos0, int nh,
                              int nkv, int nt, float scale, float* out, int ots, float* part, int chunk, hipStream_t st) {
     const int G = nh / nkv;
+    const bool direct = chunk == 0;   // one pass over every key, output written directly, no records
+    if (direct) chunk = pos0 + nt;
     const int smax = (pos0 + nt + chunk - 1) / chunk;
     const float qs = scale * 1.44269504088896340736f;
     // two 16-row blocks per workgroup once a call has more rows than one block holds
-    if (nt * G > 16) {
-        const int tpw = 32 / G;
-        const dim3 grid((unsigned)smax, (unsigned)nkv, (unsigned)((nt + tpw - 1) / tpw));
-        attn_f32kv_kernel<2><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk, smax);
-    } else {
-        const int tpw = 16 / G;
-        const dim3 grid((unsigned)smax, (unsigned)nkv, (unsigned)((nt + tpw - 1) / tpw));
-        attn_f32kv_kernel<1><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk, smax);
-    }
+    const int rb = nt * G > 16 ? 2 : 1;
+    const int tpw = 16 * rb / G;
+    const dim3 grid((unsigned)smax, (unsigned)nkv, (unsigned)((nt + tpw - 1) / tpw));
+    if (rb == 2 && direct)
+        attn_f32kv_kernel<2, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk,
+                                                        smax, out, ots);
+    else if (rb == 2)
+        attn_f32kv_kernel<2, false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk,
+                                                         smax, out, ots);
+    else if (direct)
+        attn_f32kv_kernel<1, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk,
+                                                        smax, out, ots);
+    else
+        attn_f32kv_kernel<1, false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk,
+                                                         smax, out, ots);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || direct) return e;
     return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
 }
 

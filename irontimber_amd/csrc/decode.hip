@@ -105,11 +105,20 @@ __device__ __forceinline__ MbRsrc mb_rsrc(float* p, uint32_t bytes) {
 __device__ __forceinline__ int mb_piece(int th, int db, int s, int smax) {
     return MB_HEAD + ((th * 16 + db) * smax + s) * MB_PIECE;
 }
+// A record value is stored as a word that can never equal MB_EMPTY: any NaN (which could carry a
+// payload from a NaN in q, K or V, such as 0xFFFFFFFF) is written as the canonical quiet NaN, so a
+// non-finite input gives NaN outputs for that call instead of a piece that never looks complete.
+__device__ __forceinline__ uint32_t mb_word(float v) {
+    return v != v ? 0x7FC00000u : __builtin_bit_cast(uint32_t, v);
+}
 __device__ __forceinline__ void mb_store1(MbRsrc r, int idx, float v) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, 4 * idx, 0, MB_COHERENT);
+    __builtin_amdgcn_raw_buffer_store_b32(mb_word(v), r, 4 * idx, 0, MB_COHERENT);
 }
 __device__ __forceinline__ void mb_store2(MbRsrc r, int idx, f2 v) {
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), r, 4 * idx, 0, MB_COHERENT);
+    __builtin_amdgcn_raw_buffer_store_b64(u2{mb_word(v[0]), mb_word(v[1])}, r, 4 * idx, 0, MB_COHERENT);
+}
+__device__ __forceinline__ void mb_clear2(MbRsrc r, int idx) {
+    __builtin_amdgcn_raw_buffer_store_b64(u2{MB_EMPTY, MB_EMPTY}, r, 4 * idx, 0, MB_COHERENT);
 }
 __device__ __forceinline__ void mb_store4(MbRsrc r, int idx, u4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, 4 * idx, 0, MB_COHERENT);
@@ -661,7 +670,7 @@ __device__ __forceinline__ void mailbox_merge(const float* __restrict__ q, int q
         const int base = mb_piece(th, db, l + 64 * j, smax);
 #pragma unroll
         for (int k = 0; k < 4; ++k) mb_store4(r, base + 4 * k, empty);
-        mb_store2(r, base + 16, __builtin_bit_cast(f2, u2{MB_EMPTY, MB_EMPTY}));
+        mb_clear2(r, base + 16);
     }
     merge_wave_store<SPL>(gv, nh, t, h, ns, hv, ov, out, ots, d0, l);
 }

@@ -75,8 +75,9 @@ __device__ __forceinline__ void scale_acc(f16v& acc, float a) {
     }
 }
 
-// s_waitcnt immediates (gfx9 encoding): wait until at most N vector-memory ops are outstanding
-// (expcnt/lgkmcnt left unconstrained).
+// F32REC: the key-split records in the split-K kernels' lossless f32 form instead ({m, l, 0, 0} +
+// O as 256 floats, 260 words, merged by the f32 combine), selectable through it_attn_f16_ex.
+template <bool F32REC>
 __global__ __launch_bounds__(256) void attn_flash_kernel(
     const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int kvd,
     int pos0, int nh, int nkv, int nt, float scale, float* __restrict__ out, int ots, float* __restrict__ part,
@@ -320,6 +321,22 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     const int rw = __builtin_amdgcn_readfirstlane(rt * BM + 32 * w);
     const int nrow = min(32, R - rw);
     int tq = __builtin_amdgcn_readfirstlane(rw / G), gq = rw - tq * G;   // (token, q-head) of row rw + i
+    if (F32REC && part) {
+        // f32 records of (token, head, split), 260 words each: {m, l, 0, 0}, then O
+        if (l < nrow) {
+            const int tl = (rw + l) / G, gl = rw + l - tl * G;
+            float* rec = part + ((size_t)(tl * nh + kh * G + gl) * smax + split) * 260;
+            __builtin_nontemporal_store(f4{ml[w][0][l] * 0.6931471805599453f, ml[w][1][l], 0.f, 0.f}, (f4*)rec);
+        }
+        size_t ridx = (size_t)(tq * nh + kh * G + gq) * smax + split;
+        const size_t rnext = (size_t)(nh - G + 1) * smax;
+        for (int i = 0; i < nrow; ++i) {
+            const f4 ov = *(const f4*)(os + i * HD + 4 * (l ^ i));
+            __builtin_nontemporal_store(ov, (f4*)(part + uniform_off(ridx * 260 + 4)) + l);
+            if (++gq == G) { gq = 0; ridx += rnext; } else { ridx += smax; }
+        }
+        return;
+    }
     if (part) {
         // partial records of (token, head, split), FLASH_REC words each: {m, l, k, 0} with m in
         // natural-log units of the scaled score and k = max|O| / 32767, then O as int16 in units of
@@ -394,7 +411,8 @@ hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const 
                              int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st) {
     const int R = nt * (nh / nkv);
     const dim3 grid((R + BM - 1) / BM, nkv);
-    attn_flash_kernel<<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, nullptr, 0, 1);
+    attn_flash_kernel<false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, nullptr, 0,
+                                                    1);
     return hipGetLastError();
 }
 
@@ -411,14 +429,20 @@ int flash_split_chunk(int pos0, int nt, int nh, int nkv) {
 
 hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                                    int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
-                                   hipStream_t st) {
+                                   hipStream_t st, bool f32rec) {
     const int R = nt * (nh / nkv);
     const int smax = (pos0 + nt + chunk - 1) / chunk;
     const dim3 grid((R + BM - 1) / BM, nkv, smax);
-    attn_flash_kernel<<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, part, chunk, smax);
+    if (f32rec)
+        attn_flash_kernel<true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, part,
+                                                      chunk, smax);
+    else
+        attn_flash_kernel<false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, part,
+                                                       chunk, smax);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_attn_combine_q16(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
+    return f32rec ? launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st)
+                  : launch_attn_combine_q16(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
 }
 
 }  // namespace it

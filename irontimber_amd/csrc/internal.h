@@ -45,7 +45,7 @@ hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const 
 int flash_split_chunk(int pos0, int nt, int nh, int nkv);
 hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                                    int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
-                                   hipStream_t st);
+                                   hipStream_t st, bool f32rec = false);
 
 // ck / ck_after: optional checkpoint of the state after token ck_after (null = none).
 hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,

@@ -11,7 +11,7 @@ import torch
 
 from ._lib import call, lib
 
-KERNEL_AUTO, KERNEL_SPLITK, KERNEL_FLASH = 0, 1, 2
+KERNEL_AUTO, KERNEL_SPLITK, KERNEL_FLASH, KERNEL_FLASH_F32 = 0, 1, 2, 3
 
 
 def _stream() -> int:
@@ -115,11 +115,12 @@ def attn_f32kv(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int, n
         scale = 1.0 / hd ** 0.5
     if out is None:
         out = torch.empty(nt, nh * hd, device=q.device, dtype=torch.float32)
-    need = lib().it_attn_f32kv_scratch_bytes(pos0, nt, hd, nh, nkv)
     if scratch is None:
+        need = lib().it_attn_f32kv_scratch_bytes(pos0, nt, hd, nh, nkv)
         scratch = torch.empty(max(need, 16), device=q.device, dtype=torch.uint8)
+    sp, sb = (scratch.data_ptr(), scratch.numel() * scratch.element_size()) if scratch.numel() else (None, 0)
     call("it_attn_f32kv", q.data_ptr(), nh * 2 * hd, kc.data_ptr(), vc.data_ptr(), kvd, pos0, hd, nh, nkv, nt,
-         float(scale), out.data_ptr(), nh * hd, scratch.data_ptr(), scratch.numel(), _stream())
+         float(scale), out.data_ptr(), nh * hd, sp, sb, _stream())
     return out
 
 

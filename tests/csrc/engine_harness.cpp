@@ -3,14 +3,16 @@
 // one caller-owned device arena addressed by word offsets, a prompt split by prefill_chunks
 // (it_prefill_chunks, vk/mod.rs:130-134), each attention call given exactly the arena room the
 // reference reserves for its dispatch (attention_dispatch_room, vk/mod.rs:148) as scratch, then
-// decode tokens one at a time: attention in one launch through a mailbox slot of the arena, the
-// one-launch GDN layer with its ping-pong conv state.
+// decode tokens one at a time: attention through it_attn_f16 with the same room, the one-launch
+// GDN layer with its ping-pong conv state. The MTP head's attention over an f32 cache (vk/mod.rs:942)
+// runs over the same tokens in 64-token catch-up calls (effective_prefill_batch, vk/mod.rs:143-146),
+// each given the dispatch room as scratch too.
 //
 // Test driver only (tests/test_gpu_engine_harness.py builds the inputs and checks the outputs
 // against the oracle). Usage: engine_harness DIR T_PROMPT T_DECODE UBATCH
 //   DIR holds q.bin k.bin v.bin (attention inputs, f32 [T][...]) and x.bin w.bin cst.bin st.bin
-//   br.bin ar.bin dt.bin a.bin (GDN inputs); attn_out.bin gdn_out.bin state_out.bin cst_out.bin are
-//   written back. Geometry: 16 q / 2 KV heads, head_dim 256; 32 V / 16 QK heads, state 128, conv 4.
+//   br.bin ar.bin dt.bin a.bin (GDN inputs); attn_out.bin gdn_out.bin state_out.bin cst_out.bin
+//   mtp_out.bin are written back. Geometry: 16 q / 2 KV heads, head_dim 256; 32 V / 16 QK heads, state 128, conv 4.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -63,7 +65,7 @@ void write_file(const std::string& path, const float* d, size_t n) {
 
 // Word offsets into the arena (f32 words; the f16 KV caches take kvd/2 words a position).
 struct Layout {
-    size_t q, k, v, kc, vc, aout, scr, mbox, x, w, cst0, cst1, st, br, ar, dt, a, gout, gscr, words;
+    size_t q, k, v, kc, vc, aout, scr, mout, x, w, cst0, cst1, st, br, ar, dt, a, gout, gscr, words;
 };
 
 }  // namespace
@@ -89,8 +91,7 @@ int main(int argc, char** argv) {
     // the arena's attention scratch: ubatch x heads x max(ctx, 260) words (vk/mod.rs:546), which is
     // the dispatch room of the largest chunk; it_attention_scratch_words is only the 64-token case
     L.scr = take(it_attention_dispatch_room(ctx, NH, ub));
-    const size_t mbox_bytes = it_attn_mailbox_bytes(ctx, 1, NH);   // decode attention in one launch
-    L.mbox = take(mbox_bytes / 4);
+    L.mout = take((size_t)T * OTS);   // the MTP head's attention output
     L.x = take((size_t)T * CD);
     L.w = take((size_t)CD * KC);
     L.cst0 = take((size_t)(KC - 1) * CD);
@@ -125,21 +126,16 @@ int main(int argc, char** argv) {
     up(L.a, "a.bin", NV);
 
     auto a = [&](size_t off) { return arena + off; };
-    ITCHECK(it_attn_mailbox_init(a(L.mbox), mbox_bytes, s));
     uint16_t* kc = (uint16_t*)(arena + L.kc);
     uint16_t* vc = (uint16_t*)(arena + L.vc);
     const size_t gscr_bytes = it_gdn_prefill_scratch_bytes(ub, NV, NK, S);
 
-    // one attention layer call for tokens [t0, t0 + nt): every call goes through the mailbox entry
-    // point, which runs a decode step in one launch and anything else as it_attn_f16 with the
-    // dispatch room as scratch
-    int one_launch = 0;
+    // one attention layer call for tokens [t0, t0 + nt) with the dispatch room as scratch
     auto attention = [&](int t0, int nt) {
         const size_t room = it_attention_dispatch_room(ctx, NH, nt) * sizeof(float);
         ITCHECK(it_kv_append_f16(a(L.k + (size_t)t0 * KVD), a(L.v + (size_t)t0 * KVD), KVD, kc, vc, t0, nt, KVD, 0, s));
-        one_launch += it_attn_mailbox_would_launch(t0, nt, HD, NH, NKV, mbox_bytes);
-        ITCHECK(it_attn_f16_mailbox(a(L.q + (size_t)t0 * QTS), QTS, kc, vc, KVD, t0, HD, NH, NKV, nt, 0.0625f,
-                                    a(L.aout + (size_t)t0 * OTS), OTS, a(L.mbox), mbox_bytes, a(L.scr), room, s));
+        ITCHECK(it_attn_f16(a(L.q + (size_t)t0 * QTS), QTS, kc, vc, KVD, t0, HD, NH, NKV, nt, 0.0625f,
+                            a(L.aout + (size_t)t0 * OTS), OTS, a(L.scr), room, s));
     };
 
     // ---- prefill: the reference's chunk loop (vk/mod.rs:896)
@@ -166,6 +162,14 @@ int main(int argc, char** argv) {
                                     a(L.gout + (size_t)t * NV * S), NV * S, 1, NV, NK, S, EPS, s));
         p ^= 1;
     }
+    // ---- MTP head catch-up: its attention over an f32 cache (here the f32 k/v rows themselves) in
+    // calls of at most 64 tokens, each with the dispatch room of the arena as scratch
+    for (int t0 = 0; t0 < T; t0 += 64) {
+        const int nt = T - t0 < 64 ? T - t0 : 64;
+        const size_t room = it_attention_dispatch_room(ctx, NH, nt) * sizeof(float);
+        ITCHECK(it_attn_f32kv(a(L.q + (size_t)t0 * QTS), QTS, a(L.k), a(L.v), KVD, t0, HD, NH, NKV, nt, 0.0625f,
+                              a(L.mout + (size_t)t0 * OTS), OTS, a(L.scr), room, s));
+    }
     HIPCHECK(hipStreamSynchronize(s));
 
     auto down = [&](size_t off, const char* name, size_t n) {
@@ -177,11 +181,8 @@ int main(int argc, char** argv) {
     down(L.gout, "gdn_out.bin", (size_t)T * NV * S);
     down(L.st, "state_out.bin", (size_t)NV * S * S);
     down(p ? L.cst1 : L.cst0, "cst_out.bin", (size_t)(KC - 1) * CD);
-    int poisoned = 1;
-    ITCHECK(it_attn_mailbox_poisoned(a(L.mbox), &poisoned, s));
-    std::printf("ok %ld prefill calls, %d decode steps (%d attention calls in one launch), mailbox %s, arena %zu MiB\n",
-                nr, td, one_launch, poisoned ? "POISONED" : "clean", L.words * 4 >> 20);
-    if (poisoned) return 5;
+    down(L.mout, "mtp_out.bin", (size_t)T * OTS);
+    std::printf("ok %ld prefill calls, %d decode steps, arena %zu MiB\n", nr, td, L.words * 4 >> 20);
     HIPCHECK(hipFree(arena));
     return 0;
 }

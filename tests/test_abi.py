@@ -269,3 +269,51 @@ def test_gdn_prefill_host_side():
     assert call(nbytes=need - 16) != 0 and b"scratch" in lib.it_last_error()
     assert call(scratch=ctypes.c_void_p((1 << 20) + 8)) != 0 and b"16-byte" in lib.it_last_error()
     assert call(nt=0) == 0                        # nothing to do, no device work
+
+
+@pytest.mark.parametrize("nh,nkv,ctx", [(16, 2, 8192), (24, 4, 8192), (16, 2, 300)])
+def test_f32kv_plan_fits_reference_room_sweep(nh, nkv, ctx):
+    """The MTP head's f32-KV attention: for every nt 1..64 and pos0 <= ctx - nt, the split that
+    it_attn_f32kv picks for the reference room at capacity ctx (attention_dispatch_room,
+    src/vk/mod.rs:148-150) fits it, keeps the preferred split when that fits, follows the record
+    formula, and never takes the one-pass form while a record per (token, head) fits."""
+    import subprocess
+    exe = os.path.join(ROOT, "tests", "csrc", "plan_sweep")
+    r = subprocess.run([exe, _lib.LIB_PATH, str(nh), str(nkv), str(ctx), "64", "f32kv"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout + r.stderr
+    plans, grown, one_pass = map(int, r.stdout.split()[1:])
+    assert plans == sum(ctx - nt + 1 for nt in range(1, 65)) and one_pass == 0
+    assert grown > 0 if ctx == 8192 else True
+
+
+def f32kv_plan(pos0, nt, nh, nkv, budget):
+    c, b = ctypes.c_int(), ctypes.c_size_t()
+    rc = _lib.lib().it_attn_f32kv_plan(pos0, nt, 256, nh, nkv, budget, ctypes.byref(c), ctypes.byref(b))
+    return rc, c.value, b.value
+
+
+def test_f32kv_plan_cases():
+    lib = _lib.lib()
+    # decode at 8192 slots keeps 64-key splits within the room
+    room1 = lib.it_attention_dispatch_room(8192, 16, 1) * 4
+    assert f32kv_plan(8191, 1, 16, 2, room1) == (0, 64, 16 * 128 * 1040)
+    # the MTP catch-up of 64 tokens at slot 4096: the preferred 64-key split needs 69,222,400 B,
+    # the room is 33,554,432 B; the split doubles to 128 keys (34,611,200 B) -> 256 (17,305,600 B)
+    room64 = lib.it_attention_dispatch_room(8192, 16, 64) * 4
+    assert room64 == 33554432
+    assert lib.it_attn_f32kv_scratch_bytes(4096, 64, 256, 16, 2) == 69222400
+    assert f32kv_plan(4096, 64, 16, 2, room64) == (0, 256, 64 * 16 * 17 * 1040)
+    # the reference's own doubling (src/vk/mod.rs:731-733) ends at the same C here
+    total, c = 4096 + 64, 64
+    while c < 1024 and 64 * 16 * -(-total // c) * 260 * 4 > room64:
+        c *= 2
+    assert c == 256
+    # past the reference's 1024 keys: one split over every key still needs only a record per row
+    assert f32kv_plan(8000, 64, 16, 2, 64 * 16 * 1040) == (0, 8192, 64 * 16 * 1040)
+    # below one record per (token, head): the one-pass form, no scratch
+    assert f32kv_plan(8000, 64, 16, 2, 64 * 16 * 1040 - 1) == (0, 0, 0)
+    assert f32kv_plan(10, 1, 16, 2, 0) == (0, 0, 0)
+    # bad geometry
+    assert f32kv_plan(10, 1, 16, 3, 0)[0] != 0 and "bad geometry" in _lib.last_error()
+    assert f32kv_plan(10, 1, 34, 2, 0)[0] != 0

@@ -132,6 +132,65 @@ def test_flash_whole_prompt_8192(dev):
         assert np.abs(whole - chunked).max() <= TOL
 
 
+@pytest.mark.parametrize("chunk", [0, 64, 192, 640])
+def test_flash_f32_records(dev, chunk):
+    """The key-split flash path with lossless f32 records (kernel 3: the split-K kernels' 260-word
+    {m, l, 0, 0, o[256]} form, merged by the f32 combine) at BASELINE config 3's first case: the
+    oracle's result within 2e-3 with no argmax flip, the int16-record form with the same splits
+    within its quantisation bound, and the same bits on a second call."""
+    got, want = run_case(dev, 2, 4096 + 64, 64, kernel=ops.KERNEL_FLASH_F32, chunk=chunk)
+    err = np.abs(got - want).max()
+    print(f"flash f32 records chunk={chunk} max_abs={err:.3g}")
+    assert np.isfinite(got).all() and err <= TOL
+    assert assert_argmax_agrees(got, want) == 0
+    q16, _ = run_case(dev, 2, 4096 + 64, 64, kernel=ops.KERNEL_FLASH, chunk=chunk)
+    d = np.abs(q16 - got).max()
+    print(f"int16 records vs f32 records: {d:.3g}")
+    assert d <= 2e-4
+    again, _ = run_case(dev, 2, 4096 + 64, 64, kernel=ops.KERNEL_FLASH_F32, chunk=chunk)
+    np.testing.assert_array_equal(again, got)
+
+
+def test_flash_int16_record_error_config3(dev):
+    """BASELINE config 3 as configured (the 8192-token prompt as 128 chunks of 64 tokens, each given
+    the reference arena's room): at every chunk position, the int16-record result against the same
+    splits with f32 records (the quantisation error alone) and against the whole prompt in one pass.
+    Prints the table per position; the int16 form stays within 2e-4 of the f32 records."""
+    import ctypes
+    from irontimber_amd._lib import call, lib
+    T = 8192
+    q, kb, vb = attn_inputs(2, ctx=T, nt=T)
+    announce("flash int16 record error, 128 chunks of config 3")
+    qd = dev_f32(q.reshape(T, -1), dev)
+    kc, vc = dev_f16bits(kb, dev), dev_f16bits(vb, dev)
+    whole = host(ops.attn_f16(qd, kc, vc, 0, 16, 2, kernel=ops.KERNEL_FLASH))
+    room = lib().it_attention_dispatch_room(T, 16, 64) * 4
+    scr = torch.empty(room, dtype=torch.uint8, device=dev)
+    rows, worst = [], 0.0
+    for c in range(0, T, 64):
+        k_, ch, nb = ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+        assert lib().it_attn_plan(c, 64, 256, 16, 2, room, ctypes.byref(k_), ctypes.byref(ch), ctypes.byref(nb)) == 0
+        qc = qd[c:c + 64].contiguous()
+        out = torch.empty(64, 16 * 256, device=dev)
+        call("it_attn_f16", qc.data_ptr(), 16 * 512, kc.data_ptr(), vc.data_ptr(), 512, c, 256, 16, 2, 64, 1.0 / 16,
+             out.data_ptr(), 16 * 256, scr.data_ptr(), room, None)
+        got = host(out)
+        if ch.value:   # key splits: the same splits with f32 records
+            ref = host(ops.attn_f16(qc, kc, vc, c, 16, 2, kernel=ops.KERNEL_FLASH_F32, chunk=ch.value))
+            dq = float(np.abs(got - ref).max())
+        else:
+            dq = 0.0   # one pass: no records
+        dw = float(np.abs(got - whole[c:c + 64]).max())
+        rows.append((c, ch.value, dq, dw))
+        worst = max(worst, dq)
+        assert dw <= TOL
+    print("pos0 chunk int16_vs_f32rec vs_one_pass")
+    for r_ in rows:
+        print(f"{r_[0]} {r_[1]} {r_[2]:.3g} {r_[3]:.3g}")
+    print(f"max int16 quantisation error over the 128 chunks: {worst:.3g}")
+    assert worst <= 2e-4
+
+
 def test_decode_tokens_equal_single_pass(dev):
     """Token-by-token decode (nt = 1 at every position, split-K with the library's splits) equals
     one causal prefill pass over the same prompt (decode == single-pass causal)."""
