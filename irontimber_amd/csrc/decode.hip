@@ -480,6 +480,57 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     }
 }
 
+// Merge of the rows of a prefill chunk (at most NS <= 64 splits a row): one wave per query row,
+// lane l owning dims 4l .. 4l+3. Lane j also loads the header of split j, so the row maximum and
+// the denominator are one wave reduction each and split j's weight is read from lane j; every
+// header and O load is issued before any is used (one memory round trip; O slots past the row's
+// ns reload its last split and are skipped). No LDS, no barrier. Same formula as
+// attn_combine_kernel, the splits' O summed in order.
+template <int NS, bool Q16>
+__global__ __launch_bounds__(256) void attn_combine_row_kernel(const float* __restrict__ q, int qts, int pos0, int nh,
+                                                               int nt, const float* __restrict__ part, int chunk,
+                                                               int smax, float* __restrict__ out, int ots) {
+    constexpr int RW = Q16 ? FLASH_REC : PART;   // record words
+    const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+    if (row >= nt * nh) return;
+    const int l = threadIdx.x & 63;
+    const int t = row / nh, h = row - t * nh;
+    const int ns = (pos0 + t + chunk) / chunk;   // splits holding keys <= pos0 + t (1 .. smax)
+    const float* base = part + (size_t)row * smax * RW;
+    const f4 hl = *(const f4*)(base + (size_t)min(l, ns - 1) * RW);   // lane l: header of split l
+    f4 ov[NS];
+    u2 qv[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const float* rec = base + (size_t)min(j, ns - 1) * RW;
+        if constexpr (Q16) qv[j] = *((const u2*)(rec + 4) + l);
+        else ov[j] = ld_f4(rec + 4 + 4 * l);
+    }
+    const f4 gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + 4 * l);
+    const float M = wave_max(l < ns ? hl[0] : -INFINITY);   // finite: split 0 holds key 0
+    const float wl = l < ns ? __expf(hl[0] - M) : 0.f;
+    const float den = wave_sum(hl[1] * wl);
+    const float wk = Q16 ? wl * hl[2] : wl;   // int16 records: the scale k folded into the weight
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        // lanes at or past ns hold weight 0; their slots reloaded split ns - 1, which the row sees,
+        // so a non-finite O there reaches the output through that split's own term anyway
+        const float wj = readlane_f(wk, j);
+        if constexpr (Q16) {
+            // int16 pairs, low half first: sign-extend, convert
+            const int32_t a = (int32_t)qv[j][0], b = (int32_t)qv[j][1];
+            o += f4{(float)((a << 16) >> 16), (float)(a >> 16), (float)((b << 16) >> 16), (float)(b >> 16)} * wj;
+        } else {
+            o += ov[j] * wj;
+        }
+    }
+    f4 res;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) res[e] = o[e] / den * sigmoidf_(gt[e]);
+    *(f4*)(out + (size_t)t * ots + (size_t)h * HD + 4 * l) = res;
+}
+
 // Merge without barriers: one wave per (token, head, 16-dim block). Lane l takes splits l, l + 64,
 // ... (SPL of them, loads clamped to the last valid split and masked), merges them in registers,
 // then the 64 lanes are reduced by a halving butterfly: the swap across lane halves (and across
@@ -799,8 +850,13 @@ hipError_t launch_attn_combine(const float* q, int qts, const float* part, int p
     const unsigned wgs = (unsigned)(((long)nt * nh * 16 + 3) / 4);   // 4 waves each
     // the wave merge for the few rows of decode and verify; the workgroup merge (fewer, longer
     // waves) for the many rows of a prefill chunk
-    if ((long)nt * nh > 256 && smax <= 32)
-        attn_combine_kernel<4><<<dim3(1, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
+    const unsigned rwgs = (unsigned)(((long)nt * nh + 3) / 4);   // one wave per row
+    if ((long)nt * nh > 256 && smax <= 8)
+        attn_combine_row_kernel<8, false><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+    else if ((long)nt * nh > 256 && smax <= 16)
+        attn_combine_row_kernel<16, false><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+    else if ((long)nt * nh > 256 && smax <= 32)
+        attn_combine_row_kernel<32, false><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
     else if ((long)nt * nh > 256)
         attn_combine_kernel<16><<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
     else if (smax <= 64)
@@ -817,8 +873,13 @@ hipError_t launch_attn_combine(const float* q, int qts, const float* part, int p
 hipError_t launch_attn_combine_q16(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                    float* out, int ots, hipStream_t st) {
     const int smax = (pos0 + nt + chunk - 1) / chunk;
-    if (smax <= 32)
-        attn_combine_kernel<4, true><<<dim3(1, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
+    const unsigned rwgs = (unsigned)(((long)nt * nh + 3) / 4);   // one wave per row
+    if (smax <= 8)
+        attn_combine_row_kernel<8, true><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+    else if (smax <= 16)
+        attn_combine_row_kernel<16, true><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+    else if (smax <= 32)
+        attn_combine_row_kernel<32, true><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
     else
         attn_combine_kernel<16, true><<<dim3(4, nh, nt), 256, 0, st>>>(q, qts, pos0, nh, part, chunk, smax, out, ots);
     return hipGetLastError();
