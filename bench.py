@@ -389,8 +389,8 @@ def main():
         qm = torch.randn(64, NH * 2 * HD, device=dev, generator=g)
         om = torch.empty(64, NH * HD, device=dev)
         from irontimber_amd._lib import lib as _lm
-        scm = torch.empty(max(_lm().it_attn_f32kv_scratch_bytes(S8 - 64, 64, HD, NH, NKV),
-                              _lm().it_attn_f32kv_scratch_bytes(S8 - 2, 2, HD, NH, NKV)), dtype=torch.uint8, device=dev)
+        scm = torch.empty(max(_lm().it_attn_f32kv_scratch_bytes(p0, n, HD, NH, NKV)
+                              for p0, n in ((S8 - 1, 1), (S8 - 2, 2), (4096, 64))), dtype=torch.uint8, device=dev)
 
         def mtp_attn(i, nt, pos0):
             call("it_attn_f32kv", qm.data_ptr(), NH * 2 * HD, kf[i % NMT].data_ptr(), vf[i % NMT].data_ptr(), KVD, pos0,

@@ -101,9 +101,23 @@ bool plan_attn(int pos0, int nt, int nh, int nkv, int kernel, size_t budget, Att
 // writes the output directly and needs no scratch (the reference falls back to its whole-context
 // `attn` kernel there, src/vk/mod.rs:740). Always succeeds.
 struct F32kvPlan { int chunk; size_t bytes; };
+// The f32-KV kernel's preferred split. Calls of one block of query rows (decode, verify: up to 32
+// rows per KV head) keep one 64-key tile per split. Calls with several row blocks (the 64-token
+// catch-up) read each K/V tile once per block, so they take 256-key splits, doubled while the grid
+// has more than 640 workgroups (measured for 64 tokens at slot 1024 / 4096 / 8128: 36 / 102 /
+// 127 us against 45 / 131 / 242 us with 64-key splits).
+int f32kv_pref_chunk(int pos0, int nt, int nh, int nkv) {
+    const int G = nh / nkv;
+    if ((long)nt * G <= 32) return auto_chunk(pos0, nt, nh, nkv);
+    const long total = (long)pos0 + nt;
+    const long blocks = ((long)nt * G + 31) / 32;   // 32-row blocks of the multi-block kernel
+    int c = 256;
+    while (c < total && ((total + c - 1) / c) * nkv * blocks > 640) c *= 2;
+    return c > auto_chunk(pos0, nt, nh, nkv) ? c : auto_chunk(pos0, nt, nh, nkv);
+}
 F32kvPlan plan_f32kv(int pos0, int nt, int nh, int nkv, size_t budget) {
     const long total = (long)pos0 + nt;
-    int c = auto_chunk(pos0, nt, nh, nkv);
+    int c = f32kv_pref_chunk(pos0, nt, nh, nkv);
     while (splitk_scratch(pos0, nt, nh, c) > budget && c < total) c *= 2;
     if (splitk_scratch(pos0, nt, nh, c) > budget) return {0, 0};
     return {c, splitk_scratch(pos0, nt, nh, c)};
@@ -231,7 +245,7 @@ int it_attn_prep_f32kv(float* q, int qts, const float* k, const float* v, int kt
 size_t it_attn_f32kv_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv) {
     (void)hd;
     if (nt <= 0 || pos0 < 0 || nh <= 0 || nkv <= 0 || nh % nkv) return 0;
-    return splitk_scratch(pos0, nt, nh, auto_chunk(pos0, nt, nh, nkv));
+    return splitk_scratch(pos0, nt, nh, f32kv_pref_chunk(pos0, nt, nh, nkv));
 }
 
 int it_attn_f32kv_plan(int pos0, int nt, int hd, int nh, int nkv, size_t scratch_bytes, int* chunk, size_t* bytes) {

@@ -851,9 +851,9 @@ hipError_t launch_attn_combine(const float* q, int qts, const float* part, int p
     // the wave merge for the few rows of decode and verify; the workgroup merge (fewer, longer
     // waves) for the many rows of a prefill chunk
     const unsigned rwgs = (unsigned)(((long)nt * nh + 3) / 4);   // one wave per row
-    if ((long)nt * nh > 256 && smax <= 8)
+    if (smax <= 8)
         attn_combine_row_kernel<8, false><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
-    else if ((long)nt * nh > 256 && smax <= 16)
+    else if (smax <= 16)
         attn_combine_row_kernel<16, false><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
     else if ((long)nt * nh > 256 && smax <= 32)
         attn_combine_row_kernel<32, false><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);

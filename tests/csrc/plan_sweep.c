@@ -3,7 +3,8 @@
  * (attention_dispatch_room, src/vk/mod.rs:148-150, in words). Host-only: loads libit_attn.so with
  * dlopen and calls no device function. Prints "ok <plans>" or the first failing geometry.
  * With a sixth argument "f32kv" it sweeps it_attn_f32kv_plan (the MTP head's attention) instead,
- * with the room of the configured capacity, and prints "ok <plans> <grown> <one_pass>". */
+ * with the room of the configured capacity divided by an optional seventh argument (default 1),
+ * and prints "ok <plans> <grown> <one_pass>". */
 #include <dlfcn.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -15,13 +16,13 @@ typedef int (*plan32_fn)(int, int, int, int, int, size_t, int*, size_t*);
 
 /* every f32-KV plan fits the room, splits are multiples of 64 keys, the preferred split is kept when
  * it fits and the one-pass form is used only where one record per (token, head) does not fit */
-static int sweep_f32kv(void* h, int nh, int nkv, int ctxmax, int ntmax) {
+static int sweep_f32kv(void* h, int nh, int nkv, int ctxmax, int ntmax, int div) {
     plan32_fn plan = (plan32_fn)dlsym(h, "it_attn_f32kv_plan");
     room_fn room = (room_fn)dlsym(h, "it_attention_dispatch_room");
     if (!plan || !room) { fprintf(stderr, "missing symbols\n"); return 2; }
     long plans = 0, grown = 0, one_pass = 0;
     for (int nt = 1; nt <= ntmax; ++nt) {
-        const size_t budget = room(ctxmax, nh, nt) * 4;
+        const size_t budget = room(ctxmax, nh, nt) * 4 / div;
         for (int pos0 = 0; pos0 + nt <= ctxmax; ++pos0) {
             int chunk = -1, c2 = -1;
             size_t bytes = 0, pref = 0;
@@ -61,7 +62,7 @@ int main(int argc, char** argv) {
     room_fn room = (room_fn)dlsym(h, "it_attention_dispatch_room");
     if (!plan || !room) { fprintf(stderr, "missing symbols\n"); return 2; }
     const int nh = atoi(argv[2]), nkv = atoi(argv[3]), ctxmax = atoi(argv[4]), ntmax = atoi(argv[5]);
-    if (argc > 6 && !strcmp(argv[6], "f32kv")) return sweep_f32kv(h, nh, nkv, ctxmax, ntmax);
+    if (argc > 6 && !strcmp(argv[6], "f32kv")) return sweep_f32kv(h, nh, nkv, ctxmax, ntmax, argc > 7 ? atoi(argv[7]) : 1);
     long plans = 0, flash_one_pass = 0, grown = 0;
     for (int nt = 1; nt <= ntmax; ++nt) {
         for (int pos0 = 0; pos0 + nt <= ctxmax; ++pos0) {

@@ -271,20 +271,29 @@ def test_gdn_prefill_host_side():
     assert call(nt=0) == 0                        # nothing to do, no device work
 
 
-@pytest.mark.parametrize("nh,nkv,ctx", [(16, 2, 8192), (24, 4, 8192), (16, 2, 300)])
-def test_f32kv_plan_fits_reference_room_sweep(nh, nkv, ctx):
+@pytest.mark.parametrize("nh,nkv,ctx,div", [(16, 2, 8192, 1), (24, 4, 8192, 1), (16, 2, 300, 1), (16, 2, 8192, 16),
+                                            (24, 4, 8192, 64), (16, 2, 8192, 4096)])
+def test_f32kv_plan_fits_reference_room_sweep(nh, nkv, ctx, div):
     """The MTP head's f32-KV attention: for every nt 1..64 and pos0 <= ctx - nt, the split that
     it_attn_f32kv picks for the reference room at capacity ctx (attention_dispatch_room,
-    src/vk/mod.rs:148-150) fits it, keeps the preferred split when that fits, follows the record
-    formula, and never takes the one-pass form while a record per (token, head) fits."""
+    src/vk/mod.rs:148-150), or for 1/div of it, fits it, keeps the preferred split when that fits,
+    follows the record formula, and takes the one-pass form only where a record per (token, head)
+    does not fit."""
     import subprocess
     exe = os.path.join(ROOT, "tests", "csrc", "plan_sweep")
-    r = subprocess.run([exe, _lib.LIB_PATH, str(nh), str(nkv), str(ctx), "64", "f32kv"], capture_output=True,
-                       text=True, timeout=120)
+    r = subprocess.run([exe, _lib.LIB_PATH, str(nh), str(nkv), str(ctx), "64", "f32kv", str(div)],
+                       capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout + r.stderr
     plans, grown, one_pass = map(int, r.stdout.split()[1:])
-    assert plans == sum(ctx - nt + 1 for nt in range(1, 65)) and one_pass == 0
-    assert grown > 0 if ctx == 8192 else True
+    assert plans == sum(ctx - nt + 1 for nt in range(1, 65))
+    # the one-pass form exactly for the call sizes whose one record per (token, head) exceeds the
+    # budget (every pos0 of such an nt)
+    room = lambda nt: _lib.lib().it_attention_dispatch_room(ctx, nh, nt) * 4 // div
+    assert one_pass == sum(ctx - nt + 1 for nt in range(1, 65) if nt * nh * 1040 > room(nt))
+    if div == 1 and ctx == 8192:   # the reference room holds the preferred split everywhere
+        assert grown == 0 and one_pass == 0
+    if div > 1:   # a smaller arena: splits grow
+        assert grown > 0
 
 
 def f32kv_plan(pos0, nt, nh, nkv, budget):
@@ -298,17 +307,24 @@ def test_f32kv_plan_cases():
     # decode at 8192 slots keeps 64-key splits within the room
     room1 = lib.it_attention_dispatch_room(8192, 16, 1) * 4
     assert f32kv_plan(8191, 1, 16, 2, room1) == (0, 64, 16 * 128 * 1040)
-    # the MTP catch-up of 64 tokens at slot 4096: the preferred 64-key split needs 69,222,400 B,
-    # the room is 33,554,432 B; the split doubles to 128 keys (34,611,200 B) -> 256 (17,305,600 B)
+    # the MTP catch-up of 64 tokens at slot 4096: 64-key splits would need 69,222,400 B against a
+    # room of 33,554,432 B (the reference doubles its C from 64 to 256 to fit, src/vk/mod.rs:731-733);
+    # the library prefers 256-key splits for multi-block calls, 17 splits = 18,104,320 B
     room64 = lib.it_attention_dispatch_room(8192, 16, 64) * 4
     assert room64 == 33554432
-    assert lib.it_attn_f32kv_scratch_bytes(4096, 64, 256, 16, 2) == 69222400
-    assert f32kv_plan(4096, 64, 16, 2, room64) == (0, 256, 64 * 16 * 17 * 1040)
-    # the reference's own doubling (src/vk/mod.rs:731-733) ends at the same C here
+    assert 64 * 16 * 65 * 1040 == 69222400
     total, c = 4096 + 64, 64
     while c < 1024 and 64 * 16 * -(-total // c) * 260 * 4 > room64:
         c *= 2
     assert c == 256
+    assert lib.it_attn_f32kv_scratch_bytes(4096, 64, 256, 16, 2) == 64 * 16 * 17 * 1040
+    assert f32kv_plan(4096, 64, 16, 2, room64) == (0, 256, 64 * 16 * 17 * 1040)
+    # at slot 8128 the preferred split is 512 keys (16 splits x 2 KV heads x 16 row blocks = 512
+    # workgroups); a budget of 5 records per row doubles it to 2048
+    assert f32kv_plan(8128, 64, 16, 2, room64) == (0, 512, 64 * 16 * 16 * 1040)
+    assert f32kv_plan(8128, 64, 16, 2, 64 * 16 * 5 * 1040) == (0, 2048, 64 * 16 * 4 * 1040)
+    # one row block (decode, verify) keeps 64-key splits
+    assert f32kv_plan(8188, 4, 16, 2, 1 << 40)[1] == 64
     # past the reference's 1024 keys: one split over every key still needs only a record per row
     assert f32kv_plan(8000, 64, 16, 2, 64 * 16 * 1040) == (0, 8192, 64 * 16 * 1040)
     # below one record per (token, head): the one-pass form, no scratch

@@ -116,7 +116,7 @@ def test_f32kv_reference_room_is_enough(dev, pos0, nt):
     (attention_dispatch_room, src/vk/mod.rs:148-150; the f32 branch's C doubling, 730-733), with a
     guard band behind it: the split grows until the records fit, nothing past the room is written,
     and the result matches the restatement of mtp.rs:122-130. nt = 64 from slot 1921 on is the MTP
-    prefill catch-up (vk/mod.rs:1002 -> 942), which the library's preferred split overflows."""
+    prefill catch-up (vk/mod.rs:1002 -> 942), which 64-key splits overflow."""
     from irontimber_amd._lib import lib
     nh, nkv = 16, 2
     room = lib().it_attention_dispatch_room(8192, nh, nt) * 4
