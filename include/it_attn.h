@@ -127,7 +127,9 @@ int it_attn_f16_noalloc(const float* q, int q_tok_stride, const uint16_t* kc, co
  * kernels/src/lib.rs:722-798), with the split records and their merge in one kernel: each split
  * writes its record to a caller-owned mailbox, per 16 output dims, and the waves that merge a
  * (token, head, 16 dims) unit wait for exactly the pieces they read. Results are bit-identical to
- * it_attn_f16's. Taken when the geometry qualifies: a split-K call (nt < 16) with at most 8 query
+ * it_attn_f16's. Slower than it_attn_f16 on MI355X (9.7 against 9.4 us per layer at ctx 8192),
+ * and it relies on its whole grid being resident at once, so it_attn_f16 is the default; this
+ * form is for a GPU the caller has to itself where one launch per layer matters. Taken when the geometry qualifies: a split-K call (nt < 16) with at most 8 query
  * rows per KV head (nt * nh / nkv <= 8: decode), at most 256 splits of 64 keys (pos0 + nt <= 16384)
  * and enough of them to give every (token, head, 16-dim block) merge a wave of its own (nt * nh *
  * 16 <= 4 * splits * nkv * row groups: with fewer, as at ctx 512, two launches are faster),
