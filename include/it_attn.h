@@ -144,7 +144,10 @@ int it_attn_f16_noalloc(const float* q, int q_tok_stride, const uint16_t* kc, co
  * (possible only if other work holds the device's compute units) gives up, writes NaN outputs and
  * poisons the mailbox: every later call then gives NaN at once until it_attn_mailbox_init runs
  * again. A mailbox that was never initialised (or was overwritten) is treated as poisoned too;
- * it_attn_mailbox_poisoned reports either. */
+ * it_attn_mailbox_poisoned reports either. A merge that finds its mailbox poisoned also sets a
+ * host-visible word that it_attn_mailbox_init allocates for the mailbox (pinned, one per mailbox,
+ * kept until the process ends), so once such a call has completed, the next it_attn_f16_mailbox
+ * call with that mailbox returns -1 ("poisoned", before any device work) instead of NaN again. */
 size_t it_attn_mailbox_bytes(int ctx, int nt, int nh);
 int it_attn_mailbox_init(void* mailbox, size_t bytes, void* stream);
 int it_attn_mailbox_poisoned(const void* mailbox, int* poisoned, void* stream);   /* synchronises stream */

@@ -3,6 +3,8 @@
 // checks (src/vk/mod.rs:179-220); runtime errors come back as nonzero codes with a thread-local
 // message instead of the reference's panics.
 #include <mutex>
+#include <unordered_map>
+#include <utility>
 #include <string>
 #include <cstdio>
 #include <cstdarg>
@@ -165,6 +167,31 @@ int noalloc_scratch(void** out) {
         g_scratch_dev[dev] = p;
     }
     *out = g_scratch_dev[dev];
+    return 0;
+}
+
+// Host-visible report words of the mailboxes this process initialised (one pinned, coherent word
+// each, kept until the process ends): a merge that finds its mailbox poisoned sets the word, and
+// it_attn_f16_mailbox checks it without touching the device.
+std::mutex g_report_mu;
+std::unordered_map<const void*, std::pair<volatile uint32_t*, uint32_t*>> g_report;
+
+int mailbox_report(const void* mailbox, bool create, volatile uint32_t** host, uint32_t** dev) {
+    std::lock_guard<std::mutex> lk(g_report_mu);
+    auto it = g_report.find(mailbox);
+    if (it == g_report.end()) {
+        if (!create) { *host = nullptr; if (dev) *dev = nullptr; return 0; }
+        void* h = nullptr;
+        hipError_t e = hipHostMalloc(&h, 64, hipHostMallocCoherent | hipHostMallocMapped);
+        if (e != hipSuccess) return fail("it_attn_mailbox_init: hipHostMalloc: %s", hipGetErrorString(e));
+        void* d = nullptr;
+        e = hipHostGetDevicePointer(&d, h, 0);
+        if (e != hipSuccess) return fail("it_attn_mailbox_init: hipHostGetDevicePointer: %s", hipGetErrorString(e));
+        *(volatile uint32_t*)h = 0;
+        it = g_report.emplace(mailbox, std::make_pair((volatile uint32_t*)h, (uint32_t*)d)).first;
+    }
+    *host = it->second.first;
+    if (dev) *dev = it->second.second;
     return 0;
 }
 
@@ -387,7 +414,11 @@ size_t it_attn_mailbox_bytes(int ctx, int nt, int nh) {
 int it_attn_mailbox_init(void* mailbox, size_t bytes, void* stream) {
     if (!mailbox || bytes < it::mailbox_bytes(1, 1, 1) || bytes % 4) return fail("it_attn_mailbox_init: bad buffer");
     if (!aligned16(mailbox)) return fail("it_attn_mailbox_init: the mailbox must be 16-byte aligned");
-    return check(it::launch_mailbox_fill(mailbox, bytes, (hipStream_t)stream), "it_attn_mailbox_init");
+    volatile uint32_t* host = nullptr;
+    uint32_t* dev = nullptr;
+    if (mailbox_report(mailbox, true, &host, &dev)) return -1;
+    *host = 0;   // now, for the calls that follow; the fill clears it again in stream order
+    return check(it::launch_mailbox_fill(mailbox, bytes, dev, (hipStream_t)stream), "it_attn_mailbox_init");
 }
 
 int it_attn_mailbox_poisoned(const void* mailbox, int* poisoned, void* stream) {
@@ -416,6 +447,15 @@ int it_attn_f16_mailbox(const float* q, int qts, const uint16_t* kc, const uint1
                         void* scratch, size_t scratch_bytes, void* stream) {
     if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, out, ots)) return -1;
     if (mailbox && !aligned16(mailbox)) return fail("it_attn_f16_mailbox: the mailbox must be 16-byte aligned");
+    if (mailbox) {
+        // an earlier call's merge found this mailbox poisoned (it gave up waiting, or the mailbox
+        // was overwritten): fail before any device work instead of returning NaN again
+        volatile uint32_t* host = nullptr;
+        if (mailbox_report(mailbox, false, &host, nullptr)) return -1;
+        if (host && *host)
+            return fail("it_attn_f16_mailbox: the mailbox was found poisoned by an earlier call (a merge gave up "
+                        "waiting); re-initialise it with it_attn_mailbox_init");
+    }
     if (auto_kernel(nt) == KERNEL_SPLITK) {
         bool launched = false;
         if (check(it::launch_attn_decode_mailbox(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots,

@@ -90,7 +90,8 @@ template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
 // MB_EMPTY back, which leaves the buffer ready for the next call. Word 0 of the buffer is the
 // poison flag, set by a merge that gave up waiting; word 1 holds MAILBOX_MAGIC once the buffer is
 // initialised, so a buffer that never was (or was overwritten) fails loudly instead of passing its
-// stale words off as records.
+// stale words off as records; words 2-3 the address of a host-visible report word that a merge
+// which finds the mailbox poisoned sets to 1.
 constexpr int MB_PIECE = 24;        // floats per piece: o[16], {m, l}, unused; whole 32-byte sectors
 constexpr int MB_HEAD = 64;         // floats before the first piece
 constexpr uint32_t MB_EMPTY = 0xFFFFFFFFu;
@@ -710,6 +711,13 @@ __device__ __forceinline__ void mailbox_merge(const float* __restrict__ q, int q
     }
     if (bad) {
         if (l < 16) out[(size_t)t * ots + (size_t)h * HD + d0 + l] = __builtin_nanf("");
+        // tell the host (an initialised header holds the address of its report word), so the
+        // next it_attn_f16_mailbox call with this mailbox fails instead of returning NaN again
+        if (l == 0 && hdr[1] == MAILBOX_MAGIC) {
+            const u2 a = mb_load2(r, 2);
+            uint32_t* rep = (uint32_t*)(uintptr_t)(((uint64_t)a[1] << 32) | a[0]);
+            if (rep) __hip_atomic_store(rep, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
         return;
     }
     // clear the pieces for the next call, then merge (clearing first measured faster: the clears
@@ -746,9 +754,15 @@ __global__ __launch_bounds__(256) void attn_decode_mailbox_kernel(const float* _
         mailbox_merge<SPL>(q, qts, pos0, nh, chunk, smax, r, out, ots, u >> 4, u & 15, threadIdx.x & 63);
 }
 
-__global__ __launch_bounds__(256) void mailbox_fill_kernel(uint32_t* p, size_t words) {
+// Header words 2-3 hold the device address of the mailbox's host-visible report word (0 if none);
+// the fill clears that word too, in stream order after every earlier call.
+__global__ __launch_bounds__(256) void mailbox_fill_kernel(uint32_t* p, size_t words, uint32_t* report) {
+    const uint64_t rp = (uint64_t)(uintptr_t)report;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (size_t)gridDim.x * 256)
-        p[i] = i == 1 ? MAILBOX_MAGIC : i < (size_t)MB_HEAD ? 0u : MB_EMPTY;
+        p[i] = i == 1 ? MAILBOX_MAGIC : i == 2 ? (uint32_t)rp : i == 3 ? (uint32_t)(rp >> 32)
+             : i < (size_t)MB_HEAD ? 0u : MB_EMPTY;
+    if (report && blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(report, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
@@ -837,10 +851,10 @@ hipError_t launch_attn_decode_mailbox(const float* q, int qts, const uint16_t* k
     return hipSuccess;
 }
 
-hipError_t launch_mailbox_fill(void* mb, size_t bytes, hipStream_t st) {
+hipError_t launch_mailbox_fill(void* mb, size_t bytes, uint32_t* report, hipStream_t st) {
     const size_t words = bytes / 4;
     const unsigned blocks = (unsigned)std::min<size_t>((words + 255) / 256, 2048);
-    mailbox_fill_kernel<<<blocks, 256, 0, st>>>((uint32_t*)mb, words);
+    mailbox_fill_kernel<<<blocks, 256, 0, st>>>((uint32_t*)mb, words, report);
     return hipGetLastError();
 }
 

@@ -38,7 +38,9 @@ constexpr uint32_t MAILBOX_MAGIC = 0x4D424F58u;
 hipError_t launch_attn_decode_mailbox(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
                                       int pos0, int nh, int nkv, int nt, float scale, float* out, int ots, float* mb,
                                       size_t mbb, hipStream_t st, bool* launched, bool dry_run = false);
-hipError_t launch_mailbox_fill(void* mb, size_t bytes, hipStream_t st);
+// report: device address of a host-visible word the fill clears and a merge that finds the
+// mailbox poisoned sets (null: none)
+hipError_t launch_mailbox_fill(void* mb, size_t bytes, uint32_t* report, hipStream_t st);
 hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                              int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st);
 

@@ -27,7 +27,9 @@ MAGIC = np.uint32(0x4D424F58)
 
 def _clean(mb):
     words = host(mb).view(np.uint32)
-    return words[0] == 0 and words[1] == MAGIC and (words[2:64] == 0).all() and (words[64:] == EMPTY).all()
+    # words 2-3: the device address of the mailbox's host-visible report word
+    return (words[0] == 0 and words[1] == MAGIC and (words[2:4] != 0).any() and (words[4:64] == 0).all()
+            and (words[64:] == EMPTY).all())
 
 
 # (ctx, nt, nh, nkv, one launch expected): decode at the BASELINE geometry (ctx 8192), 256 splits
@@ -131,7 +133,10 @@ def test_poisoned_mailbox_fails_loudly(dev):
     got = host(ops.attn_f16_mailbox(qd, kc, vc, ctx - 1, nh, nkv, mb))
     assert np.isnan(got).all()
     assert ops.attn_mailbox_poisoned(mb)
-    from irontimber_amd._lib import call
+    # that call has completed: the next one fails before any device work
+    from irontimber_amd._lib import ItError, call
+    with pytest.raises(ItError, match="poisoned"):
+        ops.attn_f16_mailbox(qd, kc, vc, ctx - 1, nh, nkv, mb)
     call("it_attn_mailbox_init", mb.data_ptr(), mb.numel(), torch.cuda.current_stream().cuda_stream)
     got = host(ops.attn_f16_mailbox(qd, kc, vc, ctx - 1, nh, nkv, mb))
     np.testing.assert_array_equal(got, host(ops.attn_f16(qd, kc, vc, ctx - 1, nh, nkv)))
