@@ -66,6 +66,22 @@ __device__ __forceinline__ void v_tile_to_lds(const uint16_t* __restrict__ vc, i
     }
 }
 
+// The same V tile into registers (lane l of wave w: the 16 bytes v_tile_to_lds would land at its
+// slot of rows 16w + 2i + (l >> 5)), written to that slot once the scores and softmax are done.
+__device__ __forceinline__ void v_tile_to_regs(const uint16_t* __restrict__ vc, int kvd, size_t head_off, int kb,
+                                               int kend, u4 (&vr)[8], int w, int l) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = 16 * w + 2 * i + (l >> 5);
+        const int j = (l & 31) ^ vswz(r);
+        vr[i] = *(const u4*)(vc + (size_t)min(kb + r, kend - 1) * kvd + head_off + 8 * j);
+    }
+}
+__device__ __forceinline__ void v_regs_to_lds(const u4 (&vr)[8], _Float16* lds, int w, int l) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *(u4*)(lds + (16 * w + 2 * i + (l >> 5)) * HD + 8 * (l & 31)) = vr[i];
+}
+
 // K rows as the A operand of S^T = K q^T: lane l holds key kb + 16w + (l & 15), dims 32ks + 8*(l >> 4).
 __device__ __forceinline__ void k_tile_to_regs(const uint16_t* __restrict__ kc, int kvd, size_t head_off, int kb,
                                                int kend, u4 (&kr)[8], int w, int l) {
@@ -131,7 +147,15 @@ __device__ __forceinline__ u2 mb_load2(MbRsrc r, int idx) {
     return __builtin_amdgcn_raw_buffer_load_b64(r, 4 * idx, 0, MB_COHERENT);
 }
 
-template <int NB, bool MULTI, bool MB = false>
+// VR (one-tile splits only): V is loaded into registers right behind K and written to LDS after
+// the softmax, instead of the direct global->LDS copy issued after the q planes. With the copy in
+// flight the compiler waits for every outstanding load before the first score product (it treats a
+// pending global->LDS copy and ordinary loads as completing out of order), so the scores and the
+// softmax could not start until V had landed; with ordinary loads the counter stays in order and
+// the scores wait for K only. Decode at ctx 8192: partial kernel 5.95 -> 5.65 us, layer 9.41 ->
+// 9.13 us; with few workgroups (ctx 512, 16 of them) the copy is faster (6.09 against 6.27 us per
+// layer), so the launch takes VR from 64 workgroups up.
+template <int NB, bool MULTI, bool MB = false, bool VR = false>
 __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc,
                                                const uint16_t* __restrict__ vc, int kvd, int pos0, int nh, int nkv,
                                                int nt, float scale, float* __restrict__ part, int chunk, int smax,
@@ -167,6 +191,9 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
     }
     u4 kr[8];
     k_tile_to_regs(kc, kvd, head_off, p0, pend, kr, w, l);
+    static_assert(!(VR && MULTI), "V in registers is for one-tile splits");
+    u4 vr[VR ? 8 : 1];
+    if constexpr (VR) v_tile_to_regs(vc, kvd, head_off, p0, pend, vr, w, l);
 #pragma unroll
     for (int it = 0; it < QPT; ++it) {
         const int idx = tid + 256 * it, row = idx >> 5, d0 = 8 * (idx & 31);
@@ -218,7 +245,7 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
         for (int ks = 0; ks < 8; ++ks) qb[b][ks] = ld_h8(&Qs[c >> 3][8 * b + (c & 7)][32 * ks + 8 * g]);
     // V goes out only now: the q planes were built while the K rows were in flight, and the scores
     // and softmax below run while V lands (the memory system is kept busy by the other waves' K)
-    v_tile_to_lds(vc, kvd, head_off, p0, pend, V0, w, l);
+    if constexpr (!VR) v_tile_to_lds(vc, kvd, head_off, p0, pend, V0, w, l);
 
     int it = 0;
     for (int kb = p0; kb < pend; kb += TK, ++it) {
@@ -288,7 +315,8 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
             *(h4*)&Ps[b][c][16 * w + 4 * g] = ph;
             if (MULTI && w == 0 && g == 0 && c < 8) Al[row] = a;   // (one tile: nothing to rescale)
         }
-        IT_WAIT_VMCNT(0);   // this tile's V
+        if constexpr (VR) v_regs_to_lds(vr, V0, w, l);   // (the compiler waits for V's loads)
+        else IT_WAIT_VMCNT(0);   // this tile's V
         __syncthreads();    // B: P planes, alpha, V tile
         // prefetch the next tile (K registers are free, the other V buffer was last read two
         // barriers ago)
@@ -377,13 +405,13 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
     }
 }
 
-template <int NB, bool MULTI>
+template <int NB, bool MULTI, bool VR = false>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, int qts,
                                                           const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, int kvd, int pos0, int nh,
                                                           int nkv, int nt, float scale, float* __restrict__ part,
                                                           int chunk, int smax) {
-    decode_partial<NB, MULTI>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax, blockIdx.x, blockIdx.y,
+    decode_partial<NB, MULTI, false, VR>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax, blockIdx.x, blockIdx.y,
                        blockIdx.z);
 }
 
@@ -745,7 +773,7 @@ __global__ __launch_bounds__(256) void attn_decode_mailbox_kernel(const float* _
                                                                   int nh, int nkv, int nt, float scale, int chunk,
                                                                   int smax, float* mb, uint32_t mbb,
                                                                   float* __restrict__ out, int ots) {
-    decode_partial<NB, false, true>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, nullptr, chunk, smax, blockIdx.x,
+    decode_partial<NB, false, true, true>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, nullptr, chunk, smax, blockIdx.x,
                                     blockIdx.y, blockIdx.z, mb, mbb);
     const int nwg = gridDim.x * gridDim.y * gridDim.z;
     const int wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
@@ -783,8 +811,17 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
                                                                 chunk, smax)                                        \
            : attn_decode_kernel<NB_, false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, \
                                                                  chunk, smax))
+    // decode rows (one block of 8) over 64 or more workgroups load V into registers (see
+    // decode_partial); verify blocks measured equal either way and keep the copy
+    const bool vr = !multi && rows == 8 && (long)grid.x * grid.y * grid.z >= 64;
     switch (rows / 8) {
-        case 1: IT_DECODE_LAUNCH(1); break;
+        case 1:
+            if (vr)
+                attn_decode_kernel<1, false, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale,
+                                                                        part, chunk, smax);
+            else
+                IT_DECODE_LAUNCH(1);
+            break;
         case 2: IT_DECODE_LAUNCH(2); break;
         case 3: IT_DECODE_LAUNCH(3); break;
         default: IT_DECODE_LAUNCH(4); break;
