@@ -308,10 +308,8 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
         r.a = ar[(size_t)t * bts + h];
         return r;
     };
-    Tok nx = load_tok(0);
-    for (int t = 0; t < nt; ++t) {
-        const Tok cur = nx;
-        if (t + 1 < nt) nx = load_tok(t + 1);
+    // one token: decay, the fused exchange, the update; the output row (threads tid < 4) in o4
+    auto step = [&](int t, const Tok& cur, f4& o4) {
         const float q0 = cur.q0, q1 = cur.q1, k0 = cur.k0, k1 = cur.k1;
         const f4 v = cur.v;
         const float beta = sigmoid_hw(cur.b);
@@ -338,16 +336,32 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
         if (tid < 4) {
             const f4 sq = (red[b][0][1][cg] + red[b][1][1][cg]) + (red[b][2][1][cg] + red[b][3][1][cg]);
             const float kqs = (rkq[b][0] + rkq[b][1]) + (rkq[b][2] + rkq[b][3]);
-            *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = (sq + kqs * delta) * scale;
+            o4 = (sq + kqs * delta) * scale;
         }
         if (ck && t == ck_after) {
             float* cb_ = ck + (size_t)h * S * S;
             *(f4*)(cb_ + (size_t)i0 * S + j0) = s0;
             *(f4*)(cb_ + (size_t)(i0 + 1) * S + j0) = s1;
         }
+    };
+    // Every token but the last in a loop, storing its output there; the last one (nt >= 1) as
+    // straight-line code with the state stored before its output row. The load counter also
+    // counts stores, and at a loop's merge points the compiler cannot tell which of them a wave
+    // issued, so it waits for all: with the decode step inside the loop, the state stores waited
+    // for the output store's round trip.
+    Tok nx = load_tok(0);
+    f4 o4 = {0.f, 0.f, 0.f, 0.f};
+    int t = 0;
+    for (; t + 1 < nt; ++t) {
+        const Tok cur = nx;
+        nx = load_tok(t + 1);
+        step(t, cur, o4);
+        if (tid < 4) *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = o4;
     }
+    step(t, nx, o4);
     *(f4*)(sb + (size_t)i0 * S + j0) = s0;
     *(f4*)(sb + (size_t)(i0 + 1) * S + j0) = s1;
+    if (tid < 4) *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = o4;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -441,9 +455,10 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     const float dth = dt[h], ah = A[h];
     f4 s0 = ld_f4(sb + (size_t)i0 * S + j0), s1 = ld_f4(sb + (size_t)(i0 + 1) * S + j0);
     const float scale = 1.0f / sqrtf((float)S);
+    f4 olast = {0.f, 0.f, 0.f, 0.f};   // the last token's output row (threads tid < 4)
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-        if (t >= nt) break;   // uniform
+        if (TM > 1 && t >= nt) break;   // uniform (a one-token build runs its token straight-line)
         // ---- conv + SiLU of this thread's channels
         float q[2], k[2];
         f4 v;
@@ -501,7 +516,9 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
         s0 += k0 * delta; s1 += k1 * delta;
         if (tid < 4) {
             const f4 sq4 = (red[b][0][1][cg] + red[b][1][1][cg]) + (red[b][2][1][cg] + red[b][3][1][cg]);
-            *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = (sq4 * fq + (fq * fk * n[2]) * delta) * scale;
+            olast = (sq4 * fq + (fq * fk * n[2]) * delta) * scale;
+            // the last token's row goes out after the state (see below)
+            if (TM > 1 && t + 1 < nt) *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = olast;
         }
         if (t == ck_after) {   // MTP verify checkpoint: both states after this token, from registers
             if (ck_state) {
@@ -524,8 +541,11 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
             }
         }
     }
+    // the state first: the load counter also counts stores, and a wait the compiler places for a
+    // store it cannot count (one under a branch) must not hold up the state
     *(f4*)(sb + (size_t)i0 * S + j0) = s0;
     *(f4*)(sb + (size_t)(i0 + 1) * S + j0) = s1;
+    if (tid < 4) *(f4*)(out + (size_t)(nt - 1) * ots + (size_t)h * S + j0) = olast;
     if (cb == 0 && h == kh && cg == 0) {
 #pragma unroll
         for (int i = 0; i < K - 1; ++i) {
@@ -759,6 +779,7 @@ hipError_t launch_l2norm(float* x, int ts, int nheads, int d, int nt, float eps,
 hipError_t launch_gdn_step(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                            const float* a, float* state, float* out, int ots, int nt, int nv, int nk, float* ck,
                            int ck_after, hipStream_t st) {
+    if (nt <= 0) return hipSuccess;   // the kernel runs its last token unconditionally
     gdn_step_kernel<<<dim3(8 * nv), 256, 0, st>>>(co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, ck, ck_after);
     return hipGetLastError();
 }
