@@ -377,8 +377,10 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const float* __restrict__
 // use the hardware exp2 / log2 / reciprocal (a few ulp), and the q/k norms, being per-head scalars,
 // are applied after the S k and S^T q sums: their sums of squares share the one exchange of the
 // token (one barrier a token). Results agree with conv + L2 + gdn_step_kernel to rounding.
-// TM: tokens the kernel is built for (1, 2 or 4; nt <= TM): every token's inputs are loaded up
-// front, so a decode step built for one token issues no loads for tokens it does not have.
+// TM: the tokens of the call (1 to 4; the launch builds the kernel for exactly nt = TM): every
+// token's inputs are loaded up front, and the token loop has no exit other than its end, so the
+// compiler's load-counter waits need not assume a path that skipped tokens (such a path made the
+// state stores wait for the output and checkpoint stores of the earlier tokens).
 template <int K, int TM>
 __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     const float* __restrict__ x, int xts, const float* __restrict__ cw, const float* __restrict__ cst_in,
@@ -406,7 +408,7 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     f4 xv[TM];
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-        const float* xr = x + (size_t)min(t, nt - 1) * xts;
+        const float* xr = x + (size_t)t * xts;
         xq[t] = *(const f2*)(xr + cq);
         xk[t] = *(const f2*)(xr + ck);
         xv[t] = ld_f4(xr + cv);
@@ -449,8 +451,8 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     float brt[TM], art[TM];
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-        brt[t] = br[(size_t)min(t, nt - 1) * bts + h];
-        art[t] = ar[(size_t)min(t, nt - 1) * bts + h];
+        brt[t] = br[(size_t)t * bts + h];
+        art[t] = ar[(size_t)t * bts + h];
     }
     const float dth = dt[h], ah = A[h];
     f4 s0 = ld_f4(sb + (size_t)i0 * S + j0), s1 = ld_f4(sb + (size_t)(i0 + 1) * S + j0);
@@ -458,7 +460,6 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     f4 olast = {0.f, 0.f, 0.f, 0.f};   // the last token's output row (threads tid < 4)
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-        if (TM > 1 && t >= nt) break;   // uniform (a one-token build runs its token straight-line)
         // ---- conv + SiLU of this thread's channels
         float q[2], k[2];
         f4 v;
@@ -518,7 +519,7 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
             const f4 sq4 = (red[b][0][1][cg] + red[b][1][1][cg]) + (red[b][2][1][cg] + red[b][3][1][cg]);
             olast = (sq4 * fq + (fq * fk * n[2]) * delta) * scale;
             // the last token's row goes out after the state (see below)
-            if (TM > 1 && t + 1 < nt) *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = olast;
+            if (t + 1 < TM) *(f4*)(out + (size_t)t * ots + (size_t)h * S + j0) = olast;
         }
         if (t == ck_after) {   // MTP verify checkpoint: both states after this token, from registers
             if (ck_state) {
@@ -545,7 +546,7 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     // store it cannot count (one under a branch) must not hold up the state
     *(f4*)(sb + (size_t)i0 * S + j0) = s0;
     *(f4*)(sb + (size_t)(i0 + 1) * S + j0) = s1;
-    if (tid < 4) *(f4*)(out + (size_t)(nt - 1) * ots + (size_t)h * S + j0) = olast;
+    if (tid < 4) *(f4*)(out + (size_t)(TM - 1) * ots + (size_t)h * S + j0) = olast;
     if (cb == 0 && h == kh && cg == 0) {
 #pragma unroll
         for (int i = 0; i < K - 1; ++i) {
@@ -569,7 +570,8 @@ hipError_t launch_gdn_decode_fused(const float* x, int xts, const float* cw, int
                                                           out, ots, nt, nv, nk, eps, ck_state, ck_conv, ck_after)
 #define IT_FUSED_T(KK)                    \
     if (nt <= 1) IT_FUSED(KK, 1);         \
-    else if (nt <= 2) IT_FUSED(KK, 2);    \
+    else if (nt == 2) IT_FUSED(KK, 2);    \
+    else if (nt == 3) IT_FUSED(KK, 3);    \
     else IT_FUSED(KK, 4);
     switch (K) {
         case 2: IT_FUSED_T(2) break;
