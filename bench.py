@@ -118,7 +118,7 @@ def measure_decode_traffic():
     """HBM bytes per launch of the ctx-8192 partial kernel: FETCH_SIZE and WRITE_SIZE medians, each
     scaled by what the same counter reads for a plain 256 MiB device copy. Returns (bytes, note)."""
     dec = ["--only", "decode", "--no-cpu", "--steps", "20", "--warmup", "2"]
-    kern, grid = "void it::attn_decode_kernel<1, false>", str(32768 * 2)
+    kern, grid = "void it::attn_decode_kernel<1, false, true>", str(32768 * 2)
     got = {}
     for key, counter, args, k, g in (("fetch", "FETCH_SIZE", dec, kern, grid),
                                      ("write", "WRITE_SIZE", dec, kern, grid),
@@ -693,7 +693,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": rnd(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": rnd(None if part_gbs is None else part_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_unit": "bytes per launch", "traffic_source": traffic_note,
-                     "kernel": "attn_decode_kernel<1, false>", "kernel_us": rnd(part_us, 3),
+                     "kernel": "attn_decode_kernel<1, false, true>", "kernel_us": rnd(part_us, 3),
                      "bytes_per_launch": dbytes},
         "roofline_prefill": {"bound": "mfma", "achieved": prefill_tflops, "peak": F16_MFMA_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": rnd(None if prefill_tflops is None else prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4),
