@@ -152,3 +152,25 @@ def test_uninitialised_mailbox_fails_loudly(dev):
     assert ops.attn_mailbox_poisoned(mb)
     got = host(ops.attn_f16_mailbox(qd, kc, vc, ctx - 1, nh, nkv, mb))
     assert np.isnan(got).all()
+
+
+@pytest.mark.parametrize("bits", [0xFFFF, 0x7E01, 0xFC00])
+def test_nonfinite_value_does_not_poison_the_mailbox(dev, bits):
+    """A NaN or infinite value in V (f16 0xFFFF: a NaN with every payload bit set; 0x7E01; -inf)
+    reaches the outputs of that call as it does on the two-launch path, and leaves the mailbox
+    clean: record words are stored with NaN canonicalised, so no stored word equals the empty
+    pattern and no merge waits on a piece that looks unwritten. The next call is exact again."""
+    nh, nkv, ctx = 16, 2, 8192
+    q, kb, vb, qd, kc, vc = _inputs(dev, 13, ctx, 1, nh, nkv)
+    mb = ops.attn_mailbox(ctx, 1, nh, dev)
+    bad = vb.copy()
+    bad[4000, 3] = bits                      # key 4000, KV head 0, dim 3
+    vbad = dev_f16bits(bad, dev)
+    got = host(ops.attn_f16_mailbox(qd, kc, vbad, ctx - 1, nh, nkv, mb))
+    ref = host(ops.attn_f16(qd, kc, vbad, ctx - 1, nh, nkv))
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    np.testing.assert_array_equal(np.isinf(got), np.isinf(ref))
+    assert not np.isfinite(got[0, 3])        # head 0 sees the key: dim 3 is not finite
+    assert not ops.attn_mailbox_poisoned(mb) and _clean(mb)
+    got = host(ops.attn_f16_mailbox(qd, kc, vc, ctx - 1, nh, nkv, mb))
+    np.testing.assert_array_equal(got, host(ops.attn_f16(qd, kc, vc, ctx - 1, nh, nkv)))
