@@ -182,7 +182,7 @@ int mailbox_report(const void* mailbox, bool create, volatile uint32_t** host, u
     if (it == g_report.end()) {
         if (!create) { *host = nullptr; if (dev) *dev = nullptr; return 0; }
         void* h = nullptr;
-        hipError_t e = hipHostMalloc(&h, 64, hipHostMallocCoherent | hipHostMallocMapped);
+        hipError_t e = hipHostMalloc(&h, 64, hipHostMallocCoherent | hipHostMallocMapped | hipHostMallocPortable);
         if (e != hipSuccess) return fail("it_attn_mailbox_init: hipHostMalloc: %s", hipGetErrorString(e));
         void* d = nullptr;
         e = hipHostGetDevicePointer(&d, h, 0);
