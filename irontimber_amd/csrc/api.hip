@@ -684,7 +684,7 @@ int it_gdn_rollback(const float* ck_conv, float* conv_state, size_t conv_words, 
 
 size_t it_gdn_chunked_scratch_bytes(int nt, int nv, int S) {
     if (nt <= 0 || nv <= 0 || S != 128) return 0;
-    return it::gdn_chunked_scratch_bytes(nt, nv, S);
+    return it::gdn_chunked_scratch_bytes(nt, nv, S, false);
 }
 
 int it_gdn_chunked(const float* co, int cts, const float* br, const float* ar, int bts, const float* dt, const float* a,
@@ -692,7 +692,7 @@ int it_gdn_chunked(const float* co, int cts, const float* br, const float* ar, i
                    void* stream) {
     if (validate_gdn("it_gdn_chunked", co, cts, br, ar, bts, dt, a, state, out, ots, nt, nv, nk, S)) return -1;
     if (nt == 0) { g_err.clear(); return 0; }
-    const size_t need = it::gdn_chunked_scratch_bytes(nt, nv, S);
+    const size_t need = it::gdn_chunked_scratch_bytes(nt, nv, S, false);
     if (scratch_bytes < need || (need && !scratch))
         return fail("it_gdn_chunked: scratch of %zu bytes < %zu required", scratch_bytes, need);
     if (!aligned16(scratch)) return fail("it_gdn_chunked: scratch must be 16-byte aligned");
@@ -707,7 +707,7 @@ static size_t gdn_prefill_co_bytes(int nt, int nv, int nk, int S) {
 
 size_t it_gdn_prefill_scratch_bytes(int nt, int nv, int nk, int S) {
     if (nt <= 0 || nv <= 0 || nk <= 0 || S != 128) return 0;
-    return gdn_prefill_co_bytes(nt, nv, nk, S) + it::gdn_chunked_scratch_bytes(nt, nv, S);
+    return gdn_prefill_co_bytes(nt, nv, nk, S) + it::gdn_chunked_scratch_bytes(nt, nv, S, true);
 }
 
 int it_gdn_prefill(const float* x, int xts, const float* w, int K, float* conv_state, const float* br, const float* ar,

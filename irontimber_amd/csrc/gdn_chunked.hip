@@ -10,13 +10,17 @@
 // decay differences G_t - G_s <= 0 (t >= s) are exponentiated, so nothing overflows.
 //
 // Kernel 1 (gdn_chunk_prep, one workgroup per (chunk, V head), all chunks in parallel) produces
-// everything that does not depend on S0: W and e^G Q (f16), U (f32), the decayed K^T (f16),
-// the masked Q K^T block (f16) and e^{G_last}. K K^T / Q K^T are f16 MFMA products of hi+lo
-// splits (three products, ~f32 accurate); the triangular solve is blocked by 16 rows: small
-// substitutions for the diagonal blocks, MFMA hi+lo products for the rest.
-// Kernel 2 (gdn_chunk_scan, one workgroup per (32-column block of the state, V head)) walks the
-// chunks in order with its 128x32 slice of S in MFMA accumulators; S0 and V' enter the products
-// as f16 hi+lo pairs through LDS, so the state path keeps f32 accuracy.
+// everything that does not depend on S0 and is not a row of q or k: W (f16), U (f32), the masked
+// Q K^T block (f16) and a table of the chunk's decays (G, e^G, e^{G_last - G}, e^{G_last}).
+// K K^T / Q K^T are f16 MFMA products of hi+lo splits (three products, ~f32 accurate); the solve
+// is blocked by 16 rows: small substitutions for the diagonal blocks, MFMA hi+lo products for the
+// rest. From an f32 conv output it also writes the chunk's q and k rows as f16; an f16 conv
+// output is read in place by kernel 2.
+// Kernel 2 (gdn_chunk_scan, one workgroup per (16-column block of the state, V head)) walks the
+// chunks in order with its 128x16 slice of S in MFMA accumulators; S0 and V' enter the products
+// as f16 hi+lo pairs through LDS, so the state path keeps f32 accuracy. It takes e^G Q S0 as
+// (Q S0) scaled per row, and the decayed K^T as the k rows read transposed from LDS and scaled
+// per token, so neither is kept in the records.
 #include "common.h"
 #include "internal.h"
 
@@ -27,19 +31,22 @@ constexpr int C = 64;      // chunk length
 constexpr int SD = 128;    // state size (d_k = d_v)
 // per-(V head, chunk) record in scratch, byte offsets
 constexpr size_t OFF_W = 0;                        // f16 [C][SD]   W (token-major)
-constexpr size_t OFF_QG = OFF_W + C * SD * 2;       // f16 [C][SD]   e^{G_t} q_t
-constexpr size_t OFF_KT = OFF_QG + C * SD * 2;      // f16 [SD][C]   e^{G_last - G_t} k_t, transposed
-constexpr size_t OFF_AQK = OFF_KT + SD * C * 2;     // f16 [C][C]    lower_incl(D * Q K^T)
-constexpr size_t OFF_U = OFF_AQK + C * C * 2;       // f32 [C][SD]   U
-constexpr size_t OFF_GC = OFF_U + C * SD * 4;       // f32 [4]       e^{G_last} (4 copies)
-constexpr size_t REC = (OFF_GC + 16 + 255) / 256 * 256;
+constexpr size_t OFF_U = OFF_W + C * SD * 2;        // f32 [C][SD]   U
+constexpr size_t OFF_T = OFF_U + C * SD * 4;        // f32 [4][C]    G, e^G, e^{G_last - G}, e^{G_last} (x64)
+constexpr size_t OFF_AQK = OFF_T + 4 * C * 4;       // f16 [C][C]    lower_incl(D * Q K^T)
+constexpr size_t OFF_Q = OFF_AQK + C * C * 2;       // f16 [C][SD]   q rows (f32 conv output only)
+constexpr size_t OFF_K = OFF_Q + C * SD * 2;        // f16 [C][SD]   k rows (f32 conv output only)
+constexpr size_t REC_DIRECT = OFF_Q;                // the scan reads an f16 conv output in place
+constexpr size_t REC_ROWS = OFF_K + C * SD * 2;
+static_assert(REC_DIRECT % 256 == 0 && REC_ROWS % 256 == 0, "records stay 256-byte aligned");
+template <bool DIRECT> constexpr size_t rec_bytes() { return DIRECT ? REC_DIRECT : REC_ROWS; }
 }
 #define IT_SCAN_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt((((N) & 15) | (((N) >> 4) << 14)) | 0x0F70)
 
-size_t gdn_chunked_scratch_bytes(int nt, int nv, int S) {
+size_t gdn_chunked_scratch_bytes(int nt, int nv, int S, bool f16_conv) {
     (void)S;
     const size_t nch = (size_t)(nt + C - 1) / C;
-    return nch * (size_t)nv * REC;
+    return nch * (size_t)nv * (f16_conv ? REC_DIRECT : REC_ROWS);
 }
 
 __device__ __forceinline__ f4 mfma16x16x16(h4 a, h4 b, f4 c) {
@@ -92,8 +99,8 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
     static_assert(2 * C * KP * 2 >= C * SD * 4, "the V rows fit in the K tile");
 
-    // an f16 conv output is exact in f16, so its hi/lo splits have lo == 0 and the K K^T / Q K^T
-    // products need only the hi x hi term (bit-identical to the three-term form)
+    // an f16 conv output is exact in f16, so its hi/lo splits have lo == 0 and the K K^T product
+    // needs only the hi x hi term (bit-identical to the three-term form)
     constexpr bool F16 = sizeof(CoT) == 2;
     const int nch = (nt + C - 1) / C;
     int c, h;
@@ -101,11 +108,8 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     const int t0 = c * C, L = min(C, nt - t0);
     const int kh = h % nk, qk = nk * SD;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
-    char* rec = scr + ((size_t)h * nch + c) * REC;
+    char* rec = scr + ((size_t)h * nch + c) * rec_bytes<F16>();
     const int col = 16 * w + li;                 // this lane's column of the solve
-
-    // q row of this lane in the Q K^T and e^G q products (global; rows past the prompt masked)
-    auto qrow = [&](int t) { return co + (size_t)(t0 + min(t, L - 1)) * cts + kh * SD; };
 
     // the gate inputs go out first (wave 7 computes beta and the cumulative log-decay below)
     float braw = 0.f, araw = 0.f;
@@ -130,6 +134,19 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         split_hi_lo(k0, k1, hi, lo);
         *(h8*)&Kx[0][t][d8] = hi; *(h8*)&Kx[1][t][d8] = lo;
     }
+    // q rows as f16 into the record (f32 conv output only: the scan reads an f16 one in place);
+    // rows past the prompt are zero
+    if constexpr (!F16) {
+#pragma unroll
+        for (int it = 0; it < C * SD / 8 / PREP_THREADS; ++it) {
+            const int idx = tid + it * PREP_THREADS;
+            const int t = idx >> 4, d8 = 8 * (idx & 15);
+            const float m = t < L ? 1.f : 0.f;
+            f4 q0, q1;
+            ld8(co + (size_t)(t0 + min(t, L - 1)) * cts + kh * SD + d8, q0, q1);
+            ((u4*)(rec + OFF_Q))[idx] = __builtin_bit_cast(u4, to_h8(q0 * m, q1 * m));
+        }
+    }
     // q rows of the Q K^T waves (below), issued after the K rows so the K staging never waits for
     // them, and their round trip overlaps the staging and the gates
     const int nb = w == 2 ? 2 : 1;                  // row blocks of waves 0-2
@@ -140,7 +157,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         for (int b = 0; b < 2; ++b) {
             if (b >= nb) break;   // uniform
             const int ta = 16 * (mb0 - b) + li;
-            const CoT* qr = qrow(ta);
+            const CoT* qr = co + (size_t)(t0 + min(ta, L - 1)) * cts + kh * SD;
             const float qm = ta < L ? 1.f : 0.f;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
@@ -150,7 +167,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             }
         }
     }
-    if (w == 7) {   // a wave without q loads in flight
+    if (w == 7) {
         float gg = 0.f, b = 0.f;
         if (l < L) {
             b = sigmoidf_(braw);
@@ -166,6 +183,23 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     }
     __syncthreads();
 
+    // k rows as f16 (the hi parts, zero past the prompt) for an f32 conv output, and the chunk's
+    // decay table: G, e^G, e^{G_last - G} and e^{G_last} (64 copies, one per lane of a load)
+    if constexpr (!F16) {
+#pragma unroll
+        for (int it = 0; it < C * SD / 8 / PREP_THREADS; ++it) {
+            const int idx = tid + it * PREP_THREADS;
+            ((u4*)(rec + OFF_K))[idx] = *(const u4*)&Kx[0][idx >> 4][8 * (idx & 15)];
+        }
+    }
+    if (tid < C) {
+        const float gt = sG[tid], glast = sG[C - 1];
+        float* T = (float*)(rec + OFF_T);
+        T[tid] = gt;
+        T[C + tid] = exp_hw(gt);
+        T[2 * C + tid] = exp_hw(fminf(glast - gt, 0.f));
+        T[3 * C + tid] = exp_hw(glast);
+    }
     // ---- lower 16x16 tiles of K K^T and Q K^T, hi+lo products. The Q K^T tiles are grouped by
     // their 16-row block, whose q rows (read from global, split in registers) serve every tile of
     // the block: wave 0 takes row block 3 (4 tiles), wave 1 row block 2 (3), wave 2 row blocks 1
@@ -189,15 +223,6 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             h8 ah[4], al[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) split_hi_lo(qv[b][2 * ks], qv[b][2 * ks + 1], ah[ks], al[ks]);
-            // e^G q of these rows (token-major f16) straight from the registers
-            {
-                const int t = 16 * mt + li;
-                const float e = t < L ? exp_hw(sG[t]) : 0.f;
-                u4* QG = (u4*)(rec + OFF_QG);
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks)
-                    QG[t * (SD / 8) + 4 * ks + g] = __builtin_bit_cast(u4, to_h8(qv[b][2 * ks] * e, qv[b][2 * ks + 1] * e));
-            }
             for (int nt_ = 0; nt_ <= mt; ++nt_) {
                 f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -238,27 +263,11 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     }
     // upper tiles of the Q K^T block are zero (16-byte stores)
     {
-        u4* aqk = (u4*)(rec + OFF_AQK);
+        u4* aq = (u4*)(rec + OFF_AQK);
         for (int idx = tid; idx < C * C / 8; idx += PREP_THREADS) {
             const int t = idx >> 3, s8 = 8 * (idx & 7);
-            if ((s8 >> 4) > (t >> 4)) aqk[idx] = u4{0u, 0u, 0u, 0u};
+            if ((s8 >> 4) > (t >> 4)) aq[idx] = u4{0u, 0u, 0u, 0u};
         }
-    }
-    // ---- e^{G_last - G} k (dim-major), 8 halves per store (e^G q went out with the Q K^T tiles)
-    {
-        u4* KT = (u4*)(rec + OFF_KT);
-        const float glast = sG[C - 1];
-        for (int idx = tid; idx < C * SD / 8; idx += PREP_THREADS) {
-            const int d = idx >> 3, t8 = 8 * (idx & 7);
-            h8 r;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int t = t8 + j;
-                r[j] = (_Float16)(exp_hw(fminf(glast - sG[t], 0.f)) * ((float)Kx[0][t][d] + (float)Kx[1][t][d]));
-            }
-            KT[idx] = __builtin_bit_cast(u4, r);
-        }
-        if (tid < 4) ((float*)(rec + OFF_GC))[tid] = exp_hw(glast);   // 4 copies: read per lane
     }
     __syncthreads();   // A' complete
     // ---- (I + A') [W | U] = diag(beta) [e^G K | V], blocked by 16 rows:
@@ -358,38 +367,42 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 typedef __attribute__((address_space(3))) void lds_void;
 
 // One chunk's operands for one column block, staged in LDS by the direct global->LDS path. Rows
-// are XOR-swizzled by 16-byte chunk so the operand reads of 16 consecutive rows hit distinct banks:
-// 256-byte rows (W, e^G Q) by row & 15, 128-byte rows (K^T, Q K^T) by (row >> 1) & 7 (two rows
-// share a 256-byte bank window). U holds only this block's CW columns; GC the 4 copies of
-// e^{G_last} (lane l of its 4-byte load reads copy l & 3).
+// are XOR-swizzled by 16-byte chunk so the operand reads hit distinct banks: W and q rows by
+// row & 15, the 128-byte Q K^T rows by (row >> 1) & 7 (two rows share a 256-byte bank window), k
+// rows by kswz (even, see below). U holds only this block's CW columns; T the chunk's decay table
+// (G, e^G, e^{G_last - G}, e^{G_last} x64).
 struct ScanStage {
     _Float16 W[C * SD];      // [token][dim]
-    _Float16 QG[C * SD];     // [token][dim]
-    _Float16 KT[SD * C];     // [dim][token]
+    _Float16 Q[C * SD];      // [token][dim]
+    _Float16 K[C * SD];      // [token][dim]
     _Float16 AQK[C * C];     // [token][token]
     float U[C * CW];         // [token][column]
-    float GC[64];
+    float T[4 * C];
 };
 __device__ __forceinline__ int swz256(int r) { return r & 15; }
 __device__ __forceinline__ int swz128(int r) { return (r >> 1) & 7; }
+// Even, so 16-byte chunks 2m and 2m+1 stay adjacent and in order (a transpose read takes 32
+// aligned bytes per 4 lanes). The 16 rows of one transpose read (8g + 0..3, or 8g + 4..7, for
+// g = 0..3, plus a multiple of 32) take each of the 8 values twice, as do 16 consecutive rows.
+__device__ __forceinline__ int kswz(int r) { return 2 * ((r & 3) | (((r >> 3) & 1) << 2)); }
 
-// Issue loads of chunk record `rec` into stage B as the share `part` (0-3) of the loader waves:
-// instructions of 64 lanes x 16 bytes, per wave W 4, e^G Q 4, K^T 4, Q K^T 2, U CW/16 (+1 for GC
-// on part 0); lane l lands at byte 16*l of its instruction's 1 KB.
-__device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, ScanStage& B, int n0, int part, int l) {
+// Issue loads of one chunk into stage B as the share `part` (0-3) of the loader waves: W from the
+// record `rec`, q and k rows from `qb` (row r at qb + min(r, L-1) * pitch, its k row koff halves
+// further), the Q K^T block, this block's U columns and (part 0) the decay table. Instructions of
+// 64 lanes x 16 bytes, per wave W 4, q 4, k 4, Q K^T 2, U CW/16 (+1); lane l lands at byte 16*l of
+// its instruction's 1 KB.
+__device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, const _Float16* __restrict__ qb, int pitch,
+                                                 int koff, int L, ScanStage& B, int n0, int part, int l) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {   // W and e^G Q: 4 rows of 256 B per instruction
-        const int i = 4 * part + k, r = 4 * i + (l >> 4), j = (l & 15) ^ swz256(r);
-        __builtin_amdgcn_global_load_lds(rec + OFF_W + r * SD * 2 + 16 * j, (lds_void*)(B.W + 4 * i * SD), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(rec + OFF_QG + r * SD * 2 + 16 * j, (lds_void*)(B.QG + 4 * i * SD), 16, 0, 0);
+    for (int k = 0; k < 4; ++k) {   // 4 rows of 256 B per instruction
+        const int i = 4 * part + k, r = 4 * i + (l >> 4), j = l & 15;
+        const _Float16* qr = qb + (size_t)min(r, L - 1) * pitch;
+        __builtin_amdgcn_global_load_lds(rec + OFF_W + r * SD * 2 + 16 * (j ^ swz256(r)), (lds_void*)(B.W + 4 * i * SD), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(qr + 8 * (j ^ swz256(r))), (lds_void*)(B.Q + 4 * i * SD), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(qr + koff + 8 * (j ^ kswz(r))), (lds_void*)(B.K + 4 * i * SD), 16, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {   // K^T: 8 rows of 128 B per instruction
-        const int i = 4 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
-        __builtin_amdgcn_global_load_lds(rec + OFF_KT + r * C * 2 + 16 * j, (lds_void*)(B.KT + 8 * i * C), 16, 0, 0);
-    }
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {   // Q K^T: 8 rows of 128 B
+    for (int k = 0; k < 2; ++k) {   // Q K^T: 8 rows of 128 B per instruction
         const int i = 2 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
         __builtin_amdgcn_global_load_lds(rec + OFF_AQK + r * C * 2 + 16 * j, (lds_void*)(B.AQK + 8 * i * C), 16, 0, 0);
     }
@@ -399,19 +412,23 @@ __device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, S
         const int i = (CW / 16) * part + k, r = (64 / UL) * i + l / UL;
         __builtin_amdgcn_global_load_lds(rec + OFF_U + (r * SD + n0) * 4 + 16 * (l % UL), (lds_void*)(B.U + (64 / UL) * i * CW), 16, 0, 0);
     }
-    if (part == 0) __builtin_amdgcn_global_load_lds(rec + OFF_GC + 4 * (l & 3), (lds_void*)B.GC, 4, 0, 0);
+    if (part == 0) __builtin_amdgcn_global_load_lds(rec + OFF_T + 16 * l, (lds_void*)B.T, 16, 0, 0);
 }
 
 // Scan workgroup: 8 compute waves + 4 loader waves. The dependency chain per chunk is
 // V' = U - W S0 and S1 = e^{G_last} S0 + K~^T V'; the output O = e^G Q S0 + Aqk V' hangs off it.
 // Waves 0-3 ("chain") run the chain for chunk c while waves 4-7 ("output") compute O of chunk c-1
-// from the previous chunk's S0 and V' (both double buffered in LDS). Waves 8-11 ("loaders") stage
-// chunk c+1's operands into the other LDS stage and touch chunk c+3's record lines so that the
-// staging hits L2; only they ever wait for global loads, so no compute wave stalls on load issue.
+// from the previous chunk's S0 and V' (both double buffered in LDS). Waves 8-11 ("loaders") stage chunk c+1's operands into the
+// other LDS stage and touch chunk c+3's lines so that the staging hits L2; only they ever wait
+// for global loads, so no compute wave stalls on load issue.
+// DIRECT: q and k rows come from the f16 conv output co (token stride cts), else from the record.
 constexpr int SCAN_THREADS = 768;
 
-__global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __restrict__ scr, int nch, float* __restrict__ state,
-                                                      float* __restrict__ out, int ots, int nt, int nv) {
+template <bool DIRECT>
+__global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __restrict__ scr, const _Float16* __restrict__ co,
+                                                      int cts, int nch, float* __restrict__ state, float* __restrict__ out,
+                                                      int ots, int nt, int nv, int nk) {
+    constexpr size_t REC = rec_bytes<DIRECT>();
     constexpr int SP = SD + 8, VP = C + 8;
     __shared__ __align__(16) ScanStage B0;
     __shared__ __align__(16) ScanStage B1;
@@ -421,34 +438,51 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
 
     // XCD-aware placement: workgroups are dealt to the 8 XCDs round-robin by linear id, so id L
     // runs on XCD L % 8. All column blocks of one head go to the same XCD (head = xcd + 8*(slot/NCB))
-    // and re-read that head's chunk records from the XCD's L2 instead of HBM.
+    // and re-read that head's chunk records from the XCD's L2 instead of HBM; with nk a multiple of
+    // 8, the V heads that share a q/k head (h % nk) are on one XCD too.
     const int L_id = blockIdx.x, xcd = L_id & 7, slot = L_id >> 3;
     const int h = xcd + 8 * (slot / NCB), cb = slot % NCB;
     if (h >= nv) return;
-    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, g = l >> 4, li = l & 15;
     const int n0 = CW * cb;
     const char* hrec = scr + (size_t)h * nch * REC;
+    const int kh = h % nk;
+    // chunk cc's q rows: row r at qbase(cc) + min(r, rows(cc) - 1) * pitch, its k row koff further
+    auto qbase = [&](int cc) -> const _Float16* {
+        if constexpr (DIRECT) return co + (size_t)cc * C * cts + kh * SD;
+        else return (const _Float16*)(hrec + (size_t)cc * REC + OFF_Q);
+    };
+    const int pitch = DIRECT ? cts : SD, koff = DIRECT ? nk * SD : C * SD;
+    auto rows = [&](int cc) { return DIRECT ? min(C, nt - cc * C) : C; };
 
     // Barrier schedule: step c (0 <= c <= nch) holds barriers A_c and B_c. The chain writes S0T[c&1]
     // before A_c, reads stage c&1 and writes VpT[c&1] between A_c and B_c, reads stage c&1 again
-    // after B_c. The output waves read S0T/VpT[(c-1)&1] and stage c&1 between A_c and B_c. The
-    // loaders fill stage (c+1)&1 after A_c and have it landed before A_{c+1}. Step nch only
-    // finishes the last chunk's output.
+    // after B_c. The output waves read S0T/VpT[(c-1)&1] between A_c and B_c and stage c&1 after
+    // B_c. The loaders fill stage (c+1)&1 after A_c and have it landed before A_{c+1}. Step nch
+    // only finishes the last chunk's output.
     if (wv >= 8) {
         const int part = wv - 8;
-        constexpr int LINES = (int)(REC / 128);
-        // this block's share of the 128-byte lines of chunk cc's record: 32 lines per loader wave
+        constexpr int RL = (int)(REC / 128);   // 128-byte lines of a record
+        // this block's share of chunk cc's 128-byte lines, 32 per loader wave (1024 per head):
+        // the record's, then (DIRECT) those of the q and k rows, 2 per row
         auto touch = [&](int cc) {
-            const int line = min(cb * 128 + part * 32 + (l & 31), LINES - 1);
-            __builtin_amdgcn_global_load_lds(hrec + (size_t)min(cc, nch - 1) * REC + 128 * line, (lds_void*)PfSink, 4, 0, 0);
+            cc = min(cc, nch - 1);
+            const int u = cb * 128 + part * 32 + (l & 31);
+            const char* p = hrec + (size_t)cc * REC + 128 * min(u, RL - 1);
+            if (DIRECT && u >= RL) {
+                const int v = min(u - RL, 255), r = (v >> 1) & 63;
+                p = (const char*)(qbase(cc) + (size_t)min(r, rows(cc) - 1) * pitch + (v >= 128 ? koff : 0)) + 128 * (v & 1);
+            }
+            __builtin_amdgcn_global_load_lds((const void*)p, (lds_void*)PfSink, 4, 0, 0);
         };
-        scan_stage_loads(hrec, B0, n0, part, l);
+        scan_stage_loads(hrec, qbase(0), pitch, koff, rows(0), B0, n0, part, l);
         touch(1);
         touch(2);
         IT_SCAN_WAIT_VMCNT(2);
         for (int c = 0; c <= nch; ++c) {
             lds_barrier();   // A_c
-            if (c + 1 < nch) scan_stage_loads(hrec + (size_t)(c + 1) * REC, (c & 1) ? B0 : B1, n0, part, l);
+            if (c + 1 < nch)
+                scan_stage_loads(hrec + (size_t)(c + 1) * REC, qbase(c + 1), pitch, koff, rows(c + 1), (c & 1) ? B0 : B1, n0, part, l);
             touch(c + 3);
             lds_barrier();   // B_c
             IT_SCAN_WAIT_VMCNT(1);   // stage (c+1)&1 landed; the newest touch may still be in flight
@@ -467,6 +501,17 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
 #pragma unroll
                 for (int i = 0; i < 4; ++i) st[mi][ni][i] = sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li];
         const int rw = 16 * w + li;
+        // K^T operand by transpose reads: source lane li addresses k row 8g + li/4 (+ 32ks, + 4),
+        // dims 16(2w+mi) + 4(li & 3) + 0..3; lane li receives dim 16(2w+mi) + li of 4 tokens
+        int ktoff[2];
+        {
+            const int r = 8 * g + (li >> 2);   // kswz(r + 32ks + 4) == kswz(r)
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                const int lj = 2 * (2 * w + mi) + ((li >> 1) & 1);
+                ktoff[mi] = r * SD + 8 * (lj ^ kswz(r)) + 4 * (li & 1);
+            }
+        }
         for (int c = 0; c < nch; ++c) {
             const int b = c & 1;
             const ScanStage& B = b ? B1 : B0;
@@ -508,24 +553,27 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
                     VpT[b][1][col][t] = lo;
                 }
             lds_barrier();   // B_c
-            // ---- S1 = e^{G_last} S0 + Ktilde^T V' (K^T rows 16(2w+mi)+li, tokens 32ks+8g..)
-            const float gc = B.GC[0];
+            // ---- S1 = e^{G_last} S0 + (diag(e^{G_last - G}) K)^T V': the K^T operand (dims
+            // 16(2w+mi) + li, tokens 32ks + 8g + 0..7) is two transpose reads, scaled per token
+            const float gc = B.T[3 * C];
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni) st[mi][ni] *= gc;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
+            for (int ks = 0; ks < 2; ++ks) {
+                const h8 dk = to_h8(*(const f4*)&B.T[2 * C + 32 * ks + 8 * g], *(const f4*)&B.T[2 * C + 32 * ks + 8 * g + 4]);
 #pragma unroll
                 for (int mi = 0; mi < 2; ++mi) {
-                    const int rk = 16 * (2 * w + mi) + li;
-                    const h8 a = ld_h8(B.KT + rk * C + 8 * ((4 * ks + g) ^ swz128(rk)));
+                    const _Float16* kp = B.K + ktoff[mi] + 32 * ks * SD;
+                    const h8 a = cat_h4(lds_tr4(kp), lds_tr4(kp + 4 * SD)) * dk;
 #pragma unroll
                     for (int ni = 0; ni < NI; ++ni) {
                         st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[b][0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
                         st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[b][1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
                     }
                 }
+            }
         }
         lds_barrier();   // A_nch
         lds_barrier();   // B_nch
@@ -538,10 +586,12 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
         return;
     }
     // ---- output waves: O of chunk c-1 in step c, for tokens 16w..16w+15; the A operands of chunk
-    // c (e^G Q and Q K^T rows) are copied from stage c&1 into registers in step c, used in step c+1
+    // c (q and Q K^T rows) and e^G of the output rows are copied from stage c&1 into registers in
+    // step c, used in step c+1
     const float rs = 1.0f / sqrtf((float)SD);
     const int rw = 16 * w + li;
     h8 qg[4], aqk[2];
+    f4 eg = {0.f, 0.f, 0.f, 0.f};
     for (int c = 0; c <= nch; ++c) {
         lds_barrier();   // A_c
         const int b = c & 1, pb = b ^ 1;
@@ -557,6 +607,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
                     oa[ni] = mfma16x16x32(qg[ks], ld_h8(&S0T[pb][1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
                 }
 #pragma unroll
+            for (int ni = 0; ni < NI; ++ni) oa[ni] *= eg;   // e^{G_t} of rows 16w + 4g + i
+#pragma unroll
             for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni) {
@@ -567,9 +619,10 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
         if (c < nch) {
             const ScanStage& B = b ? B1 : B0;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) qg[ks] = ld_h8(B.QG + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
+            for (int ks = 0; ks < 4; ++ks) qg[ks] = ld_h8(B.Q + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) aqk[ks] = ld_h8(B.AQK + rw * C + 8 * ((4 * ks + g) ^ swz128(rw)));
+            eg = *(const f4*)&B.T[C + 16 * w + 4 * g];
         }
         lds_barrier();   // B_c
         if (c > 0) {
@@ -600,12 +653,16 @@ template <typename CoT>
 hipError_t launch_gdn_chunked(const CoT* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
                               hipStream_t st) {
+    constexpr bool DIRECT = sizeof(CoT) == 2;
     const int nch = (nt + C - 1) / C;
     gdn_chunk_prep<<<dim3(nch * nv), PREP_THREADS, 0, st>>>(co, cts, br, ar, bts, dt, a, nt, nv, nk, (char*)scratch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const _Float16* co16 = nullptr;
+    if constexpr (DIRECT) co16 = co;
     // linear grid of 8 * NCB * ceil(nv / 8) workgroups, mapped to (head, column block) in-kernel
-    gdn_chunk_scan<<<dim3(8 * NCB * ((nv + 7) / 8)), SCAN_THREADS, 0, st>>>((const char*)scratch, nch, state, out, ots, nt, nv);
+    gdn_chunk_scan<DIRECT><<<dim3(8 * NCB * ((nv + 7) / 8)), SCAN_THREADS, 0, st>>>((const char*)scratch, co16, cts, nch, state,
+                                                                                    out, ots, nt, nv, nk);
     return hipGetLastError();
 }
 template hipError_t launch_gdn_chunked<float>(const float*, int, const float*, const float*, int, const float*,

@@ -70,7 +70,7 @@ hipError_t launch_gdn_step_head(const float* co, int cts, const float* br, const
                                 hipStream_t st);
 hipError_t launch_gdn_gated_norm(const float* o, int ots, const float* z, int zts, const float* w, float eps,
                                  float* out, int outs, int nv, int nt, hipStream_t st);
-size_t gdn_chunked_scratch_bytes(int nt, int nv, int S);
+size_t gdn_chunked_scratch_bytes(int nt, int nv, int S, bool f16_conv);
 // CoT float (it_gdn_chunked) or _Float16 (the conv output of the one-call GDN prefill)
 template <typename CoT>
 hipError_t launch_gdn_chunked(const CoT* co, int cts, const float* br, const float* ar, int bts, const float* dt,
