@@ -2,25 +2,24 @@
 // runs the recurrence token by token, kernels/src/lib.rs:285-331, cpu.rs:216-232). Per V head h
 // and chunk of L <= 64 tokens with in-chunk cumulative log-decay G (G_t = g_0 + ... + g_t) and
 // D[t,s] = exp(G_t - G_s), starting from the state S0 (key x value):
-//   A'  = strict_lower(diag(beta) (D * K K^T))        (I + A') [W | U] = diag(beta) [e^G K | V]
-//   V'  = U - W S0
-//   O   = (diag(e^G) Q S0 + lower_incl(D * Q K^T) V') / sqrt(128)
-//   S1  = e^{G_last} S0 + (diag(e^{G_last - G}) K)^T V'
+//   A'  = strict_lower(diag(beta) (D * K K^T))        M = (I + A')^-1 diag(beta)
+//   Y   = V - diag(e^G) K S0                            (V' = M Y is the chunk's corrected values)
+//   O   = (diag(e^G) Q S0 + P Y) / sqrt(128)            P  = lower_incl(D * Q K^T) M
+//   S1  = e^{G_last} S0 + Kh^T Y                        Kh = M^T diag(e^{G_last - G}) K
 // which is the token-sequential recurrence S <- e^g S + beta k (v - e^g S^T k)^T regrouped; only
 // decay differences G_t - G_s <= 0 (t >= s) are exponentiated, so nothing overflows.
 //
-// Kernel 1 (gdn_chunk_prep, one workgroup per (chunk, V head), all chunks in parallel) produces
-// everything that does not depend on S0 and is not a row of q or k: W (f16), U (f32), the masked
-// Q K^T block (f16) and a table of the chunk's decays (G, e^G, e^{G_last - G}, e^{G_last}).
-// K K^T / Q K^T are f16 MFMA products of hi+lo splits (three products, ~f32 accurate); the solve
-// is blocked by 16 rows: small substitutions for the diagonal blocks, MFMA hi+lo products for the
-// rest. From an f32 conv output it also writes the chunk's q and k rows as f16; an f16 conv
-// output is read in place by kernel 2.
+// Kernel 1 (gdn_chunk_prep, one workgroup per (chunk, V head), all chunks in parallel) produces the
+// two matrices that carry M: Kh (stored transposed, f16) and P (f16), plus the chunk's decay table
+// (G, e^G, e^{G_last - G}, e^{G_last}). K K^T / Q K^T are f16 MFMA products of hi+lo splits (three
+// products, ~f32 accurate); Kh and P^T solve (I + A')^T [Z1 | Z2] = [diag(e^{G_last-G}) K | (D *
+// Q K^T)^T] by blocked backward substitution (16x16 diagonal inverses, MFMA hi+lo products), then
+// scale rows by beta. From an f32 conv output it also writes the chunk's q and k rows as f16.
 // Kernel 2 (gdn_chunk_scan, one workgroup per (16-column block of the state, V head)) walks the
-// chunks in order with its 128x16 slice of S in MFMA accumulators; S0 and V' enter the products
-// as f16 hi+lo pairs through LDS, so the state path keeps f32 accuracy. It takes e^G Q S0 as
-// (Q S0) scaled per row, and the decayed K^T as the k rows read transposed from LDS and scaled
-// per token, so neither is kept in the records.
+// chunks in order with its 128x16 slice of S in MFMA accumulators; S0 and Y enter the products as
+// f16 hi+lo pairs through LDS, so the state path keeps f32 accuracy. It reads q, k and its V
+// columns from the conv output in place (q and k from the record for an f32 conv output), so a
+// record holds 25 KiB per chunk and V head (57 KiB with the f16 q and k rows).
 #include "common.h"
 #include "internal.h"
 
@@ -30,13 +29,12 @@ namespace {
 constexpr int C = 64;      // chunk length
 constexpr int SD = 128;    // state size (d_k = d_v)
 // per-(V head, chunk) record in scratch, byte offsets
-constexpr size_t OFF_W = 0;                        // f16 [C][SD]   W (token-major)
-constexpr size_t OFF_U = OFF_W + C * SD * 2;        // f32 [C][SD]   U
-constexpr size_t OFF_T = OFF_U + C * SD * 4;        // f32 [4][C]    G, e^G, e^{G_last - G}, e^{G_last} (x64)
-constexpr size_t OFF_AQK = OFF_T + 4 * C * 4;       // f16 [C][C]    lower_incl(D * Q K^T)
-constexpr size_t OFF_Q = OFF_AQK + C * C * 2;       // f16 [C][SD]   q rows (f32 conv output only)
+constexpr size_t OFF_KH = 0;                       // f16 [SD][C]   Kh^T (dim-major)
+constexpr size_t OFF_P = OFF_KH + SD * C * 2;       // f16 [C][C]    P
+constexpr size_t OFF_T = OFF_P + C * C * 2;         // f32 [4][C]    G, e^G, e^{G_last - G}, e^{G_last} (x64)
+constexpr size_t OFF_Q = OFF_T + 4 * C * 4;         // f16 [C][SD]   q rows (f32 conv output only)
 constexpr size_t OFF_K = OFF_Q + C * SD * 2;        // f16 [C][SD]   k rows (f32 conv output only)
-constexpr size_t REC_DIRECT = OFF_Q;                // the scan reads an f16 conv output in place
+constexpr size_t REC_DIRECT = OFF_Q;                // the scan reads an f16 conv output's q and k in place
 constexpr size_t REC_ROWS = OFF_K + C * SD * 2;
 static_assert(REC_DIRECT % 256 == 0 && REC_ROWS % 256 == 0, "records stay 256-byte aligned");
 template <bool DIRECT> constexpr size_t rec_bytes() { return DIRECT ? REC_DIRECT : REC_ROWS; }
@@ -63,12 +61,13 @@ __device__ __forceinline__ void split_hi_lo4(f4 x, h4& hi, h4& lo) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// 8 waves, 60 KB of LDS (two workgroups per CU, so one's loads overlap the other's products): the
-// K rows as f16 hi/lo pairs (the V rows pass through the same tile once K is dead), A' and the
-// diagonal-block inverses. Q never enters LDS: the Q K^T operands and e^G q are read from global
-// (the chunk's q rows stay in L2). The triangular solve runs in registers.
+// 8 waves, 74 KB of LDS (two workgroups per CU, so one's loads overlap the other's products): the
+// K rows as f16 hi/lo pairs, A'^T, the masked Q K^T block and the transposed diagonal-block
+// inverses. Q never enters LDS: the Q K^T operands are read from global (the chunk's q rows stay
+// in L2). The triangular solve runs in registers.
 constexpr int PREP_THREADS = 512;
 constexpr int KP = SD + 8;     // f16 row pitch of the K tile (272 B: 16 rows at one column hit distinct bank groups)
+constexpr int NSOL = (SD + C) / 16;   // 16-column blocks of the solve: 8 of Kh, 4 of P^T
 
 // Workgroup id -> (chunk c, V head h) of the prep grid, launched 1-D. The nv / nk V heads that
 // share a QK head read the same q and k rows; they get ids 8 apart (one XCD, under the
@@ -93,14 +92,14 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
                                                                int bts, const float* __restrict__ dt,
                                                                const float* __restrict__ A, int nt, int nv, int nk,
                                                                char* __restrict__ scr) {
-    __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows hi / lo, then the V rows (f32)
-    __shared__ __align__(16) float Ap[C][C + 4];
+    __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows hi / lo
+    __shared__ __align__(16) float ApT[C][C + 4];            // ApT[s][t] = A'[t][s] (tiles at and below the diagonal)
+    __shared__ __align__(16) float Aq[C][C + 4];             // lower_incl(D * Q K^T) [t][s]
     __shared__ float sG[C], sB[C];
-    __shared__ __align__(16) float Td[4][16][20];            // inverses of the 16x16 diagonal blocks
-    static_assert(2 * C * KP * 2 >= C * SD * 4, "the V rows fit in the K tile");
+    __shared__ __align__(16) float TdT[4][16][20];           // TdT[i][c][r] = (I + A'_ii)^-1 [r][c]
 
-    // an f16 conv output is exact in f16, so its hi/lo splits have lo == 0 and the K K^T product
-    // needs only the hi x hi term (bit-identical to the three-term form)
+    // an f16 conv output is exact in f16, so its hi/lo splits have lo == 0 and the K K^T / Q K^T
+    // products need only the hi x hi term (bit-identical to the three-term form)
     constexpr bool F16 = sizeof(CoT) == 2;
     const int nch = (nt + C - 1) / C;
     int c, h;
@@ -109,7 +108,6 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     const int kh = h % nk, qk = nk * SD;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, li = l & 15;
     char* rec = scr + ((size_t)h * nch + c) * rec_bytes<F16>();
-    const int col = 16 * w + li;                 // this lane's column of the solve
 
     // the gate inputs go out first (wave 7 computes beta and the cumulative log-decay below)
     float braw = 0.f, araw = 0.f;
@@ -204,17 +202,8 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     // their 16-row block, whose q rows (read from global, split in registers) serve every tile of
     // the block: wave 0 takes row block 3 (4 tiles), wave 1 row block 2 (3), wave 2 row blocks 1
     // and 0 (3, both blocks' rows loaded together), so each pays one memory round trip. Waves 3-7
-    // take the 10 K K^T tiles, two each.
-    _Float16* aqk = (_Float16*)(rec + OFF_AQK);
-    auto store_tile = [&](bool isq, int mt, int nt_, f4 acc) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = 16 * mt + 4 * g + i, s = 16 * nt_ + li;
-            const float d = exp_hw(fminf(sG[t] - sG[s], 0.f));
-            if (!isq) Ap[t][s] = s < t ? sB[t] * d * acc[i] : 0.f;
-            else aqk[t * C + s] = (_Float16)(s <= t ? d * acc[i] : 0.f);
-        }
-    };
+    // take the 10 K K^T tiles, two each. A K K^T tile goes to A'^T as four consecutive floats a
+    // lane (its rows t = 16mt + 4g + 0..3 at column s).
     if (w < 3) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
@@ -236,7 +225,11 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
                         acc = mfma16x16x32(al[ks], bh, acc);
                     }
                 }
-                store_tile(true, mt, nt_, acc);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * mt + 4 * g + i, s = 16 * nt_ + li;
+                    Aq[t][s] = s <= t ? exp_hw(fminf(sG[t] - sG[s], 0.f)) * acc[i] : 0.f;
+                }
             }
         }
     } else {
@@ -258,22 +251,29 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
                     acc = mfma16x16x32(al, bh, acc);
                 }
             }
-            store_tile(false, mt, nt_, acc);
+            // acc[i] = (K K^T)[16mt + 4g + i][16nt + li]
+            const int s = 16 * nt_ + li;
+            f4 a;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * mt + 4 * g + i;
+                a[i] = s < t ? sB[t] * exp_hw(fminf(sG[t] - sG[s], 0.f)) * acc[i] : 0.f;
+            }
+            *(f4*)&ApT[s][16 * mt + 4 * g] = a;
         }
     }
-    // upper tiles of the Q K^T block are zero (16-byte stores)
-    {
-        u4* aq = (u4*)(rec + OFF_AQK);
-        for (int idx = tid; idx < C * C / 8; idx += PREP_THREADS) {
-            const int t = idx >> 3, s8 = 8 * (idx & 7);
-            if ((s8 >> 4) > (t >> 4)) aq[idx] = u4{0u, 0u, 0u, 0u};
-        }
+    // upper tiles of the Q K^T block are zero
+    for (int idx = tid; idx < C * C / 4; idx += PREP_THREADS) {
+        const int t = idx >> 4, s4 = 4 * (idx & 15);
+        if ((s4 >> 4) > (t >> 4)) *(f4*)&Aq[t][s4] = f4{0.f, 0.f, 0.f, 0.f};
     }
-    __syncthreads();   // A' complete
-    // ---- (I + A') [W | U] = diag(beta) [e^G K | V], blocked by 16 rows:
-    //   T_i = (I + A'_ii)^-1 (16x16, one wave, forward substitution per column)
-    //   X_i = T_i (diag(beta) B_i - sum_{k<i} A'_ik X_k)          (MFMA, hi+lo products)
-    // W and U are solved one after the other (128 columns each, one 16-column block per wave).
+    __syncthreads();   // A'^T and the Q K^T block complete
+    // ---- (I + A')^T Z = R with R = [diag(e^{G_last - G}) K | (D * Q K^T)^T] (128 + 64 columns),
+    // blocked by 16 rows from the last block up:
+    //   T_i = (I + A'_ii)^-1 (16x16, one wave, forward substitution per column), kept transposed
+    //   Z_i = T_i^T (R_i - sum_{k>i} A'_ki^T Z_k)          (MFMA, hi+lo products)
+    // then Kh^T[d][t] = beta_t Z[t][d] and P[t'][s] = beta_s Z[s][128 + t']. Column block b of the
+    // 12 goes to wave b % 8 (waves 0-3 take two).
     if (w == 0) {
         const int kb = l >> 4, ci = l & 15;
         float y[16];
@@ -281,76 +281,74 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         for (int r = 0; r < 16; ++r) {
             float acc = r == ci ? 1.0f : 0.0f;
 #pragma unroll
-            for (int q = 0; q < r; ++q) acc -= Ap[16 * kb + r][16 * kb + q] * y[q];
+            for (int q = 0; q < r; ++q) acc -= ApT[16 * kb + q][16 * kb + r] * y[q];
             y[r] = acc;
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) Td[kb][r][ci] = y[r];
+        for (int r = 0; r < 16; r += 4) *(f4*)&TdT[kb][ci][r] = f4{y[r], y[r + 1], y[r + 2], y[r + 3]};
     }
-    // V rows, coalesced (thread: row tid >> 3, 16 columns); they reach their solve lanes through
-    // LDS once the K tile is dead. Rows past the prompt repeat the last row and are zeroed through
-    // beta = 0. (The other workgroup on the CU covers their latency.)
-    f4 vreg[4];
-    {
-        const CoT* src = co + (size_t)(t0 + min(tid >> 3, L - 1)) * cts + 2 * qk + h * SD + 16 * (tid & 7);
-        ld8(src, vreg[0], vreg[1]);
-        ld8(src + 8, vreg[2], vreg[3]);
-    }
-    // right-hand sides of this lane's 16 (row, column) cells: W from the K tile, U from V
+    // right-hand sides of this lane's cells: rows 16i + 4g + e, column li of the wave's blocks
     float rhs[2][4][4];
+    const float glast = sG[C - 1];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int t = 16 * i + 4 * g + e;
-            rhs[0][i][e] = sB[t] * (exp_hw(sG[t]) * ((float)Kx[0][t][col] + (float)Kx[1][t][col]));
-        }
-    __syncthreads();   // the K tile is dead: V passes through it to its solve lanes
-    float* const Vs = (float*)&Kx[0][0][0];   // [C][SD] f32, 32 KB of the 36 KB tile
-#pragma unroll
-    for (int j = 0; j < 4; ++j) *(f4*)(Vs + (tid >> 3) * SD + 16 * (tid & 7) + 4 * j) = vreg[j];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int t = 16 * i + 4 * g + e;
-            rhs[1][i][e] = sB[t] * Vs[t * SD + col];
-        }
-    // Each wave solves its own 16 columns in registers, no LDS and no barrier: the accumulator of a
-    // 16x16x16 MFMA (lane = column li, rows 4g..4g+3) is exactly its B-operand layout (k = 4g..4g+3),
-    // so X_k feeds the next block rows and R_i feeds T_i R_i straight from registers.
-    //   R_i = beta B_i - sum_{k<i} A'_ik X_k,   X_i = T_i R_i   (hi+lo products on both sides)
     for (int hf = 0; hf < 2; ++hf) {
-        f4 X[4];
+        const int b = w + 8 * hf;
+        if (b >= NSOL) break;   // uniform
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            if (b < SD / 16) {
+                const int d = 16 * b + li;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = 16 * i + 4 * g + e;
+                    rhs[hf][i][e] = exp_hw(fminf(glast - sG[t], 0.f)) * ((float)Kx[0][t][d] + (float)Kx[1][t][d]);
+                }
+            } else {
+                const f4 a = *(const f4*)&Aq[16 * (b - SD / 16) + li][16 * i + 4 * g];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rhs[hf][i][e] = a[e];
+            }
+        }
+    }
+    __syncthreads();   // the inverses
+    // Each wave solves its own 16 columns in registers, no LDS and no barrier: the accumulator of a
+    // 16x16x16 MFMA (lane = column li, rows 4g..4g+3) is exactly its B-operand layout (k = 4g..4g+3),
+    // so Z_k feeds the blocks above and R_i feeds T_i^T R_i straight from registers. The A operands
+    // are rows of A'^T and of T^T: lane (li, g) reads 4 consecutive floats of row li.
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        const int b = w + 8 * hf;
+        if (b >= NSOL) break;   // uniform
+        f4 Z[4];
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
             f4 acc = {rhs[hf][i][0], rhs[hf][i][1], rhs[hf][i][2], rhs[hf][i][3]};
 #pragma unroll
-            for (int k = 0; k < i; ++k) {
-                const f4 a = -*(const f4*)&Ap[16 * i + li][16 * k + 4 * g];
-                h4 ah, al, xh, xl;
+            for (int k = i + 1; k < 4; ++k) {
+                // (A'_ki)^T [li][4g + j] = A'[16k + 4g + j][16i + li] = ApT[16i + li][16k + 4g + j]
+                const f4 a = -*(const f4*)&ApT[16 * i + li][16 * k + 4 * g];
+                h4 ah, al, zh, zl;
                 split_hi_lo4(a, ah, al);
-                split_hi_lo4(X[k], xh, xl);
-                acc = mfma16x16x16(ah, xh, acc);
-                acc = mfma16x16x16(ah, xl, acc);
-                acc = mfma16x16x16(al, xh, acc);
+                split_hi_lo4(Z[k], zh, zl);
+                acc = mfma16x16x16(ah, zh, acc);
+                acc = mfma16x16x16(ah, zl, acc);
+                acc = mfma16x16x16(al, zh, acc);
             }
             h4 th, tl, rh, rl;
-            split_hi_lo4(*(const f4*)&Td[i][li][4 * g], th, tl);
+            split_hi_lo4(*(const f4*)&TdT[i][li][4 * g], th, tl);   // T_i^T [li][4g + j]
             split_hi_lo4(acc, rh, rl);
             f4 z = {0.f, 0.f, 0.f, 0.f};
             z = mfma16x16x16(th, rh, z);
             z = mfma16x16x16(th, rl, z);
             z = mfma16x16x16(tl, rh, z);
-            X[i] = z;
-            // X_i -> scratch (W f16 / U f32)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = 16 * i + 4 * g + e;
-                if (hf == 0) ((_Float16*)(rec + OFF_W))[t * SD + col] = (_Float16)z[e];
-                else ((float*)(rec + OFF_U))[t * SD + col] = z[e];
-            }
+            Z[i] = z;
+            // rows s = 16i + 4g + 0..3 of column li, scaled by beta_s: four consecutive halves of
+            // row d of Kh^T, or of row t' of P
+            const int s0 = 16 * i + 4 * g;
+            const h4 v = {(_Float16)(sB[s0] * z[0]), (_Float16)(sB[s0 + 1] * z[1]), (_Float16)(sB[s0 + 2] * z[2]),
+                          (_Float16)(sB[s0 + 3] * z[3])};
+            if (b < SD / 16) *(h4*)(rec + OFF_KH + ((size_t)(16 * b + li) * C + s0) * 2) = v;
+            else *(h4*)(rec + OFF_P + ((size_t)(16 * (b - SD / 16) + li) * C + s0) * 2) = v;
         }
     }
 }
@@ -367,73 +365,79 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 typedef __attribute__((address_space(3))) void lds_void;
 
 // One chunk's operands for one column block, staged in LDS by the direct global->LDS path. Rows
-// are XOR-swizzled by 16-byte chunk so the operand reads hit distinct banks: W and q rows by
-// row & 15, the 128-byte Q K^T rows by (row >> 1) & 7 (two rows share a 256-byte bank window), k
-// rows by kswz (even, see below). U holds only this block's CW columns; T the chunk's decay table
-// (G, e^G, e^{G_last - G}, e^{G_last} x64).
+// are XOR-swizzled by 16-byte chunk so the operand reads of 16 consecutive rows hit distinct
+// banks: 256-byte rows (k, q) by row & 15, 128-byte rows (Kh^T, P) by (row >> 1) & 7 (two rows
+// share a 256-byte bank window). V holds this block's CW columns of the conv output's V rows (f16
+// or f32, as the conv output); T the decay table.
+template <typename CoT>
 struct ScanStage {
-    _Float16 W[C * SD];      // [token][dim]
-    _Float16 Q[C * SD];      // [token][dim]
     _Float16 K[C * SD];      // [token][dim]
-    _Float16 AQK[C * C];     // [token][token]
-    float U[C * CW];         // [token][column]
+    _Float16 Q[C * SD];      // [token][dim]
+    _Float16 KHT[SD * C];    // [dim][token]
+    _Float16 P[C * C];       // [token][token]
+    CoT V[C * CW];           // [token][column]
     float T[4 * C];
 };
 __device__ __forceinline__ int swz256(int r) { return r & 15; }
 __device__ __forceinline__ int swz128(int r) { return (r >> 1) & 7; }
-// Even, so 16-byte chunks 2m and 2m+1 stay adjacent and in order (a transpose read takes 32
-// aligned bytes per 4 lanes). The 16 rows of one transpose read (8g + 0..3, or 8g + 4..7, for
-// g = 0..3, plus a multiple of 32) take each of the 8 values twice, as do 16 consecutive rows.
-__device__ __forceinline__ int kswz(int r) { return 2 * ((r & 3) | (((r >> 3) & 1) << 2)); }
 
-// Issue loads of one chunk into stage B as the share `part` (0-3) of the loader waves: W from the
-// record `rec`, q and k rows from `qb` (row r at qb + min(r, L-1) * pitch, its k row koff halves
-// further), the Q K^T block, this block's U columns and (part 0) the decay table. Instructions of
-// 64 lanes x 16 bytes, per wave W 4, q 4, k 4, Q K^T 2, U CW/16 (+1); lane l lands at byte 16*l of
-// its instruction's 1 KB.
+// Issue loads of one chunk into stage B as the share `part` (0-3) of the loader waves: Kh^T, P and
+// (part 0) the decay table from the record `rec`; q and k rows from `qb` (row r at
+// qb + min(r, L-1) * pitch, its k row koff halves further); V rows from `vb` (row r at
+// vb + min(r, L-1) * cts). Instructions of 64 lanes x 16 bytes, per wave k 4, q 4, Kh^T 4, P 2,
+// V 2 or 4 in all (+1); lane l lands at byte 16*l of its instruction's 1 KB.
+template <typename CoT>
 __device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, const _Float16* __restrict__ qb, int pitch,
-                                                 int koff, int L, ScanStage& B, int n0, int part, int l) {
+                                                 int koff, const CoT* __restrict__ vb, int cts, int L, ScanStage<CoT>& B,
+                                                 int part, int l) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {   // 4 rows of 256 B per instruction
-        const int i = 4 * part + k, r = 4 * i + (l >> 4), j = l & 15;
+    for (int k = 0; k < 4; ++k) {   // k and q: 4 rows of 256 B per instruction
+        const int i = 4 * part + k, r = 4 * i + (l >> 4), j = (l & 15) ^ swz256(r);
         const _Float16* qr = qb + (size_t)min(r, L - 1) * pitch;
-        __builtin_amdgcn_global_load_lds(rec + OFF_W + r * SD * 2 + 16 * (j ^ swz256(r)), (lds_void*)(B.W + 4 * i * SD), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(qr + 8 * (j ^ swz256(r))), (lds_void*)(B.Q + 4 * i * SD), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(qr + koff + 8 * (j ^ kswz(r))), (lds_void*)(B.K + 4 * i * SD), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(qr + koff + 8 * j), (lds_void*)(B.K + 4 * i * SD), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(qr + 8 * j), (lds_void*)(B.Q + 4 * i * SD), 16, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {   // Q K^T: 8 rows of 128 B per instruction
+    for (int k = 0; k < 4; ++k) {   // Kh^T: 8 rows of 128 B per instruction
+        const int i = 4 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
+        __builtin_amdgcn_global_load_lds(rec + OFF_KH + r * C * 2 + 16 * j, (lds_void*)(B.KHT + 8 * i * C), 16, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {   // P: 8 rows of 128 B
         const int i = 2 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
-        __builtin_amdgcn_global_load_lds(rec + OFF_AQK + r * C * 2 + 16 * j, (lds_void*)(B.AQK + 8 * i * C), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(rec + OFF_P + r * C * 2 + 16 * j, (lds_void*)(B.P + 8 * i * C), 16, 0, 0);
     }
-    constexpr int UL = CW / 4;       // 16-byte lanes per U row (CW floats)
-#pragma unroll
-    for (int k = 0; k < CW / 16; ++k) {   // this block's U columns: 64/UL rows per instruction
-        const int i = (CW / 16) * part + k, r = (64 / UL) * i + l / UL;
-        __builtin_amdgcn_global_load_lds(rec + OFF_U + (r * SD + n0) * 4 + 16 * (l % UL), (lds_void*)(B.U + (64 / UL) * i * CW), 16, 0, 0);
+    constexpr int VL = CW * (int)sizeof(CoT) / 16;   // 16-byte lanes per V row
+    constexpr int NVI = C * VL / 64;                  // V instructions in all (2 or 4)
+    for (int i = part; i < NVI; i += 4) {             // uniform
+        const int r = (64 / VL) * i + l / VL;
+        __builtin_amdgcn_global_load_lds((const void*)(vb + (size_t)min(r, L - 1) * cts + 16 / sizeof(CoT) * (l % VL)),
+                                         (lds_void*)(B.V + (64 / VL) * i * CW), 16, 0, 0);
     }
     if (part == 0) __builtin_amdgcn_global_load_lds(rec + OFF_T + 16 * l, (lds_void*)B.T, 16, 0, 0);
 }
 
 // Scan workgroup: 8 compute waves + 4 loader waves. The dependency chain per chunk is
-// V' = U - W S0 and S1 = e^{G_last} S0 + K~^T V'; the output O = e^G Q S0 + Aqk V' hangs off it.
+// Y = V - e^G K S0 and S1 = e^{G_last} S0 + Kh^T Y; the output O = e^G Q S0 + P Y hangs off it.
 // Waves 0-3 ("chain") run the chain for chunk c while waves 4-7 ("output") compute O of chunk c-1
-// from the previous chunk's S0 and V' (both double buffered in LDS). Waves 8-11 ("loaders") stage chunk c+1's operands into the
-// other LDS stage and touch chunk c+3's lines so that the staging hits L2; only they ever wait
-// for global loads, so no compute wave stalls on load issue.
-// DIRECT: q and k rows come from the f16 conv output co (token stride cts), else from the record.
+// from the previous chunk's S0 and Y (both double buffered in LDS). Waves 8-11 ("loaders") stage
+// chunk c+1's operands into the other LDS stage and touch chunk c+3's lines so that the staging
+// hits L2; only they ever wait for global loads, so no compute wave stalls on load issue.
+// An f16 conv output (CoT = _Float16) gives q and k in place; from an f32 one they are the
+// prep's f16 rows in the record. V is read in place either way.
 constexpr int SCAN_THREADS = 768;
 
-template <bool DIRECT>
-__global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __restrict__ scr, const _Float16* __restrict__ co,
+template <typename CoT>
+__global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __restrict__ scr, const CoT* __restrict__ co,
                                                       int cts, int nch, float* __restrict__ state, float* __restrict__ out,
                                                       int ots, int nt, int nv, int nk) {
+    constexpr bool DIRECT = sizeof(CoT) == 2;
     constexpr size_t REC = rec_bytes<DIRECT>();
     constexpr int SP = SD + 8, VP = C + 8;
-    __shared__ __align__(16) ScanStage B0;
-    __shared__ __align__(16) ScanStage B1;
+    __shared__ __align__(16) ScanStage<CoT> B0;
+    __shared__ __align__(16) ScanStage<CoT> B1;
     __shared__ __align__(16) _Float16 S0T[2][2][CW][SP];   // [chunk & 1][hi|lo][state column][key dim]
-    __shared__ __align__(16) _Float16 VpT[2][2][CW][VP];   // [chunk & 1][hi|lo][state column][token]
+    __shared__ __align__(16) _Float16 YT[2][2][CW][VP];    // [chunk & 1][hi|lo][state column][token]
     __shared__ uint32_t PfSink[64];                         // landing words of the L2 touches, never read
 
     // XCD-aware placement: workgroups are dealt to the 8 XCDs round-robin by linear id, so id L
@@ -447,42 +451,51 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
     const int n0 = CW * cb;
     const char* hrec = scr + (size_t)h * nch * REC;
     const int kh = h % nk;
-    // chunk cc's q rows: row r at qbase(cc) + min(r, rows(cc) - 1) * pitch, its k row koff further
+    // chunk cc's q rows: row r at qbase(cc) + min(r, rows(cc) - 1) * pitch, its k row koff further;
+    // its V rows (this block's columns) at vbase(cc) + min(r, rows(cc) - 1) * cts
     auto qbase = [&](int cc) -> const _Float16* {
         if constexpr (DIRECT) return co + (size_t)cc * C * cts + kh * SD;
         else return (const _Float16*)(hrec + (size_t)cc * REC + OFF_Q);
     };
+    auto vbase = [&](int cc) { return co + (size_t)cc * C * cts + 2 * nk * SD + h * SD + n0; };
     const int pitch = DIRECT ? cts : SD, koff = DIRECT ? nk * SD : C * SD;
-    auto rows = [&](int cc) { return DIRECT ? min(C, nt - cc * C) : C; };
+    auto rows = [&](int cc) { return min(C, nt - cc * C); };
+    auto stage_loads = [&](int cc, ScanStage<CoT>& B, int part) {
+        scan_stage_loads<CoT>(hrec + (size_t)cc * REC, qbase(cc), pitch, koff, vbase(cc), cts, rows(cc), B, part, l);
+    };
 
     // Barrier schedule: step c (0 <= c <= nch) holds barriers A_c and B_c. The chain writes S0T[c&1]
-    // before A_c, reads stage c&1 and writes VpT[c&1] between A_c and B_c, reads stage c&1 again
-    // after B_c. The output waves read S0T/VpT[(c-1)&1] between A_c and B_c and stage c&1 after
-    // B_c. The loaders fill stage (c+1)&1 after A_c and have it landed before A_{c+1}. Step nch
-    // only finishes the last chunk's output.
+    // before A_c, reads stage c&1 and writes YT[c&1] between A_c and B_c, reads stage c&1 again
+    // after B_c. The output waves read S0T/YT[(c-1)&1] and stage c&1 between A_c and B_c. The
+    // loaders fill stage (c+1)&1 after A_c and have it landed before A_{c+1}. Step nch only
+    // finishes the last chunk's output.
     if (wv >= 8) {
         const int part = wv - 8;
-        constexpr int RL = (int)(REC / 128);   // 128-byte lines of a record
-        // this block's share of chunk cc's 128-byte lines, 32 per loader wave (1024 per head):
-        // the record's, then (DIRECT) those of the q and k rows, 2 per row
+        constexpr int RL = (int)(REC / 128);                        // 128-byte lines of a record
+        constexpr int QL = DIRECT ? 2 * C * (SD * 2 / 128) : 0;     // lines of the chunk's q and k rows
+        constexpr int VLN = SD * (int)sizeof(CoT) / 128;            // lines of one V row of the head
+        // this block's share of chunk cc's 128-byte lines, 32 per loader wave (1024 per head): the
+        // record's, then (f16 conv output) those of the q and k rows, then those of the V rows
         auto touch = [&](int cc) {
             cc = min(cc, nch - 1);
-            const int u = cb * 128 + part * 32 + (l & 31);
+            const int u = cb * 128 + part * 32 + (l & 31), L = rows(cc);
             const char* p = hrec + (size_t)cc * REC + 128 * min(u, RL - 1);
-            if (DIRECT && u >= RL) {
-                const int v = min(u - RL, 255), r = (v >> 1) & 63;
-                p = (const char*)(qbase(cc) + (size_t)min(r, rows(cc) - 1) * pitch + (v >= 128 ? koff : 0)) + 128 * (v & 1);
+            if (u >= RL && u < RL + QL) {
+                const int v = u - RL, r = (v >> 1) & (C - 1);
+                p = (const char*)(qbase(cc) + (size_t)min(r, L - 1) * pitch + (v >= C * 2 ? koff : 0)) + 128 * (v & 1);
+            } else if (u >= RL + QL) {
+                const int v = min(u - RL - QL, C * VLN - 1), r = v / VLN;
+                p = (const char*)(vbase(cc) - n0 + (size_t)min(r, L - 1) * cts) + 128 * (v % VLN);
             }
             __builtin_amdgcn_global_load_lds((const void*)p, (lds_void*)PfSink, 4, 0, 0);
         };
-        scan_stage_loads(hrec, qbase(0), pitch, koff, rows(0), B0, n0, part, l);
+        stage_loads(0, B0, part);
         touch(1);
         touch(2);
         IT_SCAN_WAIT_VMCNT(2);
         for (int c = 0; c <= nch; ++c) {
             lds_barrier();   // A_c
-            if (c + 1 < nch)
-                scan_stage_loads(hrec + (size_t)(c + 1) * REC, qbase(c + 1), pitch, koff, rows(c + 1), (c & 1) ? B0 : B1, n0, part, l);
+            if (c + 1 < nch) stage_loads(c + 1, (c & 1) ? B0 : B1, part);
             touch(c + 3);
             lds_barrier();   // B_c
             IT_SCAN_WAIT_VMCNT(1);   // stage (c+1)&1 landed; the newest touch may still be in flight
@@ -501,20 +514,9 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
 #pragma unroll
                 for (int i = 0; i < 4; ++i) st[mi][ni][i] = sh[(size_t)(16 * (2 * w + mi) + 4 * g + i) * SD + n0 + 16 * ni + li];
         const int rw = 16 * w + li;
-        // K^T operand by transpose reads: source lane li addresses k row 8g + li/4 (+ 32ks, + 4),
-        // dims 16(2w+mi) + 4(li & 3) + 0..3; lane li receives dim 16(2w+mi) + li of 4 tokens
-        int ktoff[2];
-        {
-            const int r = 8 * g + (li >> 2);   // kswz(r + 32ks + 4) == kswz(r)
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-                const int lj = 2 * (2 * w + mi) + ((li >> 1) & 1);
-                ktoff[mi] = r * SD + 8 * (lj ^ kswz(r)) + 4 * (li & 1);
-            }
-        }
         for (int c = 0; c < nch; ++c) {
             const int b = c & 1;
-            const ScanStage& B = b ? B1 : B0;
+            const ScanStage<CoT>& B = b ? B1 : B0;
             // ---- S0 -> LDS as hi/lo, transposed to [column][key dim]
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
@@ -529,51 +531,49 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
                         S0T[b][1][col][dk] = lo;
                     }
             lds_barrier();   // A_c
-            // ---- V' = U - W S0 for tokens 16w..16w+15 (W row 16w+li, dims 32ks+8g..)
-            f4 vp[NI];
+            // ---- Y = V - e^G (K S0) for tokens 16w..16w+15 (k row 16w+li, dims 32ks+8g..)
+            f4 ks0[NI];
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni) vp[ni] = f4{0.f, 0.f, 0.f, 0.f};
+            for (int ni = 0; ni < NI; ++ni) ks0[ni] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const h8 a = ld_h8(B.W + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
+                const h8 a = ld_h8(B.K + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni) {
-                    vp[ni] = mfma16x16x32(a, ld_h8(&S0T[b][0][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
-                    vp[ni] = mfma16x16x32(a, ld_h8(&S0T[b][1][16 * ni + li][32 * ks + 8 * g]), vp[ni]);
+                    ks0[ni] = mfma16x16x32(a, ld_h8(&S0T[b][0][16 * ni + li][32 * ks + 8 * g]), ks0[ni]);
+                    ks0[ni] = mfma16x16x32(a, ld_h8(&S0T[b][1][16 * ni + li][32 * ks + 8 * g]), ks0[ni]);
                 }
             }
+            const f4 eg = *(const f4*)&B.T[C + 16 * w + 4 * g];
 #pragma unroll
             for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = 16 * w + 4 * g + i, col = 16 * ni + li;
-                    const float v = B.U[t * CW + col] - vp[ni][i];
+                    const float v = (float)B.V[t * CW + col] - eg[i] * ks0[ni][i];
                     const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
-                    VpT[b][0][col][t] = hi;
-                    VpT[b][1][col][t] = lo;
+                    YT[b][0][col][t] = hi;
+                    YT[b][1][col][t] = lo;
                 }
             lds_barrier();   // B_c
-            // ---- S1 = e^{G_last} S0 + (diag(e^{G_last - G}) K)^T V': the K^T operand (dims
-            // 16(2w+mi) + li, tokens 32ks + 8g + 0..7) is two transpose reads, scaled per token
+            // ---- S1 = e^{G_last} S0 + Kh^T Y (Kh^T rows 16(2w+mi)+li, tokens 32ks+8g..)
             const float gc = B.T[3 * C];
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni) st[mi][ni] *= gc;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const h8 dk = to_h8(*(const f4*)&B.T[2 * C + 32 * ks + 8 * g], *(const f4*)&B.T[2 * C + 32 * ks + 8 * g + 4]);
+            for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
                 for (int mi = 0; mi < 2; ++mi) {
-                    const _Float16* kp = B.K + ktoff[mi] + 32 * ks * SD;
-                    const h8 a = cat_h4(lds_tr4(kp), lds_tr4(kp + 4 * SD)) * dk;
+                    const int rk = 16 * (2 * w + mi) + li;
+                    const h8 a = ld_h8(B.KHT + rk * C + 8 * ((4 * ks + g) ^ swz128(rk)));
 #pragma unroll
                     for (int ni = 0; ni < NI; ++ni) {
-                        st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[b][0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
-                        st[mi][ni] = mfma16x16x32(a, ld_h8(&VpT[b][1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
+                        st[mi][ni] = mfma16x16x32(a, ld_h8(&YT[b][0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
+                        st[mi][ni] = mfma16x16x32(a, ld_h8(&YT[b][1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
                     }
                 }
-            }
         }
         lds_barrier();   // A_nch
         lds_barrier();   // B_nch
@@ -586,11 +586,11 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
         return;
     }
     // ---- output waves: O of chunk c-1 in step c, for tokens 16w..16w+15; the A operands of chunk
-    // c (q and Q K^T rows) and e^G of the output rows are copied from stage c&1 into registers in
-    // step c, used in step c+1
+    // c (q and P rows) and e^G of the output rows are copied from stage c&1 into registers in step
+    // c, used in step c+1
     const float rs = 1.0f / sqrtf((float)SD);
     const int rw = 16 * w + li;
-    h8 qg[4], aqk[2];
+    h8 qg[4], pa[2];
     f4 eg = {0.f, 0.f, 0.f, 0.f};
     for (int c = 0; c <= nch; ++c) {
         lds_barrier();   // A_c
@@ -612,16 +612,16 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
             for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni) {
-                    oa[ni] = mfma16x16x32(aqk[ks], ld_h8(&VpT[pb][0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-                    oa[ni] = mfma16x16x32(aqk[ks], ld_h8(&VpT[pb][1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+                    oa[ni] = mfma16x16x32(pa[ks], ld_h8(&YT[pb][0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
+                    oa[ni] = mfma16x16x32(pa[ks], ld_h8(&YT[pb][1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
                 }
         }
         if (c < nch) {
-            const ScanStage& B = b ? B1 : B0;
+            const ScanStage<CoT>& B = b ? B1 : B0;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) qg[ks] = ld_h8(B.Q + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) aqk[ks] = ld_h8(B.AQK + rw * C + 8 * ((4 * ks + g) ^ swz128(rw)));
+            for (int ks = 0; ks < 2; ++ks) pa[ks] = ld_h8(B.P + rw * C + 8 * ((4 * ks + g) ^ swz128(rw)));
             eg = *(const f4*)&B.T[C + 16 * w + 4 * g];
         }
         lds_barrier();   // B_c
@@ -653,16 +653,13 @@ template <typename CoT>
 hipError_t launch_gdn_chunked(const CoT* co, int cts, const float* br, const float* ar, int bts, const float* dt,
                               const float* a, float* state, float* out, int ots, int nt, int nv, int nk, void* scratch,
                               hipStream_t st) {
-    constexpr bool DIRECT = sizeof(CoT) == 2;
     const int nch = (nt + C - 1) / C;
     gdn_chunk_prep<<<dim3(nch * nv), PREP_THREADS, 0, st>>>(co, cts, br, ar, bts, dt, a, nt, nv, nk, (char*)scratch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const _Float16* co16 = nullptr;
-    if constexpr (DIRECT) co16 = co;
     // linear grid of 8 * NCB * ceil(nv / 8) workgroups, mapped to (head, column block) in-kernel
-    gdn_chunk_scan<DIRECT><<<dim3(8 * NCB * ((nv + 7) / 8)), SCAN_THREADS, 0, st>>>((const char*)scratch, co16, cts, nch, state,
-                                                                                    out, ots, nt, nv, nk);
+    gdn_chunk_scan<CoT><<<dim3(8 * NCB * ((nv + 7) / 8)), SCAN_THREADS, 0, st>>>((const char*)scratch, co, cts, nch, state,
+                                                                                 out, ots, nt, nv, nk);
     return hipGetLastError();
 }
 template hipError_t launch_gdn_chunked<float>(const float*, int, const float*, const float*, int, const float*,

@@ -250,15 +250,15 @@ def test_mailbox_host_side():
 def test_gdn_prefill_host_side():
     """it_gdn_prefill: scratch size = f16 conv output (256-byte rounded) + the chunk records, and
     every argument error reported before device work. A record per (64-token chunk, V head) holds
-    W (f16, 16 KiB), U (f32, 32 KiB), the 1 KiB decay table and the masked Q K^T block (f16,
-    8 KiB); from an f32 conv output (it_gdn_chunked) also the chunk's q and k rows as f16
-    (2 x 16 KiB), which it_gdn_prefill's scan reads from its f16 conv output instead."""
+    Kh^T (f16, 16 KiB), P (f16, 8 KiB) and the 1 KiB decay table; from an f32 conv output
+    (it_gdn_chunked) also the chunk's q and k rows as f16 (2 x 16 KiB), which it_gdn_prefill's
+    scan reads from its f16 conv output instead."""
     lib = _lib.lib()
     for nt, nv, nk in [(1, 32, 16), (64, 4, 2), (8192, 32, 16), (77, 8, 8)]:
         co = (nt * (2 * nk + nv) * 128 * 2 + 255) // 256 * 256
         nch = (nt + 63) // 64
-        assert lib.it_gdn_prefill_scratch_bytes(nt, nv, nk, 128) == co + nch * nv * 57 * 1024
-        assert lib.it_gdn_chunked_scratch_bytes(nt, nv, 128) == nch * nv * 89 * 1024
+        assert lib.it_gdn_prefill_scratch_bytes(nt, nv, nk, 128) == co + nch * nv * 25 * 1024
+        assert lib.it_gdn_chunked_scratch_bytes(nt, nv, 128) == nch * nv * 57 * 1024
     assert lib.it_gdn_prefill_scratch_bytes(0, 32, 16, 128) == 0 and lib.it_gdn_prefill_scratch_bytes(8, 32, 16, 64) == 0
     fake = ctypes.c_void_p(1 << 20)
     need = lib.it_gdn_prefill_scratch_bytes(64, 32, 16, 128)
