@@ -61,9 +61,9 @@ __device__ __forceinline__ void split_hi_lo4(f4 x, h4& hi, h4& lo) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// 8 waves, 74 KB of LDS (two workgroups per CU, so one's loads overlap the other's products): the
-// K rows as f16 hi/lo pairs, A'^T, the masked Q K^T block and the transposed diagonal-block
-// inverses. Q never enters LDS: the Q K^T operands are read from global (the chunk's q rows stay
+// 8 waves, 66 KB of LDS (two workgroups per CU, so one's loads overlap the other's products; 48 KB
+// and three from an f16 conv output, whose K rows need no lo plane): the K rows as f16 hi/lo
+// pairs, A'^T, the masked Q K^T block and the transposed diagonal-block inverses. Q never enters LDS: the Q K^T operands are read from global (the chunk's q rows stay
 // in L2). The triangular solve runs in registers.
 constexpr int PREP_THREADS = 512;
 constexpr int KP = SD + 8;     // f16 row pitch of the K tile (272 B: 16 rows at one column hit distinct bank groups)
@@ -87,20 +87,21 @@ __device__ __forceinline__ void prep_wg(int id, int nch, int nv, int nk, int& c,
 }
 
 template <typename CoT>
-__global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void gdn_chunk_prep(const CoT* __restrict__ co, int cts,
+__global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(sizeof(CoT) == 2 ? 6 : 4))) void gdn_chunk_prep(const CoT* __restrict__ co, int cts,
                                                                const float* __restrict__ br, const float* __restrict__ ar,
                                                                int bts, const float* __restrict__ dt,
                                                                const float* __restrict__ A, int nt, int nv, int nk,
                                                                char* __restrict__ scr) {
-    __shared__ __align__(16) _Float16 Kx[2][C][KP];          // K rows hi / lo
+    // an f16 conv output is exact in f16, so its hi/lo splits have lo == 0 and the K K^T / Q K^T
+    // products need only the hi x hi term (bit-identical to the three-term form); the lo plane of
+    // the K tile is then not kept, and the 48 KB of LDS leave room for three workgroups per CU
+    constexpr bool F16 = sizeof(CoT) == 2;
+    __shared__ __align__(16) _Float16 Kx[F16 ? 1 : 2][C][KP];   // K rows hi (/ lo)
     __shared__ __align__(16) float ApT[C][C + 4];            // ApT[s][t] = A'[t][s] (tiles at and below the diagonal)
-    __shared__ __align__(16) float Aq[C][C + 4];             // lower_incl(D * Q K^T) [t][s]
+    __shared__ __align__(16) _Float16 Aq[C][C + 8];          // lower_incl(D * Q K^T) [t][s], f16 as P is stored
     __shared__ float sG[C], sB[C];
     __shared__ __align__(16) float TdT[4][16][20];           // TdT[i][c][r] = (I + A'_ii)^-1 [r][c]
 
-    // an f16 conv output is exact in f16, so its hi/lo splits have lo == 0 and the K K^T / Q K^T
-    // products need only the hi x hi term (bit-identical to the three-term form)
-    constexpr bool F16 = sizeof(CoT) == 2;
     const int nch = (nt + C - 1) / C;
     int c, h;
     prep_wg(blockIdx.x, nch, nv, nk, c, h);
@@ -130,7 +131,8 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         k1 *= m;
         h8 hi, lo;
         split_hi_lo(k0, k1, hi, lo);
-        *(h8*)&Kx[0][t][d8] = hi; *(h8*)&Kx[1][t][d8] = lo;
+        *(h8*)&Kx[0][t][d8] = hi;
+        if constexpr (!F16) *(h8*)&Kx[F16 ? 0 : 1][t][d8] = lo;
     }
     // q rows as f16 into the record (f32 conv output only: the scan reads an f16 one in place);
     // rows past the prompt are zero
@@ -149,19 +151,26 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     // them, and their round trip overlaps the staging and the gates
     const int nb = w == 2 ? 2 : 1;                  // row blocks of waves 0-2
     const int mb0 = w == 0 ? 3 : w == 1 ? 2 : 1;    // first row block; wave 2 then does block 0
-    f4 qv[2][8];
+    // (an f16 conv output's q rows stay f16 in registers: 32 VGPRs for two blocks instead of 64)
+    f4 qv[F16 ? 1 : 2][F16 ? 1 : 8];
+    h8 qh[2][4];
     if (w < 3) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             if (b >= nb) break;   // uniform
             const int ta = 16 * (mb0 - b) + li;
             const CoT* qr = co + (size_t)(t0 + min(ta, L - 1)) * cts + kh * SD;
-            const float qm = ta < L ? 1.f : 0.f;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                ld8(qr + 32 * ks + 8 * g, qv[b][2 * ks], qv[b][2 * ks + 1]);
-                qv[b][2 * ks] *= qm;
-                qv[b][2 * ks + 1] *= qm;
+                if constexpr (F16) {
+                    const h8 v = ld_h8(qr + 32 * ks + 8 * g);
+                    qh[b][ks] = ta < L ? v : h8{};
+                } else {
+                    const float qm = ta < L ? 1.f : 0.f;
+                    ld8(qr + 32 * ks + 8 * g, qv[b][2 * ks], qv[b][2 * ks + 1]);
+                    qv[b][2 * ks] *= qm;
+                    qv[b][2 * ks + 1] *= qm;
+                }
             }
         }
     }
@@ -211,7 +220,10 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
             const int mt = mb0 - b;
             h8 ah[4], al[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) split_hi_lo(qv[b][2 * ks], qv[b][2 * ks + 1], ah[ks], al[ks]);
+            for (int ks = 0; ks < 4; ++ks) {
+                if constexpr (F16) ah[ks] = qh[b][ks];
+                else split_hi_lo(qv[b][2 * ks], qv[b][2 * ks + 1], ah[ks], al[ks]);
+            }
             for (int nt_ = 0; nt_ <= mt; ++nt_) {
                 f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -220,7 +232,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
                     const h8 bh = ld_h8(&Kx[0][16 * nt_ + li][d]);
                     acc = mfma16x16x32(ah[ks], bh, acc);
                     if constexpr (!F16) {
-                        const h8 bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
+                        const h8 bl = ld_h8(&Kx[F16 ? 0 : 1][16 * nt_ + li][d]);
                         acc = mfma16x16x32(ah[ks], bl, acc);
                         acc = mfma16x16x32(al[ks], bh, acc);
                     }
@@ -228,7 +240,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = 16 * mt + 4 * g + i, s = 16 * nt_ + li;
-                    Aq[t][s] = s <= t ? exp_hw(fminf(sG[t] - sG[s], 0.f)) * acc[i] : 0.f;
+                    Aq[t][s] = (_Float16)(s <= t ? exp_hw(fminf(sG[t] - sG[s], 0.f)) * acc[i] : 0.f);
                 }
             }
         }
@@ -246,7 +258,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
                 const h8 ah = ld_h8(&Kx[0][ta][d]), bh = ld_h8(&Kx[0][16 * nt_ + li][d]);
                 acc = mfma16x16x32(ah, bh, acc);
                 if constexpr (!F16) {
-                    const h8 al = ld_h8(&Kx[1][ta][d]), bl = ld_h8(&Kx[1][16 * nt_ + li][d]);
+                    const h8 al = ld_h8(&Kx[F16 ? 0 : 1][ta][d]), bl = ld_h8(&Kx[F16 ? 0 : 1][16 * nt_ + li][d]);
                     acc = mfma16x16x32(ah, bl, acc);
                     acc = mfma16x16x32(al, bh, acc);
                 }
@@ -263,9 +275,9 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
         }
     }
     // upper tiles of the Q K^T block are zero
-    for (int idx = tid; idx < C * C / 4; idx += PREP_THREADS) {
-        const int t = idx >> 4, s4 = 4 * (idx & 15);
-        if ((s4 >> 4) > (t >> 4)) *(f4*)&Aq[t][s4] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int idx = tid; idx < C * C / 8; idx += PREP_THREADS) {
+        const int t = idx >> 3, s8 = 8 * (idx & 7);
+        if ((s8 >> 4) > (t >> 4)) *(u4*)&Aq[t][s8] = u4{0u, 0u, 0u, 0u};
     }
     __syncthreads();   // A'^T and the Q K^T block complete
     // ---- (I + A')^T Z = R with R = [diag(e^{G_last - G}) K | (D * Q K^T)^T] (128 + 64 columns),
@@ -287,29 +299,7 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
 #pragma unroll
         for (int r = 0; r < 16; r += 4) *(f4*)&TdT[kb][ci][r] = f4{y[r], y[r + 1], y[r + 2], y[r + 3]};
     }
-    // right-hand sides of this lane's cells: rows 16i + 4g + e, column li of the wave's blocks
-    float rhs[2][4][4];
     const float glast = sG[C - 1];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-        const int b = w + 8 * hf;
-        if (b >= NSOL) break;   // uniform
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (b < SD / 16) {
-                const int d = 16 * b + li;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int t = 16 * i + 4 * g + e;
-                    rhs[hf][i][e] = exp_hw(fminf(glast - sG[t], 0.f)) * ((float)Kx[0][t][d] + (float)Kx[1][t][d]);
-                }
-            } else {
-                const f4 a = *(const f4*)&Aq[16 * (b - SD / 16) + li][16 * i + 4 * g];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) rhs[hf][i][e] = a[e];
-            }
-        }
-    }
     __syncthreads();   // the inverses
     // Each wave solves its own 16 columns in registers, no LDS and no barrier: the accumulator of a
     // 16x16x16 MFMA (lane = column li, rows 4g..4g+3) is exactly its B-operand layout (k = 4g..4g+3),
@@ -319,10 +309,28 @@ __global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(4)
     for (int hf = 0; hf < 2; ++hf) {
         const int b = w + 8 * hf;
         if (b >= NSOL) break;   // uniform
+        // right-hand side of this lane's cells: rows 16i + 4g + e, column li of block b
+        f4 rhs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (b < SD / 16) {
+                const int d = 16 * b + li;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = 16 * i + 4 * g + e;
+                    const float kv = F16 ? (float)Kx[0][t][d] : (float)Kx[0][t][d] + (float)Kx[F16 ? 0 : 1][t][d];
+                    rhs[i][e] = exp_hw(fminf(glast - sG[t], 0.f)) * kv;
+                }
+            } else {
+                const h4 a = *(const h4*)&Aq[16 * (b - SD / 16) + li][16 * i + 4 * g];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rhs[i][e] = (float)a[e];
+            }
+        }
         f4 Z[4];
 #pragma unroll
         for (int i = 3; i >= 0; --i) {
-            f4 acc = {rhs[hf][i][0], rhs[hf][i][1], rhs[hf][i][2], rhs[hf][i][3]};
+            f4 acc = rhs[i];
 #pragma unroll
             for (int k = i + 1; k < 4; ++k) {
                 // (A'_ki)^T [li][4g + j] = A'[16k + 4g + j][16i + li] = ApT[16i + li][16k + 4g + j]
