@@ -107,6 +107,58 @@ def gdn_chunked_f64(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, C: 
     return out.reshape(nt, nv * S), st
 
 
+
+def gdn_chunked_folded_f64(co, beta_raw, alpha_raw, dt, a, state, nv: int, nk: int, C: int = 64):
+    """The regrouping the GPU chunk kernels compute (no reference counterpart), in float64 and
+    chunk length C (a multiple of 16), the chunk padded with beta = 0, g = 0. With
+    M = (I + diag(beta) A)^-1 diag(beta) (A as in gdn_chunked_f64):
+        Y  = V - diag(e^G) K S0                      (so U above = M Y)
+        Kh = M^T diag(e^{G_L - G}) K                 P = lower_incl(D * Q K^T) M
+        O  = (diag(e^G) Q S0 + P Y) / sqrt(S)        S1 = e^{G_L} S0 + Kh^T Y
+    Kh and P^T come from one backward substitution (I + diag(beta) A)^T Z = [diag(e^{G_L - G}) K |
+    lower_incl(D * Q K^T)^T] blocked by 16 rows (the last block first), rows then scaled by beta:
+    the steps of the GPU chunk prep."""
+    co = np.asarray(co, np.float64)
+    st = np.asarray(state, np.float64).copy()
+    nt = co.shape[0]
+    S = st.shape[-1]
+    qk = nk * S
+    beta, g = gdn_decay_beta(beta_raw, alpha_raw, dt, a)
+    out = np.zeros((nt, nv, S))
+    nb = C // 16
+    for h in range(nv):
+        kh = h % nk
+        S0 = st[h]
+        for c0 in range(0, nt, C):
+            L = min(nt, c0 + C) - c0
+            pad = lambda m: np.pad(m, ((0, C - L),) + ((0, 0),) * (m.ndim - 1))
+            Q = pad(co[c0:c0 + L, kh * S:(kh + 1) * S])
+            K = pad(co[c0:c0 + L, qk + kh * S:qk + (kh + 1) * S])
+            V = pad(co[c0:c0 + L, 2 * qk + h * S:2 * qk + (h + 1) * S])
+            b = pad(beta[c0:c0 + L, h])
+            G = np.cumsum(pad(g[c0:c0 + L, h]))
+            D = np.exp(np.minimum(G[:, None] - G[None, :], 0.0))
+            Ap = np.tril(b[:, None] * (D * (K @ K.T)), -1)
+            Aqk = np.tril(D * (Q @ K.T))
+            R = np.concatenate([np.exp(G[-1] - G)[:, None] * K, Aqk.T], axis=1)
+            Z = np.zeros_like(R)
+            for i in range(nb - 1, -1, -1):
+                bi = slice(16 * i, 16 * i + 16)
+                acc = R[bi].copy()
+                for k in range(i + 1, nb):
+                    bk = slice(16 * k, 16 * k + 16)
+                    acc -= Ap[bk, bi].T @ Z[bk]
+                Ti = np.linalg.inv(np.eye(16) + Ap[bi, bi])
+                Z[bi] = Ti.T @ acc
+            Kh = b[:, None] * Z[:, :S]
+            P = (b[:, None] * Z[:, S:]).T
+            Y = V - np.exp(G)[:, None] * (K @ S0)
+            O = np.exp(G)[:, None] * (Q @ S0) + P @ Y
+            out[c0:c0 + L, h] = O[:L] / np.sqrt(S)
+            S0 = np.exp(G[-1]) * S0 + Kh.T @ Y
+        st[h] = S0
+    return out.reshape(nt, nv * S), st
+
 def rope_f64(x: np.ndarray, pos: int, n_rot: int, theta_scale: float, sections=(0, 0, 0, 0)) -> np.ndarray:
     """Neox-style (I)MRoPE in float64 with exact angles pos * theta_scale**i (theta_scale the f32
     value, cpu.rs:147), the sector rule of cpu.rs:152-155; x [..., head_dim] -> float64 copy.

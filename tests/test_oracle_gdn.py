@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle.ref_np import gdn_chunked_f64, gdn_seq_f64
+from oracle.ref_np import gdn_chunked_f64, gdn_chunked_folded_f64, gdn_seq_f64
 from irontimber_amd.synth import gdn_inputs, gdn_step_inputs
 
 
@@ -91,6 +91,28 @@ def test_chunked_f64_equals_sequential(nt, C):
     np.testing.assert_allclose(o2, o1, atol=1e-10)
     np.testing.assert_allclose(s2, s1, atol=1e-10)
 
+
+
+@pytest.mark.parametrize("nt,C", [(1, 64), (64, 64), (100, 64), (130, 16), (37, 32)])
+def test_chunked_folded_f64_equals_sequential(nt, C):
+    """The regrouping the GPU chunk kernels compute (Kh and P by a blocked backward solve, Y from
+    the raw V and K rows) equals the token-sequential recurrence, partial last chunks included."""
+    d = gdn_step_inputs(9, nt, nv=4, nk=2)
+    o1, s1 = gdn_seq_f64(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    o2, s2 = gdn_chunked_folded_f64(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2, C=C)
+    np.testing.assert_allclose(o2, o1, atol=1e-10)
+    np.testing.assert_allclose(s2, s1, atol=1e-10)
+
+
+def test_chunked_folded_f64_strong_decay_zero_beta():
+    """Near-total decay and beta ~ 0 on some tokens: the fold has no division by a decay or beta."""
+    d = gdn_step_inputs(10, 150, nv=4, nk=2)
+    d["alpha_raw"][10:20] = 30.0
+    d["beta_raw"][40:60] = -60.0
+    o1, s1 = gdn_seq_f64(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    o2, s2 = gdn_chunked_folded_f64(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], 4, 2)
+    np.testing.assert_allclose(o2, o1, atol=1e-9)
+    np.testing.assert_allclose(s2, s1, atol=1e-9)
 
 def test_layer_matches_pieces():
     """conv -> L2 -> recurrence, one token at a time (cpu.rs:201-232)."""
