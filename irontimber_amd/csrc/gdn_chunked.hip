@@ -389,22 +389,29 @@ struct ScanStage {
 __device__ __forceinline__ int swz256(int r) { return r & 15; }
 __device__ __forceinline__ int swz128(int r) { return (r >> 1) & 7; }
 
-// Issue loads of one chunk into stage B as the share `part` (0-3) of the loader waves: Kh^T, P and
-// (part 0) the decay table from the record `rec`; q and k rows from `qb` (row r at
-// qb + min(r, L-1) * pitch, its k row koff halves further); V rows from `vb` (row r at
-// vb + min(r, L-1) * cts). Instructions of 64 lanes x 16 bytes, per wave k 4, q 4, Kh^T 4, P 2,
-// V 2 or 4 in all (+1); lane l lands at byte 16*l of its instruction's 1 KB.
+// Loads of one chunk into stage B, as the share `part` (0-3) of the loader waves, in two batches:
+// the k and q rows (scan_stage_kq: from `qb`, row r at qb + min(r, L-1) * pitch, its k row koff
+// halves further; 4 + 4 instructions a wave), and the rest (scan_stage_rest: Kh^T, P and (part 0)
+// the decay table from the record `rec`, V rows from `vb`, row r at vb + min(r, L-1) * cts; Kh^T
+// 4, P 2, V 2 or 4 in all, +1). Instructions of 64 lanes x 16 bytes; lane l lands at byte 16*l of
+// its instruction's 1 KB.
 template <typename CoT>
-__device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, const _Float16* __restrict__ qb, int pitch,
-                                                 int koff, const CoT* __restrict__ vb, int cts, int L, ScanStage<CoT>& B,
-                                                 int part, int l) {
+__device__ __forceinline__ void scan_stage_kq(const _Float16* __restrict__ qb, int pitch, int koff, int L,
+                                              ScanStage<CoT>& B, int part, int l) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {   // k and q: 4 rows of 256 B per instruction
+    for (int k = 0; k < 4; ++k) {   // 4 rows of 256 B per instruction
         const int i = 4 * part + k, r = 4 * i + (l >> 4), j = (l & 15) ^ swz256(r);
         const _Float16* qr = qb + (size_t)min(r, L - 1) * pitch;
         __builtin_amdgcn_global_load_lds((const void*)(qr + koff + 8 * j), (lds_void*)(B.K + 4 * i * SD), 16, 0, 0);
         __builtin_amdgcn_global_load_lds((const void*)(qr + 8 * j), (lds_void*)(B.Q + 4 * i * SD), 16, 0, 0);
     }
+}
+constexpr int SCAN_KQ_LOADS = 8;   // instructions of scan_stage_kq per loader wave
+constexpr int SCAN_TOUCH_AHEAD = 3;   // chunks between a chunk's L2 touch and its staging
+
+template <typename CoT>
+__device__ __forceinline__ void scan_stage_rest(const char* __restrict__ rec, const CoT* __restrict__ vb, int cts,
+                                                int L, ScanStage<CoT>& B, int part, int l) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {   // Kh^T: 8 rows of 128 B per instruction
         const int i = 4 * part + k, r = 8 * i + (l >> 3), j = (l & 7) ^ swz128(r);
@@ -429,8 +436,11 @@ __device__ __forceinline__ void scan_stage_loads(const char* __restrict__ rec, c
 // Y = V - e^G K S0 and S1 = e^{G_last} S0 + Kh^T Y; the output O = e^G Q S0 + P Y hangs off it.
 // Waves 0-3 ("chain") run the chain for chunk c while waves 4-7 ("output") compute O of chunk c-1
 // from the previous chunk's S0 and Y (both double buffered in LDS). Waves 8-11 ("loaders") stage
-// chunk c+1's operands into the other LDS stage and touch chunk c+3's lines so that the staging
-// hits L2; only they ever wait for global loads, so no compute wave stalls on load issue.
+// the operands and touch chunk c+3's lines so that the staging hits L2; only they ever wait for
+// global loads, so no compute wave stalls on load issue. A stage's k and q rows are read only
+// before the step's second barrier (the chain's Y phase, the output waves' operand copy), so the
+// loaders issue chunk c+2's k and q rows after that barrier and the rest of chunk c+1 after the
+// first: the ~60 KB a step passes through the CU's load path in both halves of the step.
 // An f16 conv output (CoT = _Float16) gives q and k in place; from an f32 one they are the
 // prep's f16 rows in the record. V is read in place either way.
 constexpr int SCAN_THREADS = 768;
@@ -468,15 +478,19 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
     auto vbase = [&](int cc) { return co + (size_t)cc * C * cts + 2 * nk * SD + h * SD + n0; };
     const int pitch = DIRECT ? cts : SD, koff = DIRECT ? nk * SD : C * SD;
     auto rows = [&](int cc) { return min(C, nt - cc * C); };
-    auto stage_loads = [&](int cc, ScanStage<CoT>& B, int part) {
-        scan_stage_loads<CoT>(hrec + (size_t)cc * REC, qbase(cc), pitch, koff, vbase(cc), cts, rows(cc), B, part, l);
+    auto stage_kq = [&](int cc, ScanStage<CoT>& B, int part) {
+        scan_stage_kq<CoT>(qbase(cc), pitch, koff, rows(cc), B, part, l);
+    };
+    auto stage_rest = [&](int cc, ScanStage<CoT>& B, int part) {
+        scan_stage_rest<CoT>(hrec + (size_t)cc * REC, vbase(cc), cts, rows(cc), B, part, l);
     };
 
     // Barrier schedule: step c (0 <= c <= nch) holds barriers A_c and B_c. The chain writes S0T[c&1]
-    // before A_c, reads stage c&1 and writes YT[c&1] between A_c and B_c, reads stage c&1 again
-    // after B_c. The output waves read S0T/YT[(c-1)&1] and stage c&1 between A_c and B_c. The
-    // loaders fill stage (c+1)&1 after A_c and have it landed before A_{c+1}. Step nch only
-    // finishes the last chunk's output.
+    // before A_c, reads stage c&1 and writes YT[c&1] between A_c and B_c, reads stage c&1's Kh^T and
+    // table after B_c. The output waves read S0T/YT[(c-1)&1] and stage c&1 between A_c and B_c. The
+    // loaders fill stage (c+1)&1's Kh^T, P, V and table after A_c and stage c&1's k and q rows (for
+    // chunk c+2) after B_c, and have chunk c+1 landed before A_{c+1}. Step nch only finishes the
+    // last chunk's output.
     if (wv >= 8) {
         const int part = wv - 8;
         constexpr int RL = (int)(REC / 128);                        // 128-byte lines of a record
@@ -497,16 +511,27 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
             }
             __builtin_amdgcn_global_load_lds((const void*)p, (lds_void*)PfSink, 4, 0, 0);
         };
-        stage_loads(0, B0, part);
-        touch(1);
-        touch(2);
-        IT_SCAN_WAIT_VMCNT(2);
+        stage_kq(0, B0, part);
+        stage_rest(0, B0, part);
+        if (nch > 1) stage_kq(1, B1, part);
+#pragma unroll
+        for (int k = 1; k < SCAN_TOUCH_AHEAD; ++k) touch(k);
+        // chunk 0 landed; chunk 1's k and q rows and the touches may still be in flight
+        if (nch > 1) IT_SCAN_WAIT_VMCNT(SCAN_KQ_LOADS + SCAN_TOUCH_AHEAD - 1);
+        else IT_SCAN_WAIT_VMCNT(SCAN_TOUCH_AHEAD - 1);
         for (int c = 0; c <= nch; ++c) {
             lds_barrier();   // A_c
-            if (c + 1 < nch) stage_loads(c + 1, (c & 1) ? B0 : B1, part);
-            touch(c + 3);
+            if (c + 1 < nch) stage_rest(c + 1, (c & 1) ? B0 : B1, part);
+            touch(c + SCAN_TOUCH_AHEAD);
             lds_barrier();   // B_c
-            IT_SCAN_WAIT_VMCNT(1);   // stage (c+1)&1 landed; the newest touch may still be in flight
+            // chunk c+1 landed (its k and q rows went out a step earlier); the touch and chunk
+            // c+2's k and q rows may still be in flight
+            if (c + 2 < nch) {
+                stage_kq(c + 2, (c & 1) ? B1 : B0, part);
+                IT_SCAN_WAIT_VMCNT(SCAN_KQ_LOADS + 1);
+            } else {
+                IT_SCAN_WAIT_VMCNT(1);
+            }
         }
         return;
     }
@@ -539,49 +564,61 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
                         S0T[b][1][col][dk] = lo;
                     }
             lds_barrier();   // A_c
-            // ---- Y = V - e^G (K S0) for tokens 16w..16w+15 (k row 16w+li, dims 32ks+8g..)
-            f4 ks0[NI];
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni) ks0[ni] = f4{0.f, 0.f, 0.f, 0.f};
+            // ---- Y = V - e^G (K S0) for tokens 16w..16w+15 (k row 16w+li, dims 32ks+8g..). Every
+            // operand and V read is issued before the first product (the reads queue behind the
+            // loaders' LDS writes, so one round trip instead of one per product), the hi and lo
+            // products go to separate accumulators, and Y^T goes out as 8-byte pieces (tokens
+            // 16w + 4g + 0..3 of column li are contiguous).
+            static_assert(NI == 1, "one 16-column tile per workgroup");
+            h8 ka[4], sh[4], sl[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const h8 a = ld_h8(B.K + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
-#pragma unroll
-                for (int ni = 0; ni < NI; ++ni) {
-                    ks0[ni] = mfma16x16x32(a, ld_h8(&S0T[b][0][16 * ni + li][32 * ks + 8 * g]), ks0[ni]);
-                    ks0[ni] = mfma16x16x32(a, ld_h8(&S0T[b][1][16 * ni + li][32 * ks + 8 * g]), ks0[ni]);
-                }
+                ka[ks] = ld_h8(B.K + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
+                sh[ks] = ld_h8(&S0T[b][0][li][32 * ks + 8 * g]);
+                sl[ks] = ld_h8(&S0T[b][1][li][32 * ks + 8 * g]);
             }
+            CoT vv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vv[i] = B.V[(16 * w + 4 * g + i) * CW + li];
             const f4 eg = *(const f4*)&B.T[C + 16 * w + 4 * g];
+            f4 xh = {0.f, 0.f, 0.f, 0.f}, xl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni)
+            for (int ks = 0; ks < 4; ++ks) {
+                xh = mfma16x16x32(ka[ks], sh[ks], xh);
+                xl = mfma16x16x32(ka[ks], sl[ks], xl);
+            }
+            h4 yh, yl;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = 16 * w + 4 * g + i, col = 16 * ni + li;
-                    const float v = (float)B.V[t * CW + col] - eg[i] * ks0[ni][i];
-                    const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
-                    YT[b][0][col][t] = hi;
-                    YT[b][1][col][t] = lo;
-                }
+            for (int i = 0; i < 4; ++i) {
+                const float v = (float)vv[i] - eg[i] * (xh[i] + xl[i]);
+                yh[i] = (_Float16)v;
+                yl[i] = (_Float16)(v - (float)yh[i]);
+            }
+            *(h4*)&YT[b][0][li][16 * w + 4 * g] = yh;
+            *(h4*)&YT[b][1][li][16 * w + 4 * g] = yl;
             lds_barrier();   // B_c
-            // ---- S1 = e^{G_last} S0 + Kh^T Y (Kh^T rows 16(2w+mi)+li, tokens 32ks+8g..)
-            const float gc = B.T[3 * C];
+            // ---- S1 = e^{G_last} S0 + Kh^T Y (Kh^T rows 16(2w+mi)+li, tokens 32ks+8g..), every
+            // operand read issued first
+            h8 kt[2][2], yv[2][2];
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < NI; ++ni) st[mi][ni] *= gc;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
+            for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
                 for (int mi = 0; mi < 2; ++mi) {
                     const int rk = 16 * (2 * w + mi) + li;
-                    const h8 a = ld_h8(B.KHT + rk * C + 8 * ((4 * ks + g) ^ swz128(rk)));
-#pragma unroll
-                    for (int ni = 0; ni < NI; ++ni) {
-                        st[mi][ni] = mfma16x16x32(a, ld_h8(&YT[b][0][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
-                        st[mi][ni] = mfma16x16x32(a, ld_h8(&YT[b][1][16 * ni + li][32 * ks + 8 * g]), st[mi][ni]);
-                    }
+                    kt[ks][mi] = ld_h8(B.KHT + rk * C + 8 * ((4 * ks + g) ^ swz128(rk)));
                 }
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl) yv[ks][hl] = ld_h8(&YT[b][hl][li][32 * ks + 8 * g]);
+            }
+            const float gc = B.T[3 * C];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) st[mi][0] *= gc;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+                    for (int mi = 0; mi < 2; ++mi) st[mi][0] = mfma16x16x32(kt[ks][mi], yv[ks][hl], st[mi][0]);
         }
         lds_barrier();   // A_nch
         lds_barrier();   // B_nch
@@ -607,24 +644,31 @@ __global__ __launch_bounds__(SCAN_THREADS) void gdn_chunk_scan(const char* __res
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) oa[ni] = f4{0.f, 0.f, 0.f, 0.f};
         if (c > 0) {
+            // every operand read first, then the products (hi and lo of S0 in separate accumulators)
+            h8 sh[4], sl[4], yv[2][2];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                for (int ni = 0; ni < NI; ++ni) {
-                    oa[ni] = mfma16x16x32(qg[ks], ld_h8(&S0T[pb][0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-                    oa[ni] = mfma16x16x32(qg[ks], ld_h8(&S0T[pb][1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-                }
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni) oa[ni] *= eg;   // e^{G_t} of rows 16w + 4g + i
+            for (int ks = 0; ks < 4; ++ks) {
+                sh[ks] = ld_h8(&S0T[pb][0][li][32 * ks + 8 * g]);
+                sl[ks] = ld_h8(&S0T[pb][1][li][32 * ks + 8 * g]);
+            }
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                for (int ni = 0; ni < NI; ++ni) {
-                    oa[ni] = mfma16x16x32(pa[ks], ld_h8(&YT[pb][0][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-                    oa[ni] = mfma16x16x32(pa[ks], ld_h8(&YT[pb][1][16 * ni + li][32 * ks + 8 * g]), oa[ni]);
-                }
+                for (int hl = 0; hl < 2; ++hl) yv[ks][hl] = ld_h8(&YT[pb][hl][li][32 * ks + 8 * g]);
+            f4 qh = {0.f, 0.f, 0.f, 0.f}, ql = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                qh = mfma16x16x32(qg[ks], sh[ks], qh);
+                ql = mfma16x16x32(qg[ks], sl[ks], ql);
+            }
+            oa[0] = (qh + ql) * eg;   // e^{G_t} of rows 16w + 4g + i
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl) oa[0] = mfma16x16x32(pa[ks], yv[ks][hl], oa[0]);
         }
         if (c < nch) {
+            // chunk c's operands, before B_c: the loaders overwrite stage c&1's q rows after it
             const ScanStage<CoT>& B = b ? B1 : B0;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) qg[ks] = ld_h8(B.Q + rw * SD + 8 * ((4 * ks + g) ^ swz256(rw)));
