@@ -233,6 +233,29 @@ def test_chunked_matches_float64_recurrence(dev, nt, nv, nk):
     assert np.isfinite(out).all() and eo <= OUT_TOL and es <= STATE_TOL
 
 
+
+@pytest.mark.parametrize("nt,nv,nk", [(63, 6, 3), (127, 1, 1), (129, 48, 16), (257, 6, 3), (320, 2, 2)])
+def test_chunked_and_prefill_more_geometries(dev, nt, nv, nk):
+    """More head geometries (one V head; 48 V heads, past the 32 one grid row of the scan holds;
+    V heads sharing a q/k head three ways) and chunk counts 1-5 with ragged tails, for both the
+    chunked scan from an f32 conv output and the one-call prefill from its f16 one: each against
+    the float64 token recurrence on the conv output it consumed."""
+    announce(f"gdn chunked + prefill nt={nt} nv={nv} nk={nk}")
+    d = gdn_step_inputs(31 + nt, nt, nv=nv, nk=nk)
+    out, st = _chunked(dev, d, nv, nk)
+    o64, s64 = gdn_seq_f64(d["co"], d["beta_raw"], d["alpha_raw"], d["dt"], d["a"], d["state"], nv, nk)
+    assert np.isfinite(out).all()
+    assert np.abs(out - o64).max() <= OUT_TOL and np.abs(st - s64).max() <= STATE_TOL
+    d2 = gdn_inputs(41 + nt, nt=nt, nv=nv, nk=nk)
+    args = [dev_f32(d2["beta_raw"], dev), dev_f32(d2["alpha_raw"], dev), dev_f32(d2["dt"], dev), dev_f32(d2["a"], dev)]
+    cs, st2 = dev_f32(d2["conv_state"], dev), dev_f32(d2["state"], dev)
+    co = ops.gdn_conv_l2norm(dev_f32(d2["x"], dev), dev_f32(d2["w"], dev), dev_f32(d2["conv_state"], dev),
+                             2 * nk).half().float()
+    got = host(ops.gdn_prefill(dev_f32(d2["x"], dev), dev_f32(d2["w"], dev), cs, *args, st2, nv, nk))
+    o64, s64 = gdn_seq_f64(host(co), d2["beta_raw"], d2["alpha_raw"], d2["dt"], d2["a"], d2["state"], nv, nk)
+    assert np.isfinite(got).all()
+    assert np.abs(got - o64).max() <= OUT_TOL and np.abs(host(st2) - s64).max() <= STATE_TOL
+
 def test_chunked_strong_decay_and_zero_beta(dev):
     """Edge cases of the decay/gate: near-total decay (alpha_raw large) and beta ~ 0 on some tokens."""
     nt, nv, nk = 150, 4, 2
