@@ -63,8 +63,9 @@ __device__ __forceinline__ void split_hi_lo4(f4 x, h4& hi, h4& lo) {
 // ------------------------------------------------------------------------------------------------
 // 8 waves, 66 KB of LDS (two workgroups per CU, so one's loads overlap the other's products; 48 KB
 // and three from an f16 conv output, whose K rows need no lo plane): the K rows as f16 hi/lo
-// pairs, A'^T, the masked Q K^T block and the transposed diagonal-block inverses. Q never enters LDS: the Q K^T operands are read from global (the chunk's q rows stay
-// in L2). The triangular solve runs in registers.
+// pairs, A'^T, the masked Q K^T block and the transposed diagonal-block inverses. Q never enters
+// LDS: the Q K^T operands are read from global (the chunk's q rows stay in L2). The triangular
+// solve runs in registers.
 constexpr int PREP_THREADS = 512;
 constexpr int KP = SD + 8;     // f16 row pitch of the K tile (272 B: 16 rows at one column hit distinct bank groups)
 constexpr int NSOL = (SD + C) / 16;   // 16-column blocks of the solve: 8 of Kh, 4 of P^T
@@ -87,11 +88,10 @@ __device__ __forceinline__ void prep_wg(int id, int nch, int nv, int nk, int& c,
 }
 
 template <typename CoT>
-__global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(sizeof(CoT) == 2 ? 6 : 4))) void gdn_chunk_prep(const CoT* __restrict__ co, int cts,
-                                                               const float* __restrict__ br, const float* __restrict__ ar,
-                                                               int bts, const float* __restrict__ dt,
-                                                               const float* __restrict__ A, int nt, int nv, int nk,
-                                                               char* __restrict__ scr) {
+__global__ __launch_bounds__(PREP_THREADS) __attribute__((amdgpu_waves_per_eu(sizeof(CoT) == 2 ? 6 : 4)))
+void gdn_chunk_prep(const CoT* __restrict__ co, int cts, const float* __restrict__ br, const float* __restrict__ ar,
+                    int bts, const float* __restrict__ dt, const float* __restrict__ A, int nt, int nv, int nk,
+                    char* __restrict__ scr) {
     // an f16 conv output is exact in f16, so its hi/lo splits have lo == 0 and the K K^T / Q K^T
     // products need only the hi x hi term (bit-identical to the three-term form); the lo plane of
     // the K tile is then not kept, and the 48 KB of LDS leave room for three workgroups per CU
