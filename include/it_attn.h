@@ -61,6 +61,18 @@ int it_attn_prep_f16(float* q, int q_tok_stride, const float* k, const float* v,
                      int pos0, int hd, int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1,
                      int sec2, int sec3, int round_mode, void* stream);
 
+/* it_attn_prep_f16 that also writes the query in the form the flash prefill kernel computes with:
+ * q16[t*q16_tok_stride + h*hd + d] = f16_rne(q'[d] * (scale * log2(e))), q' the rewritten query
+ * and scale the attention scale the following it_attn_f16_q16 call will pass (the product taken
+ * in f32, as that kernel takes it). q16: 16-byte aligned f16 (uint16_t bits), q16_tok_stride a
+ * multiple of 8, >= nh*hd. No counterpart in the reference (its prefill kernels read f32 q): an
+ * opt-in for prefill callers, whose flash kernel then reads half the q bytes and no f32 rows. */
+int it_attn_prep_f16_q16(float* q, int q_tok_stride, const float* k, const float* v, int kv_tok_stride,
+                         const float* q_norm, const float* k_norm, float eps, uint16_t* kc, uint16_t* vc, int kvd,
+                         int pos0, int hd, int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1,
+                         int sec2, int sec3, int round_mode, uint16_t* q16, int q16_tok_stride, float scale,
+                         void* stream);
+
 /* Bytes of scratch it_attn_f16 needs for this call geometry (0 if the chosen kernel needs none). */
 size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv);
 
@@ -105,6 +117,16 @@ size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int k
 int it_attn_f16_ex(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd,
                    int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int out_tok_stride,
                    void* scratch, size_t scratch_bytes, int kernel, int chunk, void* stream);
+
+/* it_attn_f16 with the flash prefill kernel's query operand given pre-converted: q16 as written by
+ * it_attn_prep_f16_q16 with the same scale (f16(q * scale * log2(e)), token stride q16_tok_stride).
+ * The result is identical, bit for bit, to it_attn_f16 on the f32 q that q16 was made from; q
+ * still provides the gates, and calls that take the split-K kernels (nt < 16) read q as
+ * it_attn_f16 does. Same scratch rule and requirements as it_attn_f16. No counterpart in the
+ * reference; see it_attn_prep_f16_q16. */
+int it_attn_f16_q16(const float* q, int q_tok_stride, const uint16_t* q16, int q16_tok_stride, const uint16_t* kc,
+                    const uint16_t* vc, int kvd, int pos0, int hd, int nh, int nkv, int nt, float scale, float* out,
+                    int out_tok_stride, void* scratch, size_t scratch_bytes, void* stream);
 
 /* it_attn_f16 that allocates nothing and takes no scratch argument. No counterpart in the reference:
  * it is for callers that cannot allocate device memory or hand over a workspace (code under HIP

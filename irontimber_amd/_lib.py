@@ -18,6 +18,10 @@ SIGNATURES = {
     "it_kv_append_f16": (c_int, [P, P, c_int, P, P, c_int, c_int, c_int, c_int, P]),
     "it_attn_prep_f16": (c_int, [P, c_int, P, P, c_int, P, P, c_float, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
                                  c_int, c_float, c_int, c_int, c_int, c_int, c_int, P]),
+    "it_attn_prep_f16_q16": (c_int, [P, c_int, P, P, c_int, P, P, c_float, P, P, c_int, c_int, c_int, c_int, c_int,
+                                     c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_int, P, c_int, c_float, P]),
+    "it_attn_f16_q16": (c_int, [P, c_int, P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_int,
+                                P, c_size_t, P]),
     "it_attn_prep_f32kv": (c_int, [P, c_int, P, P, c_int, P, P, c_float, P, P, c_int, c_int, c_int, c_int, c_int,
                                    c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, P]),
     "it_attn_f32kv_scratch_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),

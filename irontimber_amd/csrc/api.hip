@@ -253,6 +253,28 @@ int it_attn_prep_f16(float* q, int qts, const float* k, const float* v, int kts,
                  who);
 }
 
+int it_attn_prep_f16_q16(float* q, int qts, const float* k, const float* v, int kts, const float* q_norm,
+                         const float* k_norm, float eps, uint16_t* kc, uint16_t* vc, int kvd, int pos0, int hd, int nh,
+                         int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1, int sec2, int sec3,
+                         int round_mode, uint16_t* q16, int q16ts, float scale, void* stream) {
+    const char* who = "it_attn_prep_f16_q16";
+    if (validate_prep(who, q, qts, k, v, kts, q_norm, k_norm, eps, kc, vc, kvd, pos0, hd, nh, nkv, nt, n_rot,
+                      theta_scale, sec0, sec1, sec2, sec3))
+        return -1;
+    if (round_mode != 0 && round_mode != 1) return fail("%s: round_mode must be 0 (RNE) or 1 (RTZ)", who);
+    if (!q16) return fail("%s: null q16", who);
+    if (!aligned16(q16) || q16ts % 8 != 0) return fail("%s: q16 must be 16-byte aligned, its token stride a multiple of 8", who);
+    if (nt > 1 && q16ts < nh * hd) return fail("%s: q16 token stride %d overlaps rows", who, q16ts);
+    if (!(scale > 0.0f) || !(scale < 1e30f)) return fail("%s: scale %g invalid", who, scale);
+    if (nt == 0) { g_err.clear(); return 0; }
+    const int sec[4] = {sec0, sec1, sec2, sec3};
+    // the flash kernel's own conversion: f16(q * (scale * LOG2E)), the product in f32
+    const float q16s = scale * it::LOG2E;
+    return check(it::launch_attn_prep(q, qts, k, v, kts, q_norm, k_norm, eps, kc, vc, pos0, hd, nh, nkv, nt, n_rot,
+                                      theta_scale, sec, round_mode, (hipStream_t)stream, q16, q16ts, q16s),
+                 who);
+}
+
 int it_attn_prep_f32kv(float* q, int qts, const float* k, const float* v, int kts, const float* q_norm,
                        const float* k_norm, float eps, float* kc, float* vc, int kvd, int pos0, int row0, int hd,
                        int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0, int sec1, int sec2, int sec3,
@@ -338,9 +360,12 @@ size_t it_attn_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv) {
     return it_attn_scratch_bytes_ex(pos0, nt, hd, nh, nkv, KERNEL_AUTO, 0);
 }
 
-int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
-                   int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes, int kernel,
-                   int chunk, void* stream) {
+// it_attn_f16_ex with an optional pre-converted q operand for the flash kernels (q16, see
+// it_attn_f16_q16); the split-K (decode, verify) kernels read q as always.
+static int attn_f16_impl(const float* q, int qts, const uint16_t* q16, int q16ts, const uint16_t* kc,
+                         const uint16_t* vc, int kvd, int pos0, int hd, int nh, int nkv, int nt, float scale,
+                         float* out, int ots, void* scratch, size_t scratch_bytes, int kernel, int chunk,
+                         void* stream) {
     if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, out, ots)) return -1;
     if (kernel != KERNEL_AUTO && kernel != KERNEL_SPLITK && kernel != KERNEL_FLASH && kernel != KERNEL_FLASH_F32)
         return fail("it_attn_f16: unknown kernel %d", kernel);
@@ -366,14 +391,14 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
         // (chunk is never 0 here: the automatic plan above has replaced it)
         const int c = flash_chunk(pos0, nt, nh, nkv, chunk);
         if (!c)
-            return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st),
+            return check(it::launch_attn_flash(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, st, q16, q16ts),
                          "it_attn_f16 (flash)");
         const size_t need = flash_scratch(pos0, nt, nh, c, f32);
         if (scratch_bytes < need || !scratch)
             return fail("it_attn_f16: scratch of %zu bytes < %zu required (it_attn_scratch_bytes)", scratch_bytes, need);
         if (!aligned16(scratch)) return fail("it_attn_f16: scratch must be 16-byte aligned");
         return check(it::launch_attn_flash_split(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots,
-                                                 (float*)scratch, c, st, f32),
+                                                 (float*)scratch, c, st, f32, q16, q16ts),
                      "it_attn_f16 (flash, key splits)");
     }
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
@@ -384,6 +409,24 @@ int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* 
     if (!aligned16(scratch)) return fail("it_attn_f16: scratch must be 16-byte aligned");
     return check(it::launch_attn_splitk(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, (float*)scratch, chunk, st),
                  "it_attn_f16 (split-K)");
+}
+
+int it_attn_f16_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,
+                   int nkv, int nt, float scale, float* out, int ots, void* scratch, size_t scratch_bytes, int kernel,
+                   int chunk, void* stream) {
+    return attn_f16_impl(q, qts, nullptr, 0, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, ots, scratch,
+                         scratch_bytes, kernel, chunk, stream);
+}
+
+int it_attn_f16_q16(const float* q, int qts, const uint16_t* q16, int q16ts, const uint16_t* kc, const uint16_t* vc,
+                    int kvd, int pos0, int hd, int nh, int nkv, int nt, float scale, float* out, int ots, void* scratch,
+                    size_t scratch_bytes, void* stream) {
+    if (!q16) return fail("it_attn_f16_q16: null q16");
+    if (!aligned16(q16) || q16ts % 8 != 0)
+        return fail("it_attn_f16_q16: q16 must be 16-byte aligned, its token stride a multiple of 8");
+    if (nt > 1 && q16ts < nh * hd) return fail("it_attn_f16_q16: q16 token stride %d overlaps rows", q16ts);
+    return attn_f16_impl(q, qts, q16, q16ts, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, out, ots, scratch,
+                         scratch_bytes, KERNEL_AUTO, 0, stream);
 }
 
 int it_attn_f16(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd, int nh,

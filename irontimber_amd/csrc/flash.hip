@@ -30,7 +30,6 @@ namespace it {
 namespace {
 constexpr int HD = 256;
 constexpr int BM = 128, BN = 64;
-constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.0f;   // log2 units
 }
 
@@ -77,11 +76,18 @@ __device__ __forceinline__ void scale_acc(f16v& acc, float a) {
 
 // F32REC: the key-split records in the split-K kernels' lossless f32 form instead ({m, l, 0, 0} +
 // O as 256 floats, 260 words, merged by the f32 combine), selectable through it_attn_f16_ex.
-template <bool F32REC>
+// QM: where the q operand comes from. 0: the f32 q rows, scaled and converted here. 1 and 2: q16,
+// pre-converted (q16[t][h][d] = f16(q * scale * log2 e), exactly what that conversion makes, from
+// it_attn_prep_f16_q16), half the bytes; q still provides the gates. 1 gathers each lane's operand
+// straight from global, no transpose through LDS: for key-split launches, whose q rows are re-read
+// by every split from L2. 2 reads whole rows and transposes them through LDS as QM 0 does: for
+// one-pass launches, which read q once from memory, where the gather's 32 rows per instruction
+// cost more than the transpose.
+template <bool F32REC, int QM>
 __global__ __launch_bounds__(256) void attn_flash_kernel(
-    const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int kvd,
-    int pos0, int nh, int nkv, int nt, float scale, float* __restrict__ out, int ots, float* __restrict__ part,
-    int chunk, int smax) {
+    const float* __restrict__ q, int qts, const _Float16* __restrict__ q16, int q16ts, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int kvd, int pos0, int nh, int nkv, int nt, float scale, float* __restrict__ out,
+    int ots, float* __restrict__ part, int chunk, int smax) {
     // two K and two V buffers as distinct objects, so the compiler can tell that the loads
     // streaming into one buffer never alias the reads of the other (no conservative waits)
     __shared__ __align__(16) _Float16 K0[BN * HD];
@@ -118,7 +124,52 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) cj[i] = 2 * (int)head_off + 16 * ((l & 31) ^ swz(16 * w + 2 * i + (l >> 5)));
     h8 qb[16];
-    {
+    if constexpr (QM == 1) {
+        // lane (c, hh) holds dims 16ks + 8hh .. +7 of its row r (rows past R: zero)
+        const int rr = rvalid ? r : R - 1;
+        const _Float16* qrow = q16 + (size_t)(rr / G) * q16ts + (size_t)(kh * G + rr % G) * HD + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) {
+            const h8 v = ld_h8(qrow + 16 * ks);
+            qb[ks] = rvalid ? v : h8{};
+        }
+        tile_to_lds(kc, kvd, kb0, kend, cj, K0, w, l);
+        tile_to_lds(vc, kvd, kb0, kend, cj, V0, w, l);
+    } else if constexpr (QM == 2) {
+        // two 512-byte rows per load instruction (lanes 0-31 row 2j, lanes 32-63 row 2j + 1 of the
+        // wave's 32; rows past R zero), then the transpose through LDS the f32 rows take below: whole
+        // rows keep the loads coalesced (a per-lane gather of the operand layout touches 32 rows per
+        // instruction)
+        h8 qx[16];
+        const int rw = __builtin_amdgcn_readfirstlane(rt * BM + 32 * w);   // even: BM, 32 are
+        int te = __builtin_amdgcn_readfirstlane(rw / G), ge = rw - te * G;   // row 2j
+        int to = te, go = ge + 1;                                           // row 2j + 1
+        if (go == G) { go = 0; ++to; }
+        const int hi = l >> 5;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const size_t oe = uniform_off((size_t)te * q16ts + (size_t)(kh * G + ge) * HD);
+            const size_t oo = uniform_off((size_t)to * q16ts + (size_t)(kh * G + go) * HD);
+            const bool valid = rw + 2 * j + hi < R;
+            const h8 v = ld_h8(q16 + (valid ? (hi ? oo : oe) : 0) + 8 * (l & 31));
+            qx[j] = valid ? v : h8{};
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                if (++ge == G) { ge = 0; ++te; }
+                if (++go == G) { go = 0; ++to; }
+            }
+        }
+        tile_to_lds(kc, kvd, kb0, kend, cj, K0, w, l);
+        tile_to_lds(vc, kvd, kb0, kend, cj, V0, w, l);
+        _Float16* qs = (w < 2 ? K1 : V1) + (w & 1) * (32 * HD);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = 2 * j + hi;
+            *(h8*)(qs + i * HD + 8 * ((l & 31) ^ i)) = qx[j];
+        }
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) qb[ks] = ld_h8(qs + c * HD + 8 * ((2 * ks + hh) ^ c));
+    } else {
         f4 qx[32];
         const int rw = __builtin_amdgcn_readfirstlane(rt * BM + 32 * w);
         // row rr = token rr / G, q-head kh*G + rr % G: one division, then a walk over the 32 rows
@@ -408,11 +459,17 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
 }
 
 hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
-                             int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st) {
+                             int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st,
+                             const uint16_t* q16, int q16ts) {
     const int R = nt * (nh / nkv);
     const dim3 grid((R + BM - 1) / BM, nkv);
-    attn_flash_kernel<false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, nullptr, 0,
-                                                    1);
+    const _Float16* qh = (const _Float16*)q16;
+    if (q16)
+        attn_flash_kernel<false, 2><<<grid, 256, 0, st>>>(q, qts, qh, q16ts, kc, vc, kvd, pos0, nh, nkv, nt, scale,
+                                                          out, ots, nullptr, 0, 1);
+    else
+        attn_flash_kernel<false, 0><<<grid, 256, 0, st>>>(q, qts, qh, q16ts, kc, vc, kvd, pos0, nh, nkv, nt, scale,
+                                                          out, ots, nullptr, 0, 1);
     return hipGetLastError();
 }
 
@@ -429,16 +486,22 @@ int flash_split_chunk(int pos0, int nt, int nh, int nkv) {
 
 hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                                    int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
-                                   hipStream_t st, bool f32rec) {
+                                   hipStream_t st, bool f32rec, const uint16_t* q16, int q16ts) {
     const int R = nt * (nh / nkv);
     const int smax = (pos0 + nt + chunk - 1) / chunk;
     const dim3 grid((R + BM - 1) / BM, nkv, smax);
-    if (f32rec)
-        attn_flash_kernel<true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, part,
-                                                      chunk, smax);
-    else
-        attn_flash_kernel<false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, ots, part,
-                                                       chunk, smax);
+    const _Float16* qh = (const _Float16*)q16;
+#define IT_FLASH_SPLIT(F32_, Q16_)                                                                                     \
+    attn_flash_kernel<F32_, Q16_><<<grid, 256, 0, st>>>(q, qts, qh, q16ts, kc, vc, kvd, pos0, nh, nkv, nt, scale, out, \
+                                                        ots, part, chunk, smax)
+    if (f32rec) {
+        if (q16) IT_FLASH_SPLIT(true, 1);
+        else IT_FLASH_SPLIT(true, 0);
+    } else {
+        if (q16) IT_FLASH_SPLIT(false, 1);
+        else IT_FLASH_SPLIT(false, 0);
+    }
+#undef IT_FLASH_SPLIT
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return f32rec ? launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st)

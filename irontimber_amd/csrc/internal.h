@@ -10,7 +10,8 @@ hipError_t launch_kv_append(const float* k, const float* v, int sts, uint16_t* k
                             int kvd, int rtz, hipStream_t st);
 hipError_t launch_attn_prep(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
                             const float* kw, float eps, uint16_t* kc, uint16_t* vc, int pos0, int hd, int nh, int nkv,
-                            int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st);
+                            int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st,
+                            uint16_t* q16 = nullptr, int q16ts = 0, float q16s = 0.f);
 hipError_t launch_attn_prep_f32kv(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
                                   const float* kw, float eps, float* kc, float* vc, int pos0, int row0, int hd, int nh,
                                   int nkv, int nt, int n_rot, float tsc, const int* sec, hipStream_t st);
@@ -22,6 +23,8 @@ hipError_t launch_attn_combine(const float* q, int qts, const float* part, int p
                                float* out, int ots, hipStream_t st);
 // Key-split flash records in the compact form: {m, l, k, 0} + 256 int16 (O in units of k).
 constexpr int FLASH_REC = 4 + 128;
+// log2(e): the flash kernel works in log2 units (its q operand is q * scale * LOG2E)
+constexpr float LOG2E = 1.4426950408889634f;
 hipError_t launch_attn_combine_q16(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                    float* out, int ots, hipStream_t st);
 hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
@@ -41,13 +44,16 @@ hipError_t launch_attn_decode_mailbox(const float* q, int qts, const uint16_t* k
 // report: device address of a host-visible word the fill clears and a merge that finds the
 // mailbox poisoned sets (null: none)
 hipError_t launch_mailbox_fill(void* mb, size_t bytes, uint32_t* report, hipStream_t st);
+// q16 (optional): the q operand pre-converted, q16[t * q16ts + h * 256 + d] = f16(q * scale * LOG2E)
 hipError_t launch_attn_flash(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
-                             int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st);
+                             int nh, int nkv, int nt, float scale, float* out, int ots, hipStream_t st,
+                             const uint16_t* q16 = nullptr, int q16ts = 0);
 
 int flash_split_chunk(int pos0, int nt, int nh, int nkv);
 hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                                    int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
-                                   hipStream_t st, bool f32rec = false);
+                                   hipStream_t st, bool f32rec = false, const uint16_t* q16 = nullptr,
+                                   int q16ts = 0);
 
 // ck / ck_after: optional checkpoint of the state after token ck_after (null = none).
 hipError_t launch_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt,

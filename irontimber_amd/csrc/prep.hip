@@ -1,6 +1,8 @@
 // Attention pre-pass in one launch: per-head RMSNorm of q and k with their weights, neox-style
 // (I)MRoPE on the first n_rot dims of each q/k head, and the f16 append of K and V to the cache.
 // The q half of each [q | gate] head block is rewritten in place (f32); the gate half is not touched.
+// Optionally q also goes out as the flash prefill kernel's f16 operand, q16[t][h][d] =
+// f16(q * q16s) with q16s = scale * log2(e), rounded as that kernel would round it.
 //
 // Reference behaviour: cpu.rs:249-258 (norm, rope, f16 round, append), cpu.rs:14-18 (rmsnorm),
 // cpu.rs:145-162 and shaders/rope.comp:1-19 (rope and its sector rule), kernels/src/lib.rs:207-229
@@ -56,7 +58,7 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void attn_prep_kernel(
     float* __restrict__ q, int qts, const float* __restrict__ k, const float* __restrict__ v, int kts,
     const float* __restrict__ qw, const float* __restrict__ kw, float eps, KVT* __restrict__ kc,
     KVT* __restrict__ vc, int kvd, int pos0, int row0, int nh, int nkv, int n_rot, float tsc, int s0, int s1, int s2,
-    int s3, int rtz) {
+    int s3, int rtz, _Float16* __restrict__ q16, int q16ts, float q16s) {
     typedef typename RowT<E>::T V;
     constexpr int HDK = 64 * E;
     __shared__ float cs_c[HDK / 2], cs_s[HDK / 2];
@@ -110,6 +112,12 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void attn_prep_kernel(
     }
     if (kind == 0) {
         *(V*)(q + (size_t)t * qts + (size_t)kh * 2 * HDK + E * l) = x;
+        if (q16) {
+            _Float16* d = q16 + (size_t)t * q16ts + (size_t)kh * HDK + E * l;
+            if constexpr (E == 4) *(h4*)d = h4{(_Float16)(x[0] * q16s), (_Float16)(x[1] * q16s), (_Float16)(x[2] * q16s),
+                                              (_Float16)(x[3] * q16s)};
+            else *(h2*)d = h2{(_Float16)(x[0] * q16s), (_Float16)(x[1] * q16s)};
+        }
         return;
     }
     KVT* dst = (kind == 1 ? kc : vc) + (size_t)(row0 + t) * kvd + (size_t)kh * HDK + E * l;
@@ -127,24 +135,28 @@ __global__ __launch_bounds__(64 * PREP_WAVES) void attn_prep_kernel(
 template <class KVT>
 static hipError_t launch_prep(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
                               const float* kw, float eps, KVT* kc, KVT* vc, int pos0, int row0, int hd, int nh,
-                              int nkv, int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st) {
+                              int nkv, int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st,
+                              _Float16* q16 = nullptr, int q16ts = 0, float q16s = 0.f) {
     const long groups = (nh + 2 * nkv + PREP_WAVES - 1) / PREP_WAVES;   // workgroups per token
     const dim3 grid((unsigned)(groups * nt)), block(64 * PREP_WAVES);
     const int kvd = nkv * hd;
     if (hd == 256)
         attn_prep_kernel<4, KVT><<<grid, block, 0, st>>>(q, qts, k, v, kts, qw, kw, eps, kc, vc, kvd, pos0, row0, nh,
-                                                        nkv, n_rot, tsc, sec[0], sec[1], sec[2], sec[3], rtz);
+                                                        nkv, n_rot, tsc, sec[0], sec[1], sec[2], sec[3], rtz, q16,
+                                                        q16ts, q16s);
     else
         attn_prep_kernel<2, KVT><<<grid, block, 0, st>>>(q, qts, k, v, kts, qw, kw, eps, kc, vc, kvd, pos0, row0, nh,
-                                                        nkv, n_rot, tsc, sec[0], sec[1], sec[2], sec[3], rtz);
+                                                        nkv, n_rot, tsc, sec[0], sec[1], sec[2], sec[3], rtz, q16,
+                                                        q16ts, q16s);
     return hipGetLastError();
 }
 
 hipError_t launch_attn_prep(float* q, int qts, const float* k, const float* v, int kts, const float* qw,
                             const float* kw, float eps, uint16_t* kc, uint16_t* vc, int pos0, int hd, int nh, int nkv,
-                            int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st) {
+                            int nt, int n_rot, float tsc, const int* sec, int rtz, hipStream_t st, uint16_t* q16,
+                            int q16ts, float q16s) {
     return launch_prep<uint16_t>(q, qts, k, v, kts, qw, kw, eps, kc, vc, pos0, pos0, hd, nh, nkv, nt, n_rot, tsc, sec,
-                                 rtz, st);
+                                 rtz, st, (_Float16*)q16, q16ts, q16s);
 }
 
 hipError_t launch_attn_prep_f32kv(float* q, int qts, const float* k, const float* v, int kts, const float* qw,

@@ -75,6 +75,36 @@ def attn_prep_f16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kc: torch.T
          round_mode, _stream())
 
 
+def attn_prep_f16_q16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int,
+                      nh: int, nkv: int, scale: float | None = None, q_norm: torch.Tensor | None = None,
+                      k_norm: torch.Tensor | None = None, eps: float = 1e-6, n_rot: int = 64,
+                      theta_scale: float | None = None, rope_base: float = 1e7, sections=(11, 11, 10, 0),
+                      round_mode: int = 0) -> torch.Tensor:
+    """attn_prep_f16 that also returns q16 [nt, nh*hd] f16 = f16(q' * scale * log2(e)), the flash
+    prefill kernel's query operand for attn_f16_q16 with the same scale (it_attn_prep_f16_q16)."""
+    _need(q, torch.float32, "q"); _need(k, torch.float32, "k"); _need(v, torch.float32, "v")
+    nt, kvd = k.shape
+    hd = kvd // nkv
+    if q.shape != (nt, nh * 2 * hd) or v.shape != k.shape:
+        raise ValueError("q must be [nt, nh*2*hd] and v the shape of k [nt, nkv*hd]")
+    for c in (kc, vc):
+        if c.dtype not in (torch.float16, torch.int16) or not c.is_contiguous() or c.shape[-1] != kvd:
+            raise ValueError("kc/vc must be contiguous [ctx, kvd] f16")
+        if c.shape[0] < pos0 + nt:
+            raise ValueError("cache too short")
+    if scale is None:
+        scale = 1.0 / hd ** 0.5
+    if theta_scale is None:
+        from .synth import rope_theta_scale
+        theta_scale = rope_theta_scale(rope_base, n_rot)
+    q16 = torch.empty(nt, nh * hd, device=q.device, dtype=torch.float16)
+    s = list(sections) + [0] * (4 - len(sections))
+    call("it_attn_prep_f16_q16", q.data_ptr(), q.shape[1], k.data_ptr(), v.data_ptr(), kvd, _ptr(q_norm),
+         _ptr(k_norm), float(eps), kc.data_ptr(), vc.data_ptr(), kvd, pos0, hd, nh, nkv, nt, n_rot, float(theta_scale),
+         *s[:4], round_mode, q16.data_ptr(), nh * hd, float(scale), _stream())
+    return q16
+
+
 def attn_prep_f32kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int,
                     row0: int, nh: int, nkv: int, q_norm: torch.Tensor | None = None,
                     k_norm: torch.Tensor | None = None, eps: float = 1e-6, n_rot: int = 64,
@@ -153,6 +183,36 @@ def attn_f16(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int, nh:
     nbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
     call("it_attn_f16_ex", q.data_ptr(), nh * 2 * hd, kc.data_ptr(), vc.data_ptr(), kvd, pos0, hd, nh, nkv, nt,
          float(scale), out.data_ptr(), nh * hd, _ptr(scratch), nbytes, kernel, chunk, _stream())
+    return out
+
+
+def attn_f16_q16(q: torch.Tensor, q16: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int, nh: int, nkv: int,
+                 scale: float | None = None, out: torch.Tensor | None = None,
+                 scratch: torch.Tensor | None = None) -> torch.Tensor:
+    """attn_f16 with the flash kernel's query operand given as q16 [nt, nh*hd] f16 (attn_prep_f16_q16
+    with the same scale, or f16(q * scale * log2(e))); q still gives the gates (it_attn_f16_q16)."""
+    _need(q, torch.float32, "q")
+    nt = q.shape[0]
+    hd = q.shape[-1] // (2 * nh)
+    kvd = nkv * hd
+    if scale is None:
+        scale = 1.0 / hd ** 0.5
+    if q16.dtype != torch.float16 or not q16.is_contiguous() or q16.shape != (nt, nh * hd):
+        raise ValueError("q16 must be contiguous [nt, nh*hd] f16")
+    for c in (kc, vc):
+        if c.dtype not in (torch.float16, torch.int16) or not c.is_contiguous() or c.shape[-1] != kvd:
+            raise ValueError("kc/vc must be contiguous [ctx, nkv*hd] f16")
+        if c.shape[0] < pos0 + nt:
+            raise ValueError("cache shorter than pos0 + nt")
+    if out is None:
+        out = torch.empty(nt, nh * hd, device=q.device, dtype=torch.float32)
+    _need(out, torch.float32, "out")
+    if scratch is None:
+        need = attn_scratch_bytes(pos0, nt, nh, nkv, hd)
+        scratch = torch.empty(need, device=q.device, dtype=torch.uint8) if need else None
+    nbytes = 0 if scratch is None else scratch.numel() * scratch.element_size()
+    call("it_attn_f16_q16", q.data_ptr(), nh * 2 * hd, q16.data_ptr(), nh * hd, kc.data_ptr(), vc.data_ptr(), kvd,
+         pos0, hd, nh, nkv, nt, float(scale), out.data_ptr(), nh * hd, _ptr(scratch), nbytes, _stream())
     return out
 
 

@@ -107,6 +107,31 @@ def test_attn_rejects_bad_geometry_before_device_work():
     assert rc != 0 and "overlaps" in _lib.last_error()
 
 
+
+def test_q16_entries_reject_bad_arguments_before_device_work():
+    """it_attn_prep_f16_q16 / it_attn_f16_q16: a missing, misaligned or overlapping q16, or a bad
+    scale, fails before any launch, as do the checks the plain calls make."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(1 << 20)
+
+    def attn(q16=fake, q16ts=4096, hd=256, nt=64):
+        return lib.it_attn_f16_q16(fake, 8192, q16, q16ts, fake, fake, 512, 0, hd, 16, 2, nt, 0.0625, fake, 4096, None,
+                                   0, None)
+    assert attn(q16=None) != 0 and "q16" in _lib.last_error()
+    assert attn(q16=ctypes.c_void_p((1 << 20) + 8)) != 0 and "16-byte" in _lib.last_error()
+    assert attn(q16ts=4092) != 0 and "multiple of 8" in _lib.last_error()
+    assert attn(q16ts=2048) != 0 and "overlaps" in _lib.last_error()
+    assert attn(hd=128) != 0 and "head_dim" in _lib.last_error()
+
+    def prep(q16=fake, q16ts=4096, scale=0.0625, rm=0):
+        return lib.it_attn_prep_f16_q16(fake, 8192, fake, fake, 512, None, None, 1e-6, fake, fake, 512, 0, 256, 16, 2,
+                                        64, 64, 0.5, 0, 0, 0, 0, rm, q16, q16ts, scale, None)
+    assert prep(q16=None) != 0 and "q16" in _lib.last_error()
+    assert prep(q16ts=4092) != 0 and "multiple of 8" in _lib.last_error()
+    assert prep(q16ts=2048) != 0 and "overlaps" in _lib.last_error()
+    assert prep(scale=0.0) != 0 and "scale" in _lib.last_error()
+    assert prep(rm=2) != 0 and "round_mode" in _lib.last_error()
+
 def test_scratch_bytes_policy():
     lib = _lib.lib()
     # decode: split-K, C = 64 -> 128 splits of 260 words per head

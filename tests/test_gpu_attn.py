@@ -34,6 +34,26 @@ def test_baseline_configs(dev, seed, ctx, nt):
     assert assert_argmax_agrees(got, want) == 0   # BASELINE config: no flip at all
 
 
+
+@pytest.mark.parametrize("ctx,nt", [(128, 128), (64, 64), (256, 64), (4160, 64), (8192, 64), (1000, 40), (103, 3)])
+def test_attn_q16_bit_equal(dev, ctx, nt):
+    """it_attn_f16_q16 with q16 = f16(q * scale * log2 e) (the f32 product, RNE) equals it_attn_f16
+    bit for bit: whole prompts and chunks in one pass, chunks with int16 key-split records, and a
+    split-K call (nt < 16, q16 not read); and both stay at the oracle's bar."""
+    nh, nkv, hd = 16, 2, 256
+    pos0 = ctx - nt
+    announce(f"attn q16 ctx={ctx} nt={nt}")
+    q, kb, vb = attn_inputs(60 + ctx, ctx=ctx, nt=nt, nh=nh, nkv=nkv)
+    q2 = np.ascontiguousarray(q.reshape(nt, -1), dtype=np.float32)
+    s = np.float32(np.float32(1.0 / 16) * np.float32(1.4426950408889634))
+    q16 = np.ascontiguousarray((q2.reshape(nt, nh, 2 * hd)[:, :, :hd] * s).astype(np.float16).reshape(nt, nh * hd))
+    qd, kc, vc = dev_f32(q2, dev), dev_f16bits(kb, dev), dev_f16bits(vb, dev)
+    a = host(ops.attn_f16(qd, kc, vc, pos0, nh, nkv))
+    b = host(ops.attn_f16_q16(qd, torch.from_numpy(q16).to(dev), kc, vc, pos0, nh, nkv))
+    np.testing.assert_array_equal(a, b)
+    want = oracle.attn(q2, kb, vb, pos0, nh, nkv)
+    assert np.abs(b - want).max() <= TOL
+
 @pytest.mark.parametrize("ctx,nt,nh,nkv", [(1, 1, 16, 2), (65, 1, 16, 2), (100, 3, 16, 2), (64, 2, 24, 4),
                                            (300, 5, 8, 8), (129, 7, 4, 1), (777, 33, 16, 2), (64, 64, 16, 2)])
 def test_ragged_and_group_shapes(dev, ctx, nt, nh, nkv):

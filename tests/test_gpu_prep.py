@@ -126,6 +126,64 @@ def test_prep_then_attention_matches_cpu_layer(dev):
     assert_argmax_agrees(got, want)
 
 
+
+LOG2E_F32 = np.float32(1.4426950408889634)
+
+
+@pytest.mark.parametrize("pos0,nt,hd", [(0, 64, 256), (4096, 64, 256), (100, 3, 256), (7, 5, 128)])
+def test_prep_q16_equals_prep_and_operand_rounding(dev, pos0, nt, hd):
+    """it_attn_prep_f16_q16 leaves q, K and V exactly as it_attn_prep_f16 does, and its q16 is the f16
+    rounding (RNE) of q' * (scale * log2 e), the product taken in f32: the flash kernel's own
+    conversion of q, so the two attention paths get the same operand bits."""
+    nh, nkv = 16, 2
+    announce(f"prep q16 pos0={pos0} nt={nt} hd={hd}")
+    d = prep_inputs(50 + nt, nt, nh, nkv, hd)
+    scale = 1.0 / hd ** 0.5
+    res = []
+    for with16 in (False, True):
+        q = dev_f32(d["q"], dev)
+        kc = torch.zeros(pos0 + nt, nkv * hd, dtype=torch.int16, device=dev)
+        vc = torch.zeros_like(kc)
+        args = (q, dev_f32(d["k"], dev), dev_f32(d["v"], dev), kc, vc, pos0, nh, nkv)
+        qn, kn = dev_f32(d["q_norm"], dev), dev_f32(d["k_norm"], dev)
+        q16 = ops.attn_prep_f16_q16(*args, scale=scale, q_norm=qn, k_norm=kn) if with16 else \
+            ops.attn_prep_f16(*args, qn, kn)
+        res.append((host(q), host(kc), host(vc), host(q16) if with16 else None))
+    for a, b in zip(res[0][:3], res[1][:3]):
+        np.testing.assert_array_equal(a, b)
+    qpart = res[1][0].reshape(nt, nh, 2 * hd)[:, :, :hd]
+    want = (qpart * (np.float32(scale) * LOG2E_F32)).astype(np.float16)
+    np.testing.assert_array_equal(res[1][3].view(np.uint16).reshape(nt, nh, hd), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("pos0", [0, 300, 4096])
+def test_prep_q16_then_attention_equals_prep_then_attention(dev, pos0):
+    """A 64-token prefill chunk through it_attn_prep_f16_q16 + it_attn_f16_q16 gives the outputs of
+    it_attn_prep_f16 + it_attn_f16 bit for bit (one pass at 0 and 300, key splits at 4096)."""
+    nh, nkv, hd, nt = 16, 2, 256, 64
+    announce(f"prep q16 + attn q16 pos0={pos0}")
+    rng = np.random.default_rng(9 + pos0)
+    old_k = f16_bits(rng.standard_normal((pos0, nkv * hd)).astype(np.float32))
+    old_v = f16_bits(rng.standard_normal((pos0, nkv * hd)).astype(np.float32))
+    d = prep_inputs(23, nt, nh, nkv, hd)
+    outs = []
+    for with16 in (False, True):
+        kc = torch.zeros(pos0 + nt, nkv * hd, dtype=torch.int16, device=dev)
+        vc = torch.zeros_like(kc)
+        if pos0:
+            kc[:pos0] = torch.from_numpy(old_k.view(np.int16)).to(dev)
+            vc[:pos0] = torch.from_numpy(old_v.view(np.int16)).to(dev)
+        q = dev_f32(d["q"], dev)
+        args = (q, dev_f32(d["k"], dev), dev_f32(d["v"], dev), kc, vc, pos0, nh, nkv)
+        qn, kn = dev_f32(d["q_norm"], dev), dev_f32(d["k_norm"], dev)
+        if with16:
+            q16 = ops.attn_prep_f16_q16(*args, scale=1.0 / 16, q_norm=qn, k_norm=kn)
+            outs.append(host(ops.attn_f16_q16(q, q16, kc, vc, pos0, nh, nkv)))
+        else:
+            ops.attn_prep_f16(*args, qn, kn)
+            outs.append(host(ops.attn_f16(q, kc, vc, pos0, nh, nkv)))
+    np.testing.assert_array_equal(outs[0], outs[1])
+
 def test_prep_rejects_bad_geometry(dev):
     from irontimber_amd._lib import ItError
     d = prep_inputs(1, 1, 16, 2, 256)
