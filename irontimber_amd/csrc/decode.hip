@@ -20,7 +20,9 @@
 //   P.V    : P (hi + lo f16 rows, as for q) goes to a small LDS plane in MFMA A layout (barrier B,
 //            which also covers V); wave w then owns output dims 64w..64w+63 for all 64 keys, and
 //            one more MFMA per k-step against a ones column gives it the full row sums.
-//   records: stored straight from the accumulators (no staging, no barrier).
+//   records: stored straight from the accumulators (no staging, no barrier), as the 260-word
+//            record or, for the wave merge inside it_attn_f16, the same values in the piece layout
+//            below.
 // Per tile that is two barriers. First tile: q and K go out first, the q planes are built while K
 // is in flight, then V goes out and the scores and softmax run while it lands; later tiles are
 // prefetched while P.V runs. MULTI = false (splits of one tile) declares a single V buffer, which
@@ -43,6 +45,18 @@ constexpr int PST = TK + 8;     // P plane row stride (halves): 144 bytes
 constexpr float LOG2E_F = 1.4426950408889634f;
 constexpr float LN2_F = 0.6931471805599453f;
 constexpr int COMB_SPL = 8;     // splits per merge split lane per batch of loads
+
+// Piece layout of the f32 split records (two-launch decode and verify whose merge is the wave
+// merge): the same values as the 260-word record, arranged for the merge, whose lane l reads split
+// l of one (row, 16-dim block). O goes into 64-byte pieces [rows][16 blocks][smax][16 floats], so
+// consecutive lanes read consecutive pieces, and {m, l} into [rows][smax] after them: 1032 bytes
+// per (row, split), against 64 lanes each reading a different 1040-byte record.
+__device__ __forceinline__ float* prec_o(float* part, int th, int db, int s, int smax) {
+    return part + ((size_t)(th * 16 + db) * smax + s) * 16;
+}
+__device__ __forceinline__ float* prec_h(float* part, int rows, int th, int s, int smax) {
+    return part + (size_t)rows * smax * 256 + 2 * ((size_t)th * smax + s);
+}
 
 // V tile chunk swizzle. The transpose read of one 16-lane group covers rows r0..r0+3 (r0 % 4 == 0)
 // x 32 bytes (two chunks of one 128-byte line); unswizzled, the four 512-byte-apart rows would hit
@@ -155,7 +169,7 @@ __device__ __forceinline__ u2 mb_load2(MbRsrc r, int idx) {
 // the scores wait for K only. Decode at ctx 8192: partial kernel 5.95 -> 5.65 us, layer 9.41 ->
 // 9.13 us; with few workgroups (ctx 512, 16 of them) the copy is faster (6.09 against 6.27 us per
 // layer), so the launch takes VR from 64 workgroups up.
-template <int NB, bool MULTI, bool MB = false, bool VR = false>
+template <int NB, bool MULTI, bool MB = false, bool VR = false, bool CR = false>
 __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int qts, const uint16_t* __restrict__ kc,
                                                const uint16_t* __restrict__ vc, int kvd, int pos0, int nh, int nkv,
                                                int nt, float scale, float* __restrict__ part, int chunk, int smax,
@@ -385,6 +399,14 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
                         for (int k = 0; k < 2; ++k) mb_store1(mbr, mb_piece(th, 4 * w + 2 * k + hi, s, smax) + c, v[k]);
                         if (hi == (i & 1) && c < 4) mb_store2(mbr, mb_piece(th, 4 * w + c, s, smax) + 16, f2{mh[i] * LN2_F, ls});
                     }
+                } else if constexpr (CR) {
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        float* dst = prec_o(part, th, 4 * w + 2 * k + hi, s, smax) + c;
+                        if constexpr (NB >= 2) __builtin_nontemporal_store(v[k], dst);   // as below
+                        else *dst = v[k];
+                    }
+                    if (w == 0 && hdr) *(f2*)prec_h(part, nt * nh, th, s, smax) = f2{mh[i] * LN2_F, ls};
                 } else if constexpr (NB >= 2) {
                     // blocks of 16 or more rows (verify at nt = 4) store their records
                     // non-temporally: measured faster there (15.7 -> 14.6 us per layer), slower for
@@ -405,13 +427,13 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
     }
 }
 
-template <int NB, bool MULTI, bool VR = false>
+template <int NB, bool MULTI, bool VR = false, bool CR = false>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, int qts,
                                                           const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, int kvd, int pos0, int nh,
                                                           int nkv, int nt, float scale, float* __restrict__ part,
                                                           int chunk, int smax) {
-    decode_partial<NB, MULTI, false, VR>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax, blockIdx.x, blockIdx.y,
+    decode_partial<NB, MULTI, false, VR, CR>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, smax, blockIdx.x, blockIdx.y,
                        blockIdx.z);
 }
 
@@ -639,28 +661,40 @@ __device__ __forceinline__ void merge_wave_store(float gv, int nh, int t, int h,
 }
 
 // One wave merges the records of query row th (token t = th / nh, head h) for output dims
-// d0 .. d0+15; lane l = the wave's lane.
-template <int SPL>
+// d0 .. d0+15; lane l = the wave's lane. CR: the records in the piece layout.
+template <int SPL, bool CR>
 __device__ __forceinline__ void combine_wave_row(const float* __restrict__ q, int qts, int pos0, int nh, int nt,
                                                  const float* __restrict__ part, int chunk, int smax,
                                                  float* __restrict__ out, int ots, int th, int d0, int l) {
     if (th >= nt * nh) return;   // whole wave
     const int t = th / nh, h = th - t * nh;
     const int ns = (pos0 + t + chunk) / chunk;   // splits that hold keys <= pos0 + t
-    const float* base = part + (size_t)th * smax * PART;
     f2 hv[SPL];
     f4 ov[SPL][4];
+    if constexpr (CR) {
+        float* pp = const_cast<float*>(part);
 #pragma unroll
-    for (int j = 0; j < SPL; ++j) {
-        const float* rec = base + (size_t)min(l + 64 * j, ns - 1) * PART;
-        hv[j] = *(const f2*)rec;
+        for (int j = 0; j < SPL; ++j) {
+            const int sj = min(l + 64 * j, ns - 1);
+            hv[j] = *(const f2*)prec_h(pp, nt * nh, th, sj, smax);
+            const float* src = prec_o(pp, th, d0 >> 4, sj, smax);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) ov[j][k] = ld_f4(rec + 4 + d0 + 4 * k);
+            for (int k = 0; k < 4; ++k) ov[j][k] = ld_f4(src + 4 * k);
+        }
+    } else {
+        const float* base = part + (size_t)th * smax * PART;
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            const float* rec = base + (size_t)min(l + 64 * j, ns - 1) * PART;
+            hv[j] = *(const f2*)rec;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ov[j][k] = ld_f4(rec + 4 + d0 + 4 * k);
+        }
     }
     merge_wave_store<SPL>(merge_gate(q, qts, t, h, d0, l), nh, t, h, ns, hv, ov, out, ots, d0, l);
 }
 
-template <int SPL>
+template <int SPL, bool CR = false>
 __global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __restrict__ q, int qts, int pos0,
                                                                 int nh, int nt, const float* __restrict__ part,
                                                                 int chunk, int smax, float* __restrict__ out,
@@ -677,7 +711,7 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __r
         row = blockIdx.x >> 2;
         quarter = blockIdx.x & 3;
     }
-    combine_wave_row<SPL>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots, row,
+    combine_wave_row<SPL, CR>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots, row,
                           16 * (4 * quarter + (threadIdx.x >> 6)), threadIdx.x & 63);
 }
 
@@ -793,9 +827,14 @@ __global__ __launch_bounds__(256) void mailbox_fill_kernel(uint32_t* p, size_t w
         __hip_atomic_store(report, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+bool piece_records(int pos0, int nt, int nh, int chunk) {
+    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    return smax > 16 && smax <= 256 && (long)nt * nh <= 256;   // the wave-merge cases of launch_attn_combine
+}
+
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd,
                                        int pos0, int nh, int nkv, int nt, float scale, float* part, int chunk,
-                                       hipStream_t st) {
+                                       hipStream_t st, bool pieces) {
     const int G = nh / nkv, R = nt * G;
     const int smax = (pos0 + nt + chunk - 1) / chunk;
     // one tile per split (chunk <= 64 keys) needs one V buffer, so two or three workgroups share a
@@ -806,17 +845,21 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
     const bool multi = chunk > TK;
     const int rows = multi ? (R <= 8 ? 8 : R <= 16 ? 16 : R <= 24 ? 24 : 32) : (R <= 16 ? 8 : R <= 32 ? 16 : 32);
     const dim3 grid(smax, nkv, (R + rows - 1) / rows);
-#define IT_DECODE_LAUNCH(NB_)                                                                                         \
-    (multi ? attn_decode_kernel<NB_, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, \
-                                                                chunk, smax)                                        \
-           : attn_decode_kernel<NB_, false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, \
-                                                                 chunk, smax))
+#define IT_DECODE_LAUNCH2(NB_, CR_)                                                                                   \
+    (multi ? attn_decode_kernel<NB_, true, false, CR_><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt,     \
+                                                                            scale, part, chunk, smax)                   \
+           : attn_decode_kernel<NB_, false, false, CR_><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt,    \
+                                                                             scale, part, chunk, smax))
+#define IT_DECODE_LAUNCH(NB_) (pieces ? IT_DECODE_LAUNCH2(NB_, true) : IT_DECODE_LAUNCH2(NB_, false))
     // decode rows (one block of 8) over 64 or more workgroups load V into registers (see
     // decode_partial); verify blocks measured equal either way and keep the copy
     const bool vr = !multi && rows == 8 && (long)grid.x * grid.y * grid.z >= 64;
     switch (rows / 8) {
         case 1:
-            if (vr)
+            if (vr && pieces)
+                attn_decode_kernel<1, false, true, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt,
+                                                                              scale, part, chunk, smax);
+            else if (vr)
                 attn_decode_kernel<1, false, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale,
                                                                         part, chunk, smax);
             else
@@ -827,6 +870,7 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
         default: IT_DECODE_LAUNCH(4); break;
     }
 #undef IT_DECODE_LAUNCH
+#undef IT_DECODE_LAUNCH2
     return hipGetLastError();
 }
 
@@ -896,8 +940,18 @@ hipError_t launch_mailbox_fill(void* mb, size_t bytes, uint32_t* report, hipStre
 }
 
 hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
-                               float* out, int ots, hipStream_t st) {
+                               float* out, int ots, hipStream_t st, bool pieces) {
     const int smax = (pos0 + nt + chunk - 1) / chunk;
+    if (pieces) {   // piece_records() holds: 16 < smax <= 256, at most 256 rows
+        const unsigned wgs = (unsigned)(((long)nt * nh * 16 + 3) / 4);
+        if (smax <= 64)
+            attn_combine_wave_kernel<1, true><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+        else if (smax <= 128)
+            attn_combine_wave_kernel<2, true><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+        else
+            attn_combine_wave_kernel<4, true><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+        return hipGetLastError();
+    }
     const unsigned wgs = (unsigned)(((long)nt * nh * 16 + 3) / 4);   // 4 waves each
     // the wave merge for the few rows of decode and verify; the workgroup merge (fewer, longer
     // waves) for the many rows of a prefill chunk
@@ -939,9 +993,10 @@ hipError_t launch_attn_combine_q16(const float* q, int qts, const float* part, i
 hipError_t launch_attn_splitk(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
                               int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
                               hipStream_t st) {
-    hipError_t e = launch_attn_partials(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, st);
+    const bool cr = piece_records(pos0, nt, nh, chunk);
+    hipError_t e = launch_attn_partials(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, st, cr);
     if (e != hipSuccess) return e;
-    return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
+    return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st, cr);
 }
 
 }  // namespace it

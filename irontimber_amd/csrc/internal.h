@@ -17,10 +17,15 @@ hipError_t launch_attn_prep_f32kv(float* q, int qts, const float* k, const float
                                   int nkv, int nt, int n_rot, float tsc, const int* sec, hipStream_t st);
 hipError_t launch_attn_f32kv(const float* q, int qts, const float* kc, const float* vc, int kvd, int pos0, int nh,
                              int nkv, int nt, float scale, float* out, int ots, float* part, int chunk, hipStream_t st);
+// pieces: the split records in decode.hip's piece layout (for the wave merge only: piece_records());
+// false: the 260-word f32 records {m, l, 0, 0, o[256]} that it_attn_partials / it_attn_combine
+// exchange
+bool piece_records(int pos0, int nt, int nh, int chunk);
 hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
-                                int nh, int nkv, int nt, float scale, float* part, int chunk, hipStream_t st);
+                                int nh, int nkv, int nt, float scale, float* part, int chunk, hipStream_t st,
+                                bool pieces = false);
 hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
-                               float* out, int ots, hipStream_t st);
+                               float* out, int ots, hipStream_t st, bool pieces = false);
 // Key-split flash records in the compact form: {m, l, k, 0} + 256 int16 (O in units of k).
 constexpr int FLASH_REC = 4 + 128;
 // log2(e): the flash kernel works in log2 units (its q operand is q * scale * LOG2E)

@@ -267,6 +267,52 @@ def test_two_phase_abi_equals_single_call(dev):
     np.testing.assert_array_equal(host(out), ref)
 
 
+def _two_phase_f32(dev, qd, kc, vc, pos0, nt, nh, nkv, chunk):
+    """it_attn_partials + it_attn_combine: the split-K path with the 260-word f32 records."""
+    from irontimber_amd._lib import call
+    nbytes = ops.attn_scratch_bytes(pos0, nt, nh, nkv, 256, ops.KERNEL_SPLITK, chunk)
+    part = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(nt, nh * 256, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    call("it_attn_partials", qd.data_ptr(), nh * 512, kc.data_ptr(), vc.data_ptr(), nkv * 256, pos0, 256, nh, nkv,
+         nt, 1 / 16, part.data_ptr(), nbytes, chunk, s)
+    call("it_attn_combine", qd.data_ptr(), nh * 512, part.data_ptr(), pos0, 256, nh, nt, chunk, out.data_ptr(),
+         nh * 256, s)
+    return host(out)
+
+
+@pytest.mark.parametrize("ctx,nt", [(1100, 1), (4096, 2), (8192, 1), (8192, 4), (16384, 1)])
+def test_piece_records_equal_f32_records(dev, ctx, nt):
+    """Decode and verify calls of it_attn_f16 whose merge is the wave merge (17-256 splits, at most
+    256 rows) lay their split records out in 64-byte pieces per (row, 16-dim block, split): the
+    same f32 values merged in the same order, so the output equals it_attn_partials +
+    it_attn_combine (the 260-word records) bit for bit, at the oracle's bar."""
+    nh, nkv, pos0 = 16, 2, ctx - nt
+    announce(f"piece records ctx={ctx} nt={nt}")
+    q, kb, vb = attn_inputs(70 + ctx + nt, ctx=ctx, nt=nt, nh=nh, nkv=nkv)
+    qd, kc, vc = dev_f32(q.reshape(nt, -1), dev), dev_f16bits(kb, dev), dev_f16bits(vb, dev)
+    got = host(ops.attn_f16(qd, kc, vc, pos0, nh, nkv, kernel=ops.KERNEL_SPLITK, chunk=64))
+    np.testing.assert_array_equal(got, _two_phase_f32(dev, qd, kc, vc, pos0, nt, nh, nkv, 64))
+    want = oracle.attn(q.reshape(nt, -1), kb, vb, pos0, nh, nkv)
+    assert np.isfinite(got).all() and np.abs(got - want).max() <= TOL
+    assert assert_argmax_agrees(got, want) == 0
+
+
+@pytest.mark.parametrize("bad", [float("nan"), float("inf")])
+def test_piece_records_nonfinite(dev, bad):
+    """A NaN or infinite V value at ctx 8192 (piece-layout records, wave merge): every row that sees
+    the key gets a non-finite output in that dim, the other KV head stays finite."""
+    nh, nkv, nt, ctx = 16, 2, 1, 8192
+    announce(f"piece records nonfinite bad={bad}")
+    q, kb, vb = attn_inputs(9, ctx=ctx, nt=nt, nh=nh, nkv=nkv)
+    vb = vb.copy()
+    vb[5000, 3] = np.float16(bad).view(np.uint16)   # dim 3 of KV head 0
+    got = host(ops.attn_f16(dev_f32(q.reshape(nt, -1), dev), dev_f16bits(kb, dev), dev_f16bits(vb, dev), ctx - nt,
+                            nh, nkv)).reshape(nh, 256)
+    assert not np.isfinite(got[:nh // nkv, 3]).any()
+    assert np.isfinite(got[nh // nkv:]).all()
+
+
 @pytest.mark.parametrize("pos0,nt,cap", [(3968, 64, 8192), (4032, 64, 8192), (8128, 64, 8192), (3977, 64, 4041),
                                          (245, 13, 258), (8188, 4, 8192), (4096, 64, 0), (7680, 512, 8192),
                                          (7000, 300, 7300)])
