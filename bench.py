@@ -118,7 +118,7 @@ def measure_decode_traffic():
     """HBM bytes per launch of the ctx-8192 partial kernel: FETCH_SIZE and WRITE_SIZE medians, each
     scaled by what the same counter reads for a plain 256 MiB device copy. Returns (bytes, note)."""
     dec = ["--only", "decode", "--no-cpu", "--steps", "20", "--warmup", "2"]
-    kern, grid = "void it::attn_decode_kernel<1, false, true>", str(32768 * 2)
+    kern, grid = "void it::attn_decode_kernel<1, false, true, true>", str(32768 * 2)
     got = {}
     for key, counter, args, k, g in (("fetch", "FETCH_SIZE", dec, kern, grid),
                                      ("write", "WRITE_SIZE", dec, kern, grid),
@@ -209,9 +209,12 @@ def main():
                  ops.KERNEL_AUTO if nt > 1 or not args.decode_chunk else ops.KERNEL_SPLITK, 0 if nt > 1 else args.decode_chunk,
                  stream_of())
 
+        rec_layout = 1 if 16 < -(-ctx // chunk) <= 256 else 0   # as it_attn_f16 picks for one token
+        # the headline layer's partial kernel alone: record layout 1 is the one it_attn_f16 writes for
+        # its wave merge (same kernel instantiation as inside decode_step)
         def decode_partials(i):
-            call("it_attn_partials", q1.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(), KVD,
-                 ctx - 1, HD, NH, NKV, 1, scale, part.data_ptr(), part.numel(), chunk, stream_of())
+            call("it_attn_partials_ex", q1.data_ptr(), NH * 2 * HD, kcs[i % NSETS].data_ptr(), vcs[i % NSETS].data_ptr(),
+                 KVD, ctx - 1, HD, NH, NKV, 1, scale, part.data_ptr(), part.numel(), chunk, rec_layout, stream_of())
 
         # correctness guard on the benchmarked path (eager vs graph replays)
         decode_step(0)
@@ -719,7 +722,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": rnd(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": rnd(None if part_gbs is None else part_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_unit": "bytes per launch", "traffic_source": traffic_note,
-                     "kernel": "attn_decode_kernel<1, false, true>", "kernel_us": rnd(part_us, 3),
+                     "kernel": "attn_decode_kernel<1, false, true, true>", "kernel_us": rnd(part_us, 3),
                      "bytes_per_launch": dbytes},
         "roofline_prefill": {"bound": "mfma", "achieved": prefill_tflops, "peak": F16_MFMA_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": rnd(None if prefill_tflops is None else prefill_tflops / F16_MFMA_PEAK_TFLOPS, 4),

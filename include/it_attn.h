@@ -204,6 +204,23 @@ int it_attn_partials(const float* q, int q_tok_stride, const uint16_t* kc, const
 int it_attn_combine(const float* q, int q_tok_stride, const float* part, int pos0, int hd, int nh, int nt, int chunk,
                     float* out, int out_tok_stride, void* stream);
 
+/* The same two phases with a choice of record layout. layout 0: the 260-float records above (these
+ * calls are then it_attn_partials / it_attn_combine). layout 1: the records it_attn_f16 itself
+ * uses when its merge takes one wave per (token, head, 16 output dims), i.e. for 17-256 splits and
+ * at most 256 (token, head) rows (decode and verify at long contexts; other geometries are
+ * refused): the same f32 values, O as 64-byte pieces of 16 floats at
+ * part + (((t*nh + h)*16 + d/16)*smax + s)*16 (+ d % 16), then {m, l} at
+ * part + nt*nh*smax*256 + ((t*nh + h)*smax + s)*2, 1,032 bytes per (token, head, split) inside
+ * the same part_bytes. The merge's lanes, one split each, then read adjacent pieces, which makes
+ * the merge faster (ctx 8192: 8.45 against 9.0 us per layer); the output is bit-identical to
+ * layout 0. Extends the reference's attn_s_h / attn_comb pair (kernels/src/lib.rs:722-798), which
+ * has one layout only. */
+int it_attn_partials_ex(const float* q, int q_tok_stride, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0,
+                        int hd, int nh, int nkv, int nt, float scale, float* part, size_t part_bytes, int chunk,
+                        int layout, void* stream);
+int it_attn_combine_ex(const float* q, int q_tok_stride, const float* part, int pos0, int hd, int nh, int nt, int chunk,
+                       int layout, float* out, int out_tok_stride, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * The MTP head's attention over its own f32 KV cache (src/mtp.rs:96-130; src/vk/mod.rs:917-942).
  * Slot p of that cache holds position p + 1 (mtp.rs:120, vk/mod.rs:932).

@@ -37,6 +37,9 @@ SIGNATURES = {
     "it_attn_partials": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_size_t, c_int,
                                  P]),
     "it_attn_combine": (c_int, [P, c_int, P, c_int, c_int, c_int, c_int, c_int, P, c_int, P]),
+    "it_attn_partials_ex": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, c_size_t,
+                                    c_int, c_int, P]),
+    "it_attn_combine_ex": (c_int, [P, c_int, P, c_int, c_int, c_int, c_int, c_int, c_int, P, c_int, P]),
     "it_gdn_conv": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
     "it_l2norm_heads": (c_int, [P, c_int, c_int, c_int, c_int, c_float, P]),
     "it_gdn_conv_l2norm": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, P]),

@@ -533,6 +533,38 @@ int it_attn_combine(const float* q, int qts, const float* part, int pos0, int hd
                  "it_attn_combine");
 }
 
+int it_attn_partials_ex(const float* q, int qts, const uint16_t* kc, const uint16_t* vc, int kvd, int pos0, int hd,
+                        int nh, int nkv, int nt, float scale, float* part, size_t part_bytes, int chunk, int layout,
+                        void* stream) {
+    if (layout == 0) return it_attn_partials(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, scale, part, part_bytes, chunk, stream);
+    if (layout != 1) return fail("it_attn_partials_ex: unknown record layout %d (0 or 1)", layout);
+    if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, q, qts)) return -1;
+    if (chunk <= 0 || chunk % 64 != 0) return fail("it_attn_partials_ex: chunk %d must be a positive multiple of 64", chunk);
+    if (!it::piece_records(pos0, nt, nh, chunk))
+        return fail("it_attn_partials_ex: record layout 1 needs 17-256 splits and at most 256 (token, head) rows");
+    const size_t need = splitk_scratch(pos0, nt, nh, chunk);
+    if (!part || part_bytes < need) return fail("it_attn_partials_ex: %zu bytes of partials < %zu required", part_bytes, need);
+    if (!aligned16(part)) return fail("it_attn_partials_ex: part must be 16-byte aligned");
+    return check(it::launch_attn_partials(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, scale, part, chunk, (hipStream_t)stream,
+                                          true),
+                 "it_attn_partials_ex");
+}
+
+int it_attn_combine_ex(const float* q, int qts, const float* part, int pos0, int hd, int nh, int nt, int chunk, int layout,
+                       float* out, int ots, void* stream) {
+    if (layout == 0) return it_attn_combine(q, qts, part, pos0, hd, nh, nt, chunk, out, ots, stream);
+    if (layout != 1) return fail("it_attn_combine_ex: unknown record layout %d (0 or 1)", layout);
+    if (hd != HD || nh <= 0 || nt <= 0 || pos0 < 0) return fail("it_attn_combine_ex: bad geometry");
+    if (chunk <= 0 || chunk % 64 != 0) return fail("it_attn_combine_ex: chunk %d must be a positive multiple of 64", chunk);
+    if (!it::piece_records(pos0, nt, nh, chunk))
+        return fail("it_attn_combine_ex: record layout 1 needs 17-256 splits and at most 256 (token, head) rows");
+    if (!q || !part || !out || !aligned16(q) || !aligned16(part) || !aligned16(out))
+        return fail("it_attn_combine_ex: buffers must be non-null and 16-byte aligned");
+    if (qts % 4 != 0 || ots % 4 != 0) return fail("it_attn_combine_ex: token strides must be multiples of 4");
+    return check(it::launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, (hipStream_t)stream, true),
+                 "it_attn_combine_ex");
+}
+
 int it_gdn_conv(const float* x, int xts, const float* w, float* state, float* out, int ots, int cd, int nt, int K,
                 void* stream) {
     if (K < 2 || K > 4) return fail("it_gdn_conv: kernel size %d unsupported (2..4)", K);

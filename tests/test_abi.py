@@ -132,6 +132,28 @@ def test_q16_entries_reject_bad_arguments_before_device_work():
     assert prep(scale=0.0) != 0 and "scale" in _lib.last_error()
     assert prep(rm=2) != 0 and "round_mode" in _lib.last_error()
 
+def test_record_layout_entries_reject_bad_arguments_before_device_work():
+    """it_attn_partials_ex / it_attn_combine_ex: an unknown layout, or the piece layout (1) for a
+    geometry whose merge is not the wave merge (at most 16 splits, or more than 256 rows), fails
+    before any launch."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    big = 1 << 30
+
+    def part(layout, pos0=8191, nt=1, chunk=64):
+        return lib.it_attn_partials_ex(fake, 8192, fake, fake, 512, pos0, 256, 16, 2, nt, 0.0625, fake, big, chunk,
+                                       layout, None)
+
+    def comb(layout, pos0=8191, nt=1, chunk=64):
+        return lib.it_attn_combine_ex(fake, 8192, fake, pos0, 256, 16, nt, chunk, layout, fake, 4096, None)
+    for f in (part, comb):
+        assert f(2) != 0 and "layout" in _lib.last_error()
+        assert f(1, pos0=511) != 0 and "17-256 splits" in _lib.last_error()      # 8 splits
+        assert f(1, pos0=8192 * 4) != 0 and "17-256 splits" in _lib.last_error()  # 513 splits
+        assert f(1, pos0=8128, nt=64) != 0 and "256" in _lib.last_error()         # 1024 rows
+        assert f(1, chunk=96) != 0 and "multiple of 64" in _lib.last_error()
+
+
 def test_scratch_bytes_policy():
     lib = _lib.lib()
     # decode: split-K, C = 64 -> 128 splits of 260 words per head

@@ -248,6 +248,40 @@ def test_decode_sequence_matches_block(dev):
         np.testing.assert_allclose(one[0], block[t], atol=1e-6)
 
 
+@pytest.mark.parametrize("ctx,nt", [(8192, 1), (8192, 4), (2048, 2)])
+def test_two_phase_piece_layout_equals_single_call(dev, ctx, nt):
+    """it_attn_partials_ex + it_attn_combine_ex with record layout 1 (the pieces it_attn_f16 uses
+    for its wave merge) == it_attn_f16 bit for bit, and the records sit where the header says: the
+    {m, l} pair of (t, h, s) equals the 260-word record's, piece (t, h, d/16, s) its o[d]."""
+    from irontimber_amd._lib import call
+    nh, nkv, chunk, pos0 = 16, 2, 64, ctx - nt
+    announce(f"two-phase piece layout ctx={ctx} nt={nt}")
+    q, kb, vb = attn_inputs(7, ctx=ctx, nt=nt)
+    qd, kc, vc = dev_f32(q.reshape(nt, -1), dev), dev_f16bits(kb, dev), dev_f16bits(vb, dev)
+    ref = host(ops.attn_f16(qd, kc, vc, pos0, nh, nkv, kernel=ops.KERNEL_SPLITK, chunk=chunk))
+    nbytes = ops.attn_scratch_bytes(pos0, nt, nh, nkv, 256, ops.KERNEL_SPLITK, chunk)
+    s = torch.cuda.current_stream().cuda_stream
+    recs = []
+    for layout in (0, 1):
+        part = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
+        out = torch.empty(nt, nh * 256, device=dev)
+        call("it_attn_partials_ex", qd.data_ptr(), nh * 512, kc.data_ptr(), vc.data_ptr(), nkv * 256, pos0, 256, nh,
+             nkv, nt, 1 / 16, part.data_ptr(), nbytes, chunk, layout, s)
+        call("it_attn_combine_ex", qd.data_ptr(), nh * 512, part.data_ptr(), pos0, 256, nh, nt, chunk, layout,
+             out.data_ptr(), nh * 256, s)
+        np.testing.assert_array_equal(host(out), ref)
+        recs.append(host(part))
+    smax, rows = -(-ctx // chunk), nt * nh
+    r0 = recs[0][:rows * smax * 260].reshape(rows, smax, 260)
+    o1 = recs[1][:rows * smax * 256].reshape(rows, 16, smax, 16)
+    h1 = recs[1][rows * smax * 256:rows * smax * 258].reshape(rows, smax, 2)
+    for t in range(nt):   # splits token t sees (the others are never read)
+        ns = (pos0 + t + chunk) // chunk
+        th = slice(t * nh, (t + 1) * nh)
+        np.testing.assert_array_equal(h1[th, :ns], r0[th, :ns, :2])
+        np.testing.assert_array_equal(o1[th, :, :ns].transpose(0, 2, 1, 3).reshape(nh, ns, 256), r0[th, :ns, 4:])
+
+
 def test_two_phase_abi_equals_single_call(dev):
     """it_attn_partials + it_attn_combine (the exchangeable split-K records) == it_attn_f16."""
     from irontimber_amd._lib import call
