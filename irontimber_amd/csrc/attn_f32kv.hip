@@ -57,7 +57,9 @@ constexpr int F32KV_ROW = F32KV_HD + 4;                 // padded LDS row (float
 // is the fallback for a caller whose scratch cannot hold even one record per (token, head), the
 // role of the reference's whole-context `attn` kernel (kernels/src/lib.rs:83-116, chosen at
 // src/vk/mod.rs:740).
-template <int RB, bool DIRECT>
+// CR: the same values in the piece layout of common.h (decode and short verify calls whose merge is
+// the wave merge).
+template <int RB, bool DIRECT, bool CR = false>
 __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict__ q, int qts,
                                                          const float* __restrict__ kc, const float* __restrict__ vc,
                                                          int kvd, int pos0, int nh, int nkv, int nt, int tpw,
@@ -221,6 +223,14 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
             }
             continue;
         }
+        if constexpr (CR) {   // the piece layout: this lane's 16 dims are piece (row, 4w + lg)
+            const int th = tr * nh + hr;
+            float* pc = prec_o(part, th, 4 * w + lg, s, smax);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) *(f4*)(pc + 4 * i) = f4{acc[rb][0][i], acc[rb][1][i], acc[rb][2][i], acc[rb][3][i]};
+            if (w == 0 && lg == 0) *(f2*)prec_h(part, nt * nh, th, s, smax) = f2{m_run[rb] * 0.69314718055994530942f, l_run[rb]};
+            continue;
+        }
         float* rec = part + ((size_t)(tr * nh + hr) * smax + s) * 260;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -239,6 +249,8 @@ hipError_t launch_attn_f32kv(const float* q, int qts, const float* kc, const flo
     // two 16-row blocks per workgroup once a call has more rows than one block holds
     const int rb = nt * G > 16 ? 2 : 1;
     const int tpw = 16 * rb / G;
+    // the piece layout for the wave merge (one 16-row block: decode and short verify calls)
+    const bool pieces = !direct && rb == 1 && piece_records(pos0, nt, nh, chunk);
     const dim3 grid((unsigned)smax, (unsigned)nkv, (unsigned)((nt + tpw - 1) / tpw));
     if (rb == 2 && direct)
         attn_f32kv_kernel<2, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk,
@@ -249,12 +261,15 @@ hipError_t launch_attn_f32kv(const float* q, int qts, const float* kc, const flo
     else if (direct)
         attn_f32kv_kernel<1, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk,
                                                         smax, out, ots);
+    else if (pieces)
+        attn_f32kv_kernel<1, false, true><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part,
+                                                               chunk, smax, out, ots);
     else
         attn_f32kv_kernel<1, false><<<grid, 256, 0, st>>>(q, qts, kc, vc, kvd, pos0, nh, nkv, nt, tpw, qs, part, chunk,
                                                          smax, out, ots);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || direct) return e;
-    return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st);
+    return launch_attn_combine(q, qts, part, pos0, nh, nt, chunk, out, ots, st, pieces);
 }
 
 }  // namespace it

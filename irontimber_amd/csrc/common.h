@@ -150,6 +150,18 @@ __device__ __forceinline__ float sum_xor32(float v) { float a = v, b = v; swap32
 __device__ __forceinline__ float max_xor16(float v) { float a = v, b = v; swap16(a, b); return fmaxf(a, b); }
 __device__ __forceinline__ float sum_xor16(float v) { float a = v, b = v; swap16(a, b); return a + b; }
 
+// Piece layout of the f32 split-K records (two-launch decode and verify whose merge is the wave
+// merge, for the f16 and the f32 KV cache): the same values as the 260-word record, arranged for the merge, whose lane l reads split
+// l of one (row, 16-dim block). O goes into 64-byte pieces [rows][16 blocks][smax][16 floats], so
+// consecutive lanes read consecutive pieces, and {m, l} into [rows][smax] after them: 1032 bytes
+// per (row, split), against 64 lanes each reading a different 1040-byte record.
+__device__ __forceinline__ float* prec_o(float* part, int th, int db, int s, int smax) {
+    return part + ((size_t)(th * 16 + db) * smax + s) * 16;
+}
+__device__ __forceinline__ float* prec_h(float* part, int rows, int th, int s, int smax) {
+    return part + (size_t)rows * smax * 256 + 2 * ((size_t)th * smax + s);
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 // The same on the hardware exp2 and reciprocal (a few ulp, ~1e-7 relative): for epilogues that apply
 // the gate to many values per lane, where the accurate forms (~20 VALU ops each) dominate.

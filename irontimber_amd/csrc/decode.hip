@@ -46,18 +46,6 @@ constexpr float LOG2E_F = 1.4426950408889634f;
 constexpr float LN2_F = 0.6931471805599453f;
 constexpr int COMB_SPL = 8;     // splits per merge split lane per batch of loads
 
-// Piece layout of the f32 split records (two-launch decode and verify whose merge is the wave
-// merge): the same values as the 260-word record, arranged for the merge, whose lane l reads split
-// l of one (row, 16-dim block). O goes into 64-byte pieces [rows][16 blocks][smax][16 floats], so
-// consecutive lanes read consecutive pieces, and {m, l} into [rows][smax] after them: 1032 bytes
-// per (row, split), against 64 lanes each reading a different 1040-byte record.
-__device__ __forceinline__ float* prec_o(float* part, int th, int db, int s, int smax) {
-    return part + ((size_t)(th * 16 + db) * smax + s) * 16;
-}
-__device__ __forceinline__ float* prec_h(float* part, int rows, int th, int s, int smax) {
-    return part + (size_t)rows * smax * 256 + 2 * ((size_t)th * smax + s);
-}
-
 // V tile chunk swizzle. The transpose read of one 16-lane group covers rows r0..r0+3 (r0 % 4 == 0)
 // x 32 bytes (two chunks of one 128-byte line); unswizzled, the four 512-byte-apart rows would hit
 // the same banks. XOR-ing the chunk index with 2*(r & 3) moves the four rows to four different
