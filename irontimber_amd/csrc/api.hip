@@ -32,7 +32,7 @@ int check(hipError_t e, const char* what) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 constexpr int HD = 256;
-constexpr size_t PART_WORDS = 260;
+constexpr size_t PART_WORDS = it::idx::PART;
 constexpr int KERNEL_AUTO = 0, KERNEL_SPLITK = 1, KERNEL_FLASH = 2, KERNEL_FLASH_F32 = 3;
 constexpr size_t AUTO_SCRATCH_CAP = size_t(256) << 20;   // keep automatic split-K scratch under 256 MiB
 
@@ -56,7 +56,7 @@ int flash_chunk(int pos0, int nt, int nh, int nkv, int chunk) {
 }
 
 size_t splitk_scratch(int pos0, int nt, int nh, int chunk) {
-    const size_t smax = ((size_t)pos0 + nt + chunk - 1) / chunk;
+    const size_t smax = (size_t)it::idx::split_count((long)pos0 + nt, chunk);
     return (size_t)nt * nh * smax * PART_WORDS * sizeof(float);
 }
 
@@ -64,7 +64,7 @@ size_t splitk_scratch(int pos0, int nt, int nh, int chunk) {
 // int16) per (token, head, split), half the split-K kernel's 260-word f32 records.
 // With f32 records (kernel 3) the records are the split-K kernel's 260 words instead.
 size_t flash_scratch(int pos0, int nt, int nh, int chunk, bool f32rec = false) {
-    const size_t smax = ((size_t)pos0 + nt + chunk - 1) / chunk;
+    const size_t smax = (size_t)it::idx::split_count((long)pos0 + nt, chunk);
     return (size_t)nt * nh * smax * (f32rec ? PART_WORDS : (size_t)it::FLASH_REC) * sizeof(float);
 }
 

@@ -231,7 +231,7 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
             if (w == 0 && lg == 0) *(f2*)prec_h(part, nt * nh, th, s, smax) = f2{m_run[rb] * 0.69314718055994530942f, l_run[rb]};
             continue;
         }
-        float* rec = part + ((size_t)(tr * nh + hr) * smax + s) * 260;
+        float* rec = part + idx::rec(tr * nh + hr, s, smax) * idx::PART;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             *(f4*)(rec + 4 + 64 * w + 16 * lg + 4 * i) = f4{acc[rb][0][i], acc[rb][1][i], acc[rb][2][i], acc[rb][3][i]};
@@ -244,7 +244,7 @@ hipError_t launch_attn_f32kv(const float* q, int qts, const float* kc, const flo
     const int G = nh / nkv;
     const bool direct = chunk == 0;   // one pass over every key, output written directly, no records
     if (direct) chunk = pos0 + nt;
-    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    const int smax = idx::split_count((long)pos0 + nt, chunk);
     const float qs = scale * 1.44269504088896340736f;
     // two 16-row blocks per workgroup once a call has more rows than one block holds
     const int rb = nt * G > 16 ? 2 : 1;

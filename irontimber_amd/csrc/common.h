@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "rec_index.h"
+
 namespace it {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -151,15 +153,15 @@ __device__ __forceinline__ float max_xor16(float v) { float a = v, b = v; swap16
 __device__ __forceinline__ float sum_xor16(float v) { float a = v, b = v; swap16(a, b); return a + b; }
 
 // Piece layout of the f32 split-K records (two-launch decode and verify whose merge is the wave
-// merge, for the f16 and the f32 KV cache): the same values as the 260-word record, arranged for the merge, whose lane l reads split
-// l of one (row, 16-dim block). O goes into 64-byte pieces [rows][16 blocks][smax][16 floats], so
-// consecutive lanes read consecutive pieces, and {m, l} into [rows][smax] after them: 1032 bytes
-// per (row, split), against 64 lanes each reading a different 1040-byte record.
+// merge, for the f16 and the f32 KV cache): the same values as the 260-word record, arranged for
+// the merge, whose lane l reads split l of one (row, 16-dim block). O goes into 64-byte pieces
+// [rows][16 blocks][smax][16 floats], so consecutive lanes read consecutive pieces, and {m, l} into
+// [rows][smax] after them (rec_index.h: piece_o, piece_h).
 __device__ __forceinline__ float* prec_o(float* part, int th, int db, int s, int smax) {
-    return part + ((size_t)(th * 16 + db) * smax + s) * 16;
+    return part + idx::piece_o(th, db, s, smax);
 }
 __device__ __forceinline__ float* prec_h(float* part, int rows, int th, int s, int smax) {
-    return part + (size_t)rows * smax * 256 + 2 * ((size_t)th * smax + s);
+    return part + idx::piece_h(rows, th, s, smax);
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }

@@ -38,13 +38,13 @@ namespace it {
 namespace {
 
 constexpr int HD = 256;
-constexpr int PART = 260;
+constexpr int PART = idx::PART;
 constexpr int TK = 64;          // keys per tile
 constexpr int QST = HD + 8;     // q plane row stride (halves)
 constexpr int PST = TK + 8;     // P plane row stride (halves): 144 bytes
 constexpr float LOG2E_F = 1.4426950408889634f;
 constexpr float LN2_F = 0.6931471805599453f;
-constexpr int COMB_SPL = 8;     // splits per merge split lane per batch of loads
+constexpr int COMB_SPL = idx::COMB_SPL;   // splits per merge split lane per batch of loads
 
 // V tile chunk swizzle. The transpose read of one 16-lane group covers rows r0..r0+3 (r0 % 4 == 0)
 // x 32 bytes (two chunks of one 128-byte line); unswizzled, the four 512-byte-apart rows would hit
@@ -110,8 +110,8 @@ template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
 // initialised, so a buffer that never was (or was overwritten) fails loudly instead of passing its
 // stale words off as records; words 2-3 the address of a host-visible report word that a merge
 // which finds the mailbox poisoned sets to 1.
-constexpr int MB_PIECE = 24;        // floats per piece: o[16], {m, l}, unused; whole 32-byte sectors
-constexpr int MB_HEAD = 64;         // floats before the first piece
+constexpr int MB_PIECE = idx::MB_PIECE;   // floats per piece: o[16], {m, l}, unused; whole 32-byte sectors
+constexpr int MB_HEAD = idx::MB_HEAD;     // floats before the first piece
 constexpr uint32_t MB_EMPTY = 0xFFFFFFFFu;
 constexpr int MB_COHERENT = 16;     // buffer cache-policy bit: device-coherent access
 constexpr uint64_t MB_SPIN_TICKS = 1000000;   // 10 ms of the 100 MHz real-time counter
@@ -121,9 +121,7 @@ __device__ __forceinline__ MbRsrc mb_rsrc(float* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(p, 0, (int)bytes, 0x00020000);
 }
 // float index of piece (row th, dim block db, split s)
-__device__ __forceinline__ int mb_piece(int th, int db, int s, int smax) {
-    return MB_HEAD + ((th * 16 + db) * smax + s) * MB_PIECE;
-}
+__device__ __forceinline__ int mb_piece(int th, int db, int s, int smax) { return idx::mb_piece(th, db, s, smax); }
 // A record value is stored as a word that can never equal MB_EMPTY: any NaN (which could carry a
 // payload from a NaN in q, K or V, such as 0xFFFFFFFF) is written as the canonical quiet NaN, so a
 // non-finite input gives NaN outputs for that call instead of a piece that never looks complete.
@@ -399,12 +397,12 @@ __device__ __forceinline__ void decode_partial(const float* __restrict__ q, int 
                     // blocks of 16 or more rows (verify at nt = 4) store their records
                     // non-temporally: measured faster there (15.7 -> 14.6 us per layer), slower for
                     // decode (10.3 -> 11.1)
-                    float* rec = part + ((size_t)th * smax + s) * PART;
+                    float* rec = part + idx::rec(th, s, smax) * PART;
 #pragma unroll
                     for (int k = 0; k < 2; ++k) __builtin_nontemporal_store(v[k], rec + 4 + 64 * w + 16 * (2 * k + hi) + c);
                     if (w == 0 && hdr) __builtin_nontemporal_store(f4{mh[i] * LN2_F, ls, 0.f, 0.f}, (f4*)rec);
                 } else {
-                    float* rec = part + ((size_t)th * smax + s) * PART;
+                    float* rec = part + idx::rec(th, s, smax) * PART;
 #pragma unroll
                     for (int k = 0; k < 2; ++k) rec[4 + 64 * w + 16 * (2 * k + hi) + c] = v[k];
                     if (w == 0 && hdr) *(f4*)rec = f4{mh[i] * LN2_F, ls, 0.f, 0.f};
@@ -446,13 +444,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     __shared__ float red_d[SL];
     const int dq = blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int sg = tid / DLN, dl = tid % DLN, d0 = DW * dq + 4 * dl;
-    const int n = pos0 + t + 1, ns = (n + chunk - 1) / chunk;
-    const float* base = part + (size_t)(t * nh + h) * smax * RW;
+    const int ns = idx::splits_seen(pos0, t, chunk);
+    const float* base = part + idx::rec(t * nh + h, 0, smax) * RW;
     const f4 gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + d0);
     float M = -INFINITY, den = 0.f;
     f4 o = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < ns; s0 += SL * COMB_SPL) {
-        const int nb = min(COMB_SPL, (ns - s0 - sg + SL - 1) / SL);   // this lane's splits in the batch
+        const int nb = idx::comb_count(ns, s0, sg, SL);   // this lane's splits in the batch
         f2 hv[COMB_SPL];
         f4 ov[COMB_SPL];
         float kv[COMB_SPL];
@@ -464,7 +462,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
         for (int j = 0; j < COMB_SPL; ++j) {
             // a lane with no split left in the batch (nb <= 0) reloads split ns - 1: every index
             // stays inside this row's records, so a buffer sized exactly for them is never overrun
-            const float* rec = base + (size_t)min(s0 + sg + SL * max(0, min(j, nb - 1)), ns - 1) * RW;
+            const float* rec = base + (size_t)idx::comb_split(s0, sg, SL, j, nb, ns) * RW;
             hv[j] = *(const f2*)rec;
             if (Q16) {
                 kv[j] = rec[2];
@@ -534,14 +532,14 @@ __global__ __launch_bounds__(256) void attn_combine_row_kernel(const float* __re
     if (row >= nt * nh) return;
     const int l = threadIdx.x & 63;
     const int t = row / nh, h = row - t * nh;
-    const int ns = (pos0 + t + chunk) / chunk;   // splits holding keys <= pos0 + t (1 .. smax)
-    const float* base = part + (size_t)row * smax * RW;
-    const f4 hl = *(const f4*)(base + (size_t)min(l, ns - 1) * RW);   // lane l: header of split l
+    const int ns = idx::splits_seen(pos0, t, chunk);   // splits holding keys <= pos0 + t (1 .. smax)
+    const float* base = part + idx::rec(row, 0, smax) * RW;
+    const f4 hl = *(const f4*)(base + (size_t)idx::row_split(l, ns) * RW);   // lane l: header of split l
     f4 ov[NS];
     u2 qv[NS];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const float* rec = base + (size_t)min(j, ns - 1) * RW;
+        const float* rec = base + (size_t)idx::row_split(j, ns) * RW;
         if constexpr (Q16) qv[j] = *((const u2*)(rec + 4) + l);
         else ov[j] = ld_f4(rec + 4 + 4 * l);
     }
@@ -656,24 +654,24 @@ __device__ __forceinline__ void combine_wave_row(const float* __restrict__ q, in
                                                  float* __restrict__ out, int ots, int th, int d0, int l) {
     if (th >= nt * nh) return;   // whole wave
     const int t = th / nh, h = th - t * nh;
-    const int ns = (pos0 + t + chunk) / chunk;   // splits that hold keys <= pos0 + t
+    const int ns = idx::splits_seen(pos0, t, chunk);   // splits that hold keys <= pos0 + t
     f2 hv[SPL];
     f4 ov[SPL][4];
     if constexpr (CR) {
         float* pp = const_cast<float*>(part);
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
-            const int sj = min(l + 64 * j, ns - 1);
+            const int sj = idx::wave_split(l, j, ns);
             hv[j] = *(const f2*)prec_h(pp, nt * nh, th, sj, smax);
             const float* src = prec_o(pp, th, d0 >> 4, sj, smax);
 #pragma unroll
             for (int k = 0; k < 4; ++k) ov[j][k] = ld_f4(src + 4 * k);
         }
     } else {
-        const float* base = part + (size_t)th * smax * PART;
+        const float* base = part + idx::rec(th, 0, smax) * PART;
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
-            const float* rec = base + (size_t)min(l + 64 * j, ns - 1) * PART;
+            const float* rec = base + (size_t)idx::wave_split(l, j, ns) * PART;
             hv[j] = *(const f2*)rec;
 #pragma unroll
             for (int k = 0; k < 4; ++k) ov[j][k] = ld_f4(rec + 4 + d0 + 4 * k);
@@ -712,7 +710,7 @@ __device__ __forceinline__ void mailbox_merge(const float* __restrict__ q, int q
                                               int smax, MbRsrc r, float* __restrict__ out, int ots, int th, int db,
                                               int l) {
     const int t = th / nh, h = th - t * nh, d0 = 16 * db;
-    const int ns = (pos0 + t + chunk) / chunk;
+    const int ns = idx::splits_seen(pos0, t, chunk);
     f2 hv[SPL];
     f4 ov[SPL][4];
     bool ok[SPL];
@@ -816,7 +814,7 @@ __global__ __launch_bounds__(256) void mailbox_fill_kernel(uint32_t* p, size_t w
 }
 
 bool piece_records(int pos0, int nt, int nh, int chunk) {
-    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    const int smax = idx::split_count((long)pos0 + nt, chunk);
     return smax > 16 && smax <= 256 && (long)nt * nh <= 256;   // the wave-merge cases of launch_attn_combine
 }
 
@@ -824,7 +822,7 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
                                        int pos0, int nh, int nkv, int nt, float scale, float* part, int chunk,
                                        hipStream_t st, bool pieces) {
     const int G = nh / nkv, R = nt * G;
-    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    const int smax = idx::split_count((long)pos0 + nt, chunk);
     // one tile per split (chunk <= 64 keys) needs one V buffer, so two or three workgroups share a
     // CU; verify rows are then spread over more workgroups (8 rows each up to 16 rows, 16 rows up to
     // 32: measured best at nt = 2 and nt = 4), with the K/V tile of a split read by each of them
@@ -863,7 +861,7 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
 }
 
 size_t mailbox_bytes(long ctx, int nt, int nh) {
-    const long smax = (ctx + TK - 1) / TK;
+    const long smax = idx::split_count(ctx, TK);
     return 4 * ((size_t)MB_HEAD + (size_t)nt * nh * 16 * smax * MB_PIECE);
 }
 
@@ -893,7 +891,7 @@ hipError_t launch_attn_decode_mailbox(const float* q, int qts, const uint16_t* k
     *launched = false;
     const int G = nh / nkv, R = nt * G;
     const long total = (long)pos0 + nt;
-    const int smax = (int)((total + TK - 1) / TK);
+    const int smax = idx::split_count(total, TK);
     const size_t need = mailbox_bytes(total, nt, nh);
     // one group of at most 8 rows (decode): with more rows the merging waves wait beside
     // workgroups still computing, and two launches measured faster (nt = 2: 12.1 against 13.8 us,
@@ -929,7 +927,7 @@ hipError_t launch_mailbox_fill(void* mb, size_t bytes, uint32_t* report, hipStre
 
 hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                float* out, int ots, hipStream_t st, bool pieces) {
-    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    const int smax = idx::split_count((long)pos0 + nt, chunk);
     if (pieces) {   // piece_records() holds: 16 < smax <= 256, at most 256 rows
         const unsigned wgs = (unsigned)(((long)nt * nh * 16 + 3) / 4);
         if (smax <= 64)
@@ -965,7 +963,7 @@ hipError_t launch_attn_combine(const float* q, int qts, const float* part, int p
 
 hipError_t launch_attn_combine_q16(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                    float* out, int ots, hipStream_t st) {
-    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    const int smax = idx::split_count((long)pos0 + nt, chunk);
     const unsigned rwgs = (unsigned)(((long)nt * nh + 3) / 4);   // one wave per row
     if (smax <= 8)
         attn_combine_row_kernel<8, true><<<rwgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);

@@ -376,14 +376,14 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         // f32 records of (token, head, split), 260 words each: {m, l, 0, 0}, then O
         if (l < nrow) {
             const int tl = (rw + l) / G, gl = rw + l - tl * G;
-            float* rec = part + ((size_t)(tl * nh + kh * G + gl) * smax + split) * 260;
+            float* rec = part + idx::rec(tl * nh + kh * G + gl, split, smax) * idx::PART;
             __builtin_nontemporal_store(f4{ml[w][0][l] * 0.6931471805599453f, ml[w][1][l], 0.f, 0.f}, (f4*)rec);
         }
-        size_t ridx = (size_t)(tq * nh + kh * G + gq) * smax + split;
+        size_t ridx = idx::rec(tq * nh + kh * G + gq, split, smax);
         const size_t rnext = (size_t)(nh - G + 1) * smax;
         for (int i = 0; i < nrow; ++i) {
             const f4 ov = *(const f4*)(os + i * HD + 4 * (l ^ i));
-            __builtin_nontemporal_store(ov, (f4*)(part + uniform_off(ridx * 260 + 4)) + l);
+            __builtin_nontemporal_store(ov, (f4*)(part + uniform_off(ridx * idx::PART + 4)) + l);
             if (++gq == G) { gq = 0; ridx += rnext; } else { ridx += smax; }
         }
         return;
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         // c + 32 both hold row c's maximum), so a row costs a few vector instructions.
         if (l < nrow) {
             const int tl = (rw + l) / G, gl = rw + l - tl * G;
-            float* rec = part + ((size_t)(tl * nh + kh * G + gl) * smax + split) * FLASH_REC;
+            float* rec = part + idx::rec(tl * nh + kh * G + gl, split, smax) * FLASH_REC;
             __builtin_nontemporal_store(f4{ml[w][0][l] * 0.6931471805599453f, ml[w][1][l], ml[w][2][l] * (1.0f / 32767.0f), 0.f},
                                         (f4*)rec);
         }
@@ -412,7 +412,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         for (int i = 0; i < 32; ++i) ov[i] = *(const f4*)(os + i * HD + 4 * (l ^ i));
         // record index of row rw + i, walked in scalar registers: +smax within a token, and past
         // the other KV heads' q-heads at a token boundary
-        size_t ridx = (size_t)(tq * nh + kh * G + gq) * smax + split;
+        size_t ridx = idx::rec(tq * nh + kh * G + gq, split, smax);
         const size_t rnext = (size_t)(nh - G + 1) * smax;
         auto put = [&](int i) {
             u2* dst = (u2*)(part + uniform_off(ridx * FLASH_REC + 4));
@@ -488,7 +488,7 @@ hipError_t launch_attn_flash_split(const float* q, int qts, const uint16_t* kc, 
                                    int nh, int nkv, int nt, float scale, float* out, int ots, float* part, int chunk,
                                    hipStream_t st, bool f32rec, const uint16_t* q16, int q16ts) {
     const int R = nt * (nh / nkv);
-    const int smax = (pos0 + nt + chunk - 1) / chunk;
+    const int smax = idx::split_count((long)pos0 + nt, chunk);
     const dim3 grid((R + BM - 1) / BM, nkv, smax);
     const _Float16* qh = (const _Float16*)q16;
 #define IT_FLASH_SPLIT(F32_, Q16_)                                                                                     \

@@ -4,6 +4,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "rec_index.h"
+
 namespace it {
 
 hipError_t launch_kv_append(const float* k, const float* v, int sts, uint16_t* kc, uint16_t* vc, int pos0, int nt,
@@ -27,7 +29,7 @@ hipError_t launch_attn_partials(const float* q, int qts, const uint16_t* kc, con
 hipError_t launch_attn_combine(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,
                                float* out, int ots, hipStream_t st, bool pieces = false);
 // Key-split flash records in the compact form: {m, l, k, 0} + 256 int16 (O in units of k).
-constexpr int FLASH_REC = 4 + 128;
+constexpr int FLASH_REC = idx::FLASH_REC;
 // log2(e): the flash kernel works in log2 units (its q operand is q * scale * LOG2E)
 constexpr float LOG2E = 1.4426950408889634f;
 hipError_t launch_attn_combine_q16(const float* q, int qts, const float* part, int pos0, int nh, int nt, int chunk,

@@ -1,81 +1,35 @@
-"""Index arithmetic of the merge kernels, walked on the CPU over many geometries: every record a
-merge loads lies inside its row's records (index < ns <= smax, so a scratch buffer sized exactly by
-it_attn_scratch_bytes is never overrun), and every valid split is merged exactly once. The same for
-the mailbox pieces of the one-launch decode against the byte size its buffer descriptor covers.
-Formulas follow irontimber_amd/csrc/decode.hip (attn_combine_kernel, combine_wave_row, mb_piece)."""
-import itertools
+"""Index arithmetic of the split records and the merges, checked on the compiled code: the kernels
+address every record, mailbox piece and merge load through irontimber_amd/csrc/rec_index.h, and
+tests/csrc/index_sweep.cpp compiles that same header for the host and walks it over many geometries
+(records inside the scratch the planner sizes, the piece layout one-to-one, every visible split
+merged exactly once, mailbox pieces disjoint and inside the buffer)."""
 import os
 import re
+import subprocess
 
-import pytest
-
-_SRC = open(os.path.join(os.path.dirname(__file__), "..", "irontimber_amd", "csrc", "decode.hip")).read()
-
-
-def _const(name):
-    return int(re.search(rf"constexpr int {name} = (\d+);", _SRC).group(1))
+ROOT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..")
+CSRC = os.path.join(ROOT, "irontimber_amd", "csrc")
 
 
-COMB_SPL = _const("COMB_SPL")   # splits per lane per batch of attn_combine_kernel
-MB_HEAD, MB_PIECE, TK = _const("MB_HEAD"), _const("MB_PIECE"), _const("TK")
+def test_index_sweep(tmp_path):
+    exe = tmp_path / "index_sweep"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-Wall", "-Werror", "-o", str(exe),
+                    os.path.join(ROOT, "tests", "csrc", "index_sweep.cpp")], check=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0 and res.stdout.startswith("ok"), res.stdout + res.stderr
+    assert int(res.stdout.split()[1]) > 1_000_000
 
 
-def combine_kernel_loads(ns, SL):
-    """(split index loaded, merged?) for every lane slot of attn_combine_kernel<SL>."""
-    out = []
-    for sg in range(SL):
-        for s0 in range(0, ns, SL * COMB_SPL):
-            nb = min(COMB_SPL, (ns - s0 - sg + SL - 1) // SL)
-            for j in range(COMB_SPL):
-                idx = min(s0 + sg + SL * max(0, min(j, nb - 1)), ns - 1)
-                out.append((idx, j < nb))
-    return out
-
-
-def wave_loads(ns, SPL):
-    out = []
-    for lane in range(64):
-        for j in range(SPL):
-            idx = min(lane + 64 * j, ns - 1)
-            out.append((idx, lane + 64 * j < ns))
-    return out
-
-
-@pytest.mark.parametrize("SL", [4, 16])
-def test_combine_kernel_indices(SL):
-    for ns in list(range(1, 300)) + [511, 512, 513, 1024, 4097]:
-        loads = combine_kernel_loads(ns, SL)
-        assert all(0 <= i < ns for i, _ in loads), (SL, ns)
-        merged = sorted(i for i, m in loads if m)
-        assert merged == list(range(ns)), (SL, ns)
-
-
-@pytest.mark.parametrize("SPL", [1, 2, 4])
-def test_wave_merge_indices(SPL):
-    for ns in range(1, 64 * SPL + 1):
-        loads = wave_loads(ns, SPL)
-        assert all(0 <= i < ns for i, _ in loads)
-        assert sorted(i for i, m in loads if m) == list(range(ns))
-
-
-def test_mailbox_piece_indices_inside_descriptor():
-    """mb_piece(th, db, s, smax) for every row, 16-dim block and visible split stays below the
-    float count it_attn_mailbox_bytes gives for the call (the buffer descriptor's range), and the
-    pieces of different (row, block, split) never overlap."""
-    for ctx, nt, nh in itertools.product([1, 63, 64, 65, 1000, 8192, 16384], [1, 2, 4, 8], [4, 16, 32]):
-        pos0 = ctx - nt
-        if pos0 < 0:
-            continue
-        smax = (ctx + TK - 1) // TK
-        words = MB_HEAD + nt * nh * 16 * smax * MB_PIECE
-        seen = set()
-        for th in range(nt * nh):
-            t = th // nh
-            ns = (pos0 + t + TK) // TK
-            assert ns <= smax
-            for db in range(16):
-                for s in range(ns):
-                    base = MB_HEAD + ((th * 16 + db) * smax + s) * MB_PIECE
-                    assert base + MB_PIECE <= words
-                    assert base not in seen
-                    seen.add(base)
+def test_kernels_use_the_shared_index_functions():
+    """No record, piece or merge-slot address is written out by hand in the kernels: the formulas
+    the sweep checks are the ones they run."""
+    for name in ("decode.hip", "attn_f32kv.hip", "flash.hip"):
+        src = open(os.path.join(CSRC, name)).read()
+        assert "idx::rec(" in src or name == "attn_f32kv.hip" and "idx::rec(" in src
+        assert not re.search(r"\* smax \+ s(plit)?\) \* (260|PART|FLASH_REC)", src), name
+        assert not re.search(r"min\(l \+ 64 \* j, ns - 1\)", src), name
+    dec = open(os.path.join(CSRC, "decode.hip")).read()
+    for fn in ("idx::wave_split(", "idx::row_split(", "idx::comb_split(", "idx::comb_count(", "idx::mb_piece(",
+               "idx::splits_seen("):
+        assert fn in dec, fn
+    assert "idx::piece_o(" in open(os.path.join(CSRC, "common.h")).read()
