@@ -431,12 +431,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
 // of them; the maxima and sums reduce through LDS.
 //   SL = 16: a quarter of the dims per workgroup (4 per row), for rows with many splits (decode).
 //   SL = 4 : the whole row per workgroup, for rows with at most 32 splits (chunked prefill).
-//   Q16: the flash key-split records ({m, l, k, 0}, then O as int16 in units of k; FLASH_REC words).
+//   Q16: the flash key-split records (O as int16 in units of k, headers {m, l, k, 0} in their own
+//        region: rec_index.h flash_o / flash_h).
 template <int SL, bool Q16 = false>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ q, int qts, int pos0, int nh,
                                                           const float* __restrict__ part, int chunk, int smax,
                                                           float* __restrict__ out, int ots) {
-    constexpr int RW = Q16 ? FLASH_REC : PART;   // record words
+    constexpr int RW = PART;                 // record words (f32 records)
     constexpr int DLN = 256 / SL;            // dim lanes, 4 dims each
     constexpr int DW = 4 * DLN;              // dims per workgroup
     __shared__ float red_m[SL];
@@ -446,6 +447,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     const int sg = tid / DLN, dl = tid % DLN, d0 = DW * dq + 4 * dl;
     const int ns = idx::splits_seen(pos0, t, chunk);
     const float* base = part + idx::rec(t * nh + h, 0, smax) * RW;
+    const int rows = (int)gridDim.z * nh;
     const f4 gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + d0);
     float M = -INFINITY, den = 0.f;
     f4 o = {0.f, 0.f, 0.f, 0.f};
@@ -462,12 +464,15 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
         for (int j = 0; j < COMB_SPL; ++j) {
             // a lane with no split left in the batch (nb <= 0) reloads split ns - 1: every index
             // stays inside this row's records, so a buffer sized exactly for them is never overrun
-            const float* rec = base + (size_t)idx::comb_split(s0, sg, SL, j, nb, ns) * RW;
-            hv[j] = *(const f2*)rec;
+            const int sj = idx::comb_split(s0, sg, SL, j, nb, ns);
             if (Q16) {
-                kv[j] = rec[2];
-                qv[j] = *((const u2*)(rec + 4) + (d0 >> 2));
+                const float* hd = part + idx::flash_h(rows, t * nh + h, sj, smax);
+                hv[j] = *(const f2*)hd;
+                kv[j] = hd[2];
+                qv[j] = *((const u2*)(part + idx::flash_o(t * nh + h, sj, smax)) + (d0 >> 2));
             } else {
+                const float* rec = base + (size_t)sj * RW;
+                hv[j] = *(const f2*)rec;
                 ov[j] = ld_f4(rec + 4 + d0);
             }
         }
@@ -527,21 +532,21 @@ template <int NS, bool Q16>
 __global__ __launch_bounds__(256) void attn_combine_row_kernel(const float* __restrict__ q, int qts, int pos0, int nh,
                                                                int nt, const float* __restrict__ part, int chunk,
                                                                int smax, float* __restrict__ out, int ots) {
-    constexpr int RW = Q16 ? FLASH_REC : PART;   // record words
     const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
     if (row >= nt * nh) return;
     const int l = threadIdx.x & 63;
     const int t = row / nh, h = row - t * nh;
     const int ns = idx::splits_seen(pos0, t, chunk);   // splits holding keys <= pos0 + t (1 .. smax)
-    const float* base = part + idx::rec(row, 0, smax) * RW;
-    const f4 hl = *(const f4*)(base + (size_t)idx::row_split(l, ns) * RW);   // lane l: header of split l
+    const float* base = part + idx::rec(row, 0, smax) * PART;   // f32 records
+    // lane l: header of split l (int16 records: the packed header region, 16 bytes a split)
+    const f4 hl = Q16 ? *(const f4*)(part + idx::flash_h(nt * nh, row, idx::row_split(l, ns), smax))
+                      : *(const f4*)(base + (size_t)idx::row_split(l, ns) * PART);
     f4 ov[NS];
     u2 qv[NS];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const float* rec = base + (size_t)idx::row_split(j, ns) * RW;
-        if constexpr (Q16) qv[j] = *((const u2*)(rec + 4) + l);
-        else ov[j] = ld_f4(rec + 4 + 4 * l);
+        if constexpr (Q16) qv[j] = *((const u2*)(part + idx::flash_o(row, idx::row_split(j, ns), smax)) + l);
+        else ov[j] = ld_f4(base + (size_t)idx::row_split(j, ns) * PART + 4 + 4 * l);
     }
     const f4 gt = ld_f4(q + (size_t)t * qts + (size_t)h * 2 * HD + HD + 4 * l);
     const float M = wave_max(l < ns ? hl[0] : -INFINITY);   // finite: split 0 holds key 0

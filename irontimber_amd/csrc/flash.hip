@@ -19,8 +19,9 @@
 //
 // Key-split form (part != null): workgroup (row tile, KV head, split s) covers keys
 // [s*chunk, (s+1)*chunk) only and writes a partial record of each of its rows for the merge
-// kernel: the {m, l} of the decode partials (kernels/src/lib.rs:753-798) plus a scale k, then O as
-// int16 in units of k (FLASH_REC words). Used when one pass would leave most CUs idle: a 64-token
+// kernel: the {m, l} of the decode partials (kernels/src/lib.rs:753-798) plus a scale k, and O as
+// int16 in units of k (FLASH_REC words a record: the O runs and the headers in two regions,
+// rec_index.h flash_o / flash_h). Used when one pass would leave most CUs idle: a 64-token
 // chunk after a long context has only 2 * ceil(64*G/128) row tiles.
 #include "common.h"
 #include "internal.h"
@@ -389,7 +390,9 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         return;
     }
     if (part) {
-        // partial records of (token, head, split), FLASH_REC words each: {m, l, k, 0} with m in
+        // partial records of (token, head, split), FLASH_REC words each: O as 256 int16 in a
+        // 512-byte run of its own (whole cache lines: no line is shared with another split's
+        // record, which another workgroup writes), the header in a packed region: {m, l, k, 0} with m in
         // natural-log units of the scaled score and k = max|O| / 32767, then O as int16 in units of
         // k (v_cvt_pk_norm_i16_f32 of O / max|O|): error <= max|O| / 65534 per value, half the
         // bytes of an f32 record (over the 128 chunks of an 8192-token prompt: 158 -> 162 TFLOP/s,
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         // c + 32 both hold row c's maximum), so a row costs a few vector instructions.
         if (l < nrow) {
             const int tl = (rw + l) / G, gl = rw + l - tl * G;
-            float* rec = part + idx::rec(tl * nh + kh * G + gl, split, smax) * FLASH_REC;
+            float* rec = part + idx::flash_h(nt * nh, tl * nh + kh * G + gl, split, smax);
             __builtin_nontemporal_store(f4{ml[w][0][l] * 0.6931471805599453f, ml[w][1][l], ml[w][2][l] * (1.0f / 32767.0f), 0.f},
                                         (f4*)rec);
         }
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
         size_t ridx = idx::rec(tq * nh + kh * G + gq, split, smax);
         const size_t rnext = (size_t)(nh - G + 1) * smax;
         auto put = [&](int i) {
-            u2* dst = (u2*)(part + uniform_off(ridx * FLASH_REC + 4));
+            u2* dst = (u2*)(part + uniform_off(ridx * 128));   // idx::flash_o of record ridx
             const float inv = readlane_f(inv_c, i);
             u2 pk;
             pk[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_i16(ov[i][0] * inv, ov[i][1] * inv));

@@ -41,6 +41,15 @@ IT_IDX size_t piece_h(int rows, int th, int s, int smax) {
 }
 IT_IDX size_t piece_words(int rows, int smax) { return (size_t)rows * smax * 258; }
 
+// Flash key-split records (O as int16 in units of k): O of (row th, split s) as 256 int16 at
+// flash_o, a 512-byte-aligned run of whole cache lines, then the headers {m, l, k, 0} of all
+// (row, split) packed after them at flash_h; flash_words floats in all (FLASH_REC per record).
+IT_IDX size_t flash_o(int th, int s, int smax) { return ((size_t)th * smax + s) * 128; }
+IT_IDX size_t flash_h(int rows, int th, int s, int smax) {
+    return (size_t)rows * smax * 128 + ((size_t)th * smax + s) * 4;
+}
+IT_IDX size_t flash_words(int rows, int smax) { return (size_t)rows * smax * FLASH_REC; }
+
 // Mailbox piece (row th, dim block db, split s): its first float.
 IT_IDX int mb_piece(int th, int db, int s, int smax) { return MB_HEAD + ((th * 16 + db) * smax + s) * MB_PIECE; }
 

@@ -39,14 +39,39 @@ static int check_merge_cover(const char* what, const std::vector<std::pair<int, 
     return 0;
 }
 
+// api.hip flash_scratch / 4: FLASH_REC words per (row, split)
+static size_t flash_words_planned(int rows, int smax) { return (size_t)rows * smax * FLASH_REC; }
+
 static int check_geometry(int pos0, int nt, int nh, int chunk) {
     const int rows = nt * nh;
     const int smax = split_count((long)pos0 + nt, chunk);
     const size_t part_words = (size_t)rows * smax * PART;   // splitk_scratch / 4
-    const size_t flash_words = (size_t)rows * smax * FLASH_REC;
+    const size_t fw = (size_t)rows * smax * FLASH_REC;
     // row-major records: the last word of the last record is inside the buffer
     REQUIRE(rec(rows - 1, smax - 1, smax) * PART + PART <= part_words, "f32 records pos0 %d nt %d", pos0, nt);
-    REQUIRE(rec(rows - 1, smax - 1, smax) * FLASH_REC + FLASH_REC <= flash_words, "flash records pos0 %d", pos0);
+    REQUIRE(rec(rows - 1, smax - 1, smax) * FLASH_REC + FLASH_REC <= fw, "flash records pos0 %d", pos0);
+    // flash int16 records: O runs 512-byte aligned and one-to-one, headers after them, all inside
+    // flash_words (the planner's size)
+    REQUIRE(flash_words(rows, smax) == flash_words_planned(rows, smax), "flash words");
+    REQUIRE(flash_o(rows - 1, smax - 1, smax) + 128 <= (size_t)rows * smax * 128, "flash o corner");
+    REQUIRE(flash_h(rows, rows - 1, smax - 1, smax) + 4 <= flash_words(rows, smax), "flash h corner");
+    REQUIRE(flash_o(0, 1, smax) - flash_o(0, 0, smax) == 128 && flash_o(0, 0, smax) % 32 == 0, "flash o stride");
+    if ((size_t)rows * smax <= 40000) {
+        std::vector<uint8_t> hit(flash_words(rows, smax), 0);
+        for (int th = 0; th < rows; ++th)
+            for (int s = 0; s < smax; ++s) {
+                for (int e = 0; e < 128; ++e) {
+                    const size_t w = flash_o(th, s, smax) + e;
+                    REQUIRE(w < (size_t)rows * smax * 128 && !hit[w], "flash o (%d,%d)", th, s);
+                    hit[w] = 1;
+                }
+                for (int e = 0; e < 4; ++e) {
+                    const size_t w = flash_h(rows, th, s, smax) + e;
+                    REQUIRE(w >= (size_t)rows * smax * 128 && w < hit.size() && !hit[w], "flash h (%d,%d)", th, s);
+                    hit[w] = 1;
+                }
+            }
+    }
     // piece layout: inside the f32 records' bytes; one word per (row, dim, split) and per header word
     REQUIRE(piece_words(rows, smax) <= part_words, "piece words pos0 %d nt %d nh %d", pos0, nt, nh);
     if ((size_t)rows * smax <= 40000) {
