@@ -130,10 +130,10 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
     }
 
     for (int kt = kb0; kt < kend; kt += F32KV_KEYS) {
+        const bool more = kt + F32KV_KEYS < kend;
         if (kt != kb0) {
-            __syncthreads();   // every wave is done with the previous tile's K, V and P
-            stage_k(kt);
-            stage_v(kt);
+            __syncthreads();   // every wave is done with the previous tile's V and P
+            stage_v(kt);       // (its K rows were staged during the previous tile)
         }
         IT_F32KV_WAIT_VMCNT16();   // K rows (and q): the 16 V loads may still fly
         // S^T block: element i = key kt + 16w + 4lg + i, query row lr of block rb.
@@ -158,6 +158,10 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
             mx = max_xor32(max_xor16(mx));
             if (lg == 0) mxs[w][16 * rb + lr] = mx;
         }
+        // the next tile's K rows go out now: a wave's scores read only its own 16 K rows, so once
+        // they are done its rows can be refilled (no barrier), and the rows land during this
+        // tile's softmax and P.V instead of after the next tile's barrier
+        if (more) stage_k(kt + F32KV_KEYS);
         __syncthreads();   // the four waves' row maxima
         float alpha[RB];
 #pragma unroll
@@ -177,7 +181,9 @@ __global__ __launch_bounds__(256) void attn_f32kv_kernel(const float* __restrict
             ps = sum_xor32(sum_xor16(ps));
             if (lg == 0) pss[w][r] = ps;
         }
-        IT_F32KV_WAIT_VMCNT0();   // this wave's V rows
+        // this wave's V rows (issued before the next tile's 16 K loads, which may still fly)
+        if (more) IT_F32KV_WAIT_VMCNT16();
+        else IT_F32KV_WAIT_VMCNT0();
         __syncthreads();          // every wave's P, row sums and V rows
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
