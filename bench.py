@@ -419,7 +419,8 @@ def main():
         om = torch.empty(64, NH * HD, device=dev)
         from irontimber_amd._lib import lib as _lm
         scm = torch.empty(max(_lm().it_attn_f32kv_scratch_bytes(p0, n, HD, NH, NKV)
-                              for p0, n in ((S8 - 1, 1), (S8 - 2, 2), (4096, 64))), dtype=torch.uint8, device=dev)
+                              for p0, n in ((S8 - 1, 1), (S8 - 2, 2), (1024, 64), (2048, 64), (4096, 64), (S8 - 64, 64))),
+                          dtype=torch.uint8, device=dev)
 
         def mtp_attn(i, nt, pos0):
             call("it_attn_f32kv", qm.data_ptr(), NH * 2 * HD, kf[i % NMT].data_ptr(), vf[i % NMT].data_ptr(), KVD, pos0,
@@ -433,8 +434,11 @@ def main():
         res["mtp_f32kv_nt2_8192_us"] = round(ms * 1000 / KM, 3)
         ms = graph_time_ms(torch, lambda: [mtp_attn(i, 64, 4096) for i in range(20)], reps=3)
         res["mtp_f32kv_catchup64_at4096_us"] = round(ms * 1000 / 20, 2)
+        for p0 in (1024, 2048, S8 - 64):   # the catch-up at other prompt positions
+            ms = graph_time_ms(torch, lambda: [mtp_attn(i, 64, p0) for i in range(20)], reps=3)
+            res[f"mtp_f32kv_catchup64_at{p0}_us"] = round(ms * 1000 / 20, 2)
         # the same catch-up given exactly the reference arena's room (src/vk/mod.rs:148, 730-733):
-        # the split doubles from 64 to 256 keys to fit it
+        # the library's preferred split fits it (64-key splits would not)
         room = _lm().it_attention_dispatch_room(S8, NH, 64) * 4
         scr_room = torch.empty(room, dtype=torch.uint8, device=dev)
 
@@ -446,7 +450,9 @@ def main():
         log(f"mtp f32-KV attention: decode 8192 slots {res['mtp_f32kv_decode_8192_us']} us "
             f"({res['mtp_f32kv_decode_8192_GBs']} GB/s), nt=2 {res['mtp_f32kv_nt2_8192_us']} us, "
             f"64-token catch-up at 4096 {res['mtp_f32kv_catchup64_at4096_us']} us, "
-            f"{res['mtp_f32kv_catchup64_at4096_room_us']} us within the reference room")
+            f"{res['mtp_f32kv_catchup64_at4096_room_us']} us within the reference room; at 1024 / 2048 / "
+            f"{S8 - 64}: {res['mtp_f32kv_catchup64_at1024_us']} / {res['mtp_f32kv_catchup64_at2048_us']} / "
+            f"{res[f'mtp_f32kv_catchup64_at{S8 - 64}_us']} us")
         del scr_room
         del kf, vf, scm
 

@@ -105,17 +105,30 @@ bool plan_attn(int pos0, int nt, int nh, int nkv, int kernel, size_t budget, Att
 struct F32kvPlan { int chunk; size_t bytes; };
 // The f32-KV kernel's preferred split. Calls of one block of query rows (decode, verify: up to 32
 // rows per KV head) keep one 64-key tile per split. Calls with several row blocks (the 64-token
-// catch-up) read each K/V tile once per block, so they take 256-key splits, doubled while the grid
-// has more than 640 workgroups (measured for 64 tokens at slot 1024 / 4096 / 8128: 36 / 102 /
-// 127 us against 45 / 131 / 242 us with 64-key splits).
+// catch-up) read each K/V tile once per block and hold one workgroup per CU (133 KB of LDS), so
+// their time goes as the number of rounds of workgroups over the CUs times the tiles a workgroup
+// walks: the split (a multiple of 64 keys) minimises rounds x (tiles + 1), the + 1 standing for a
+// workgroup's fixed cost (q rows, first tile, records), ties going to the longer split (fewer
+// records). A fixed 256-key split gave 99 us for 64 tokens at slot 4096 (544 workgroups: 3 rounds
+// of 4 tiles); 320 / 384 / 512 keys gave 81 / 91 / 114 us (2 rounds of 5 / 6 / 8 tiles).
+constexpr int F32KV_CUS = 256;   // MI355X compute units
 int f32kv_pref_chunk(int pos0, int nt, int nh, int nkv) {
     const int G = nh / nkv;
     if ((long)nt * G <= 32) return auto_chunk(pos0, nt, nh, nkv);
     const long total = (long)pos0 + nt;
     const long blocks = ((long)nt * G + 31) / 32;   // 32-row blocks of the multi-block kernel
-    int c = 256;
-    while (c < total && ((total + c - 1) / c) * nkv * blocks > 640) c *= 2;
-    return c > auto_chunk(pos0, nt, nh, nkv) ? c : auto_chunk(pos0, nt, nh, nkv);
+    int best = 64;
+    long best_cost = -1;
+    for (long c = 64;; c += 64) {
+        const long wgs = (total + c - 1) / c * nkv * blocks;
+        const long cost = (wgs + F32KV_CUS - 1) / F32KV_CUS * (c / 64 + 1);
+        if (best_cost < 0 || cost <= best_cost) {
+            best_cost = cost;
+            best = (int)c;
+        }
+        if (c >= total) break;
+    }
+    return best;
 }
 F32kvPlan plan_f32kv(int pos0, int nt, int nh, int nkv, size_t budget) {
     const long total = (long)pos0 + nt;

@@ -361,7 +361,9 @@ def test_f32kv_plan_cases():
     assert f32kv_plan(8191, 1, 16, 2, room1) == (0, 64, 16 * 128 * 1040)
     # the MTP catch-up of 64 tokens at slot 4096: 64-key splits would need 69,222,400 B against a
     # room of 33,554,432 B (the reference doubles its C from 64 to 256 to fit, src/vk/mod.rs:731-733);
-    # the library prefers 256-key splits for multi-block calls, 17 splits = 18,104,320 B
+    # the library's split for multi-block calls minimises rounds of workgroups over the 256 CUs x
+    # (tiles + 1): at slot 4096, 576 keys (8 splits x 2 KV heads x 16 row blocks = 256 workgroups,
+    # one round of 9 tiles), 8,519,680 B, inside the room
     room64 = lib.it_attention_dispatch_room(8192, 16, 64) * 4
     assert room64 == 33554432
     assert 64 * 16 * 65 * 1040 == 69222400
@@ -369,11 +371,17 @@ def test_f32kv_plan_cases():
     while c < 1024 and 64 * 16 * -(-total // c) * 260 * 4 > room64:
         c *= 2
     assert c == 256
-    assert lib.it_attn_f32kv_scratch_bytes(4096, 64, 256, 16, 2) == 64 * 16 * 17 * 1040
-    assert f32kv_plan(4096, 64, 16, 2, room64) == (0, 256, 64 * 16 * 17 * 1040)
-    # at slot 8128 the preferred split is 512 keys (16 splits x 2 KV heads x 16 row blocks = 512
-    # workgroups); a budget of 5 records per row doubles it to 2048
-    assert f32kv_plan(8128, 64, 16, 2, room64) == (0, 512, 64 * 16 * 16 * 1040)
+    assert lib.it_attn_f32kv_scratch_bytes(4096, 64, 256, 16, 2) == 64 * 16 * 8 * 1040
+    assert f32kv_plan(4096, 64, 16, 2, room64) == (0, 576, 64 * 16 * 8 * 1040)
+    # the cost model by hand: rounds x (tiles + 1) for every candidate, ties to the longer split
+    def cost(c, total=4160, per_split=2 * 16):
+        return -(-(-(-total // c) * per_split) // 256) * (c // 64 + 1)
+    costs = {c: cost(c) for c in range(64, 4160 + 64, 64)}
+    best = min(costs.values())
+    assert max(c for c, v in costs.items() if v == best) == 576 and costs[256] == 15 and costs[576] == 10
+    # at slot 8128, 1024 keys (8 splits: 256 workgroups, one round of 16 tiles); a budget of 5
+    # records per row doubles it to 2048
+    assert f32kv_plan(8128, 64, 16, 2, room64) == (0, 1024, 64 * 16 * 8 * 1040)
     assert f32kv_plan(8128, 64, 16, 2, 64 * 16 * 5 * 1040) == (0, 2048, 64 * 16 * 4 * 1040)
     # one row block (decode, verify) keeps 64-key splits
     assert f32kv_plan(8188, 4, 16, 2, 1 << 40)[1] == 64
