@@ -290,9 +290,10 @@ def main():
         v5 = [torch.from_numpy(vb5.view(np.int16)).to(dev) for _ in range(8)]
 
         def d512(i):
+            # the library's own split (as an engine calls it) unless --decode-chunk fixes one
             call("it_attn_f16_ex", q5.data_ptr(), NH * 2 * HD, k5[i % 8].data_ptr(), v5[i % 8].data_ptr(), KVD, 511, HD,
-                 NH, NKV, 1, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(), ops.KERNEL_SPLITK, chunk,
-                 stream_of())
+                 NH, NKV, 1, scale, out.data_ptr(), NH * HD, part.data_ptr(), part.numel(),
+                 ops.KERNEL_SPLITK if args.decode_chunk else ops.KERNEL_AUTO, args.decode_chunk, stream_of())
         ms = graph_time_ms(torch, lambda: [d512(i) for i in range(KM)], reps=3)
         res["decode_ctx512_us_per_layer"] = round(ms * 1000.0 / KM, 3)
         del kcs, vcs, k5, v5

@@ -109,8 +109,9 @@ int it_attn_f16(const float* q, int q_tok_stride, const uint16_t* kc, const uint
  *          3 = kernel 2 with lossless key-split records: the split-K kernel's 260-word f32 form
  *          {m, l, 0, 0, o[256]} instead of int16 O (twice the scratch; the same result as one
  *          pass up to f32 reassociation of the merge).
- *   chunk  = keys per split (multiple of 64), 0 = automatic. For kernels 2 and 3 a chunk of at
- *          least pos0 + nt means one pass.
+ *   chunk  = keys per split, 0 = automatic: a multiple of 32 for kernel 1 (the automatic split is
+ *          32 keys for 1-2 tokens below 2048 keys, else 64), of 64 for kernels 2 and 3, where a
+ *          chunk of at least pos0 + nt means one pass.
  * it_attn_scratch_bytes_ex gives the scratch for the same choice. With chunk = 0 the split is fitted
  * to scratch_bytes as in it_attn_f16; an explicit chunk needs its full record set. */
 size_t it_attn_scratch_bytes_ex(int pos0, int nt, int hd, int nh, int nkv, int kernel, int chunk);
@@ -206,7 +207,7 @@ int it_attn_combine(const float* q, int q_tok_stride, const float* part, int pos
 
 /* The same two phases with a choice of record layout. layout 0: the 260-float records above (these
  * calls are then it_attn_partials / it_attn_combine). layout 1: the records it_attn_f16 itself
- * uses when its merge takes one wave per (token, head, 16 output dims), i.e. for 17-256 splits and
+ * uses when its merge takes one wave per (token, head, 16 output dims), i.e. for 9-256 splits and
  * at most 256 (token, head) rows (decode and verify at long contexts; other geometries are
  * refused): the same f32 values, O as 64-byte pieces of 16 floats at
  * part + (((t*nh + h)*16 + d/16)*smax + s)*16 (+ d % 16), then {m, l} at
@@ -235,8 +236,9 @@ int it_attn_prep_f32kv(float* q, int q_tok_stride, const float* k, const float* 
                        int pos0, int row0, int hd, int nh, int nkv, int nt, int n_rot, float theta_scale, int sec0,
                        int sec1, int sec2, int sec3, void* stream);
 
-/* Bytes of scratch it_attn_f32kv prefers (split-K partial records of 64-key splits, same 260-float
- * layout); any smaller scratch also works (it_attn_f32kv_plan). */
+/* Bytes of scratch it_attn_f32kv prefers (split-K partial records, same 260-float layout: 64-key
+ * splits for one block of up to 32 query rows per KV head, longer splits for multi-block calls);
+ * any smaller scratch also works (it_attn_f32kv_plan). */
 size_t it_attn_f32kv_scratch_bytes(int pos0, int nt, int hd, int nh, int nkv);
 
 /* The split it_attn_f32kv uses for a scratch of scratch_bytes: *chunk keys per split and *bytes of

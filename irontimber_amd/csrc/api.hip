@@ -38,11 +38,21 @@ constexpr size_t AUTO_SCRATCH_CAP = size_t(256) << 20;   // keep automatic split
 
 // Keys per split for the split-K kernel when the caller leaves it to us: one 64-key tile per
 // workgroup (ctx 8192 -> 128 splits per KV head, 256 workgroups for two KV heads), doubled only
-// when the partial records would outgrow the scratch cap.
-int auto_chunk(int pos0, int nt, int nh, int nkv) {
-    (void)nkv;
+// when the partial records would outgrow the scratch cap. Decode and 2-token calls below 2048 keys
+// take 32-key splits (the tile's second half masked): with 64-key splits those leave most CUs idle
+// (ctx 1024: 32 workgroups); same box, 32 against 64 keys, ctx 256 / 512 / 1024 / 1984: 5.76 /
+// 5.86 / 6.16 / 6.36 against 5.89 / 6.13 / 6.53 / 6.60 us, 2 tokens at 512 / 1024: 6.08 / 6.33
+// against 6.16 / 6.65 us; 4-token calls measured better with 64 keys at 768-2048 keys. From 2048
+// keys, and wherever the one-launch mailbox form can launch (it uses 64-key splits; the two forms
+// stay bit-equal), the split stays at 64: the mailbox needs at most 8 query rows per KV head and at
+// most 4 merge units (row, 16-dim block) per workgroup. The f32-KV kernel's tiles cover whole
+// splits, so it asks for 64-key splits (short_splits = false).
+int auto_chunk(int pos0, int nt, int nh, int nkv, bool short_splits = true) {
     const size_t total = (size_t)pos0 + nt;
-    int c = 64;
+    const long R = (long)nt * (nh / nkv);                          // query rows per KV head
+    const long wgs64 = (long)((total + 63) / 64) * nkv * ((R + 7) / 8);
+    const bool mailbox_possible = R <= 8 && (long)nt * nh * 16 <= 4 * wgs64;
+    int c = short_splits && nt <= 2 && total < 2048 && !mailbox_possible ? 32 : 64;
     while (c < (1 << 20) && (size_t)nt * nh * ((total + c - 1) / c) * PART_WORDS * 4 > AUTO_SCRATCH_CAP) c *= 2;
     return c;
 }
@@ -114,7 +124,7 @@ struct F32kvPlan { int chunk; size_t bytes; };
 constexpr int F32KV_CUS = 256;   // MI355X compute units
 int f32kv_pref_chunk(int pos0, int nt, int nh, int nkv) {
     const int G = nh / nkv;
-    if ((long)nt * G <= 32) return auto_chunk(pos0, nt, nh, nkv);
+    if ((long)nt * G <= 32) return auto_chunk(pos0, nt, nh, nkv, false);
     const long total = (long)pos0 + nt;
     const long blocks = ((long)nt * G + 31) / 32;   // 32-row blocks of the multi-block kernel
     int best = 64;
@@ -415,7 +425,7 @@ static int attn_f16_impl(const float* q, int qts, const uint16_t* q16, int q16ts
                      "it_attn_f16 (flash, key splits)");
     }
     if (chunk <= 0) chunk = auto_chunk(pos0, nt, nh, nkv);
-    if (chunk % 64 != 0) return fail("it_attn_f16: chunk %d must be a multiple of 64", chunk);
+    if (chunk % 32 != 0) return fail("it_attn_f16: chunk %d must be a multiple of 32", chunk);
     const size_t need = splitk_scratch(pos0, nt, nh, chunk);
     if (scratch_bytes < need || (need && !scratch))
         return fail("it_attn_f16: scratch of %zu bytes < %zu required (it_attn_scratch_bytes)", scratch_bytes, need);
@@ -554,7 +564,7 @@ int it_attn_partials_ex(const float* q, int qts, const uint16_t* kc, const uint1
     if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, q, qts)) return -1;
     if (chunk <= 0 || chunk % 64 != 0) return fail("it_attn_partials_ex: chunk %d must be a positive multiple of 64", chunk);
     if (!it::piece_records(pos0, nt, nh, chunk))
-        return fail("it_attn_partials_ex: record layout 1 needs 17-256 splits and at most 256 (token, head) rows");
+        return fail("it_attn_partials_ex: record layout 1 needs 9-256 splits and at most 256 (token, head) rows");
     const size_t need = splitk_scratch(pos0, nt, nh, chunk);
     if (!part || part_bytes < need) return fail("it_attn_partials_ex: %zu bytes of partials < %zu required", part_bytes, need);
     if (!aligned16(part)) return fail("it_attn_partials_ex: part must be 16-byte aligned");
@@ -570,7 +580,7 @@ int it_attn_combine_ex(const float* q, int qts, const float* part, int pos0, int
     if (hd != HD || nh <= 0 || nt <= 0 || pos0 < 0) return fail("it_attn_combine_ex: bad geometry");
     if (chunk <= 0 || chunk % 64 != 0) return fail("it_attn_combine_ex: chunk %d must be a positive multiple of 64", chunk);
     if (!it::piece_records(pos0, nt, nh, chunk))
-        return fail("it_attn_combine_ex: record layout 1 needs 17-256 splits and at most 256 (token, head) rows");
+        return fail("it_attn_combine_ex: record layout 1 needs 9-256 splits and at most 256 (token, head) rows");
     if (!q || !part || !out || !aligned16(q) || !aligned16(part) || !aligned16(out))
         return fail("it_attn_combine_ex: buffers must be non-null and 16-byte aligned");
     if (qts % 4 != 0 || ots % 4 != 0) return fail("it_attn_combine_ex: token strides must be multiples of 4");

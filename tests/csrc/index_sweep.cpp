@@ -98,8 +98,8 @@ static int check_geometry(int pos0, int nt, int nh, int chunk) {
     for (int t = 0; t < nt; ++t) {
         const int ns = splits_seen(pos0, t, chunk);
         REQUIRE(ns >= 1 && ns <= smax, "ns %d smax %d (pos0 %d t %d chunk %d)", ns, smax, pos0, t, chunk);
-        // wave merge (launch_attn_combine: 16 < smax <= 256, SPL by smax), also the piece layout's
-        if (smax > 16 && smax <= 256) {
+        // wave merge (piece_records: 8 < smax <= 256, SPL by smax)
+        if (smax > 8 && smax <= 256) {
             const int spl = smax <= 64 ? 1 : smax <= 128 ? 2 : 4;
             std::vector<std::pair<int, bool>> loads;
             for (int l = 0; l < 64; ++l)

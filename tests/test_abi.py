@@ -148,8 +148,8 @@ def test_record_layout_entries_reject_bad_arguments_before_device_work():
         return lib.it_attn_combine_ex(fake, 8192, fake, pos0, 256, 16, nt, chunk, layout, fake, 4096, None)
     for f in (part, comb):
         assert f(2) != 0 and "layout" in _lib.last_error()
-        assert f(1, pos0=511) != 0 and "17-256 splits" in _lib.last_error()      # 8 splits
-        assert f(1, pos0=8192 * 4) != 0 and "17-256 splits" in _lib.last_error()  # 513 splits
+        assert f(1, pos0=511) != 0 and "9-256 splits" in _lib.last_error()       # 8 splits
+        assert f(1, pos0=8192 * 4) != 0 and "9-256 splits" in _lib.last_error()  # 513 splits
         assert f(1, pos0=8128, nt=64) != 0 and "256" in _lib.last_error()         # 1024 rows
         assert f(1, chunk=96) != 0 and "multiple of 64" in _lib.last_error()
 

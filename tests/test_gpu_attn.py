@@ -317,7 +317,7 @@ def _two_phase_f32(dev, qd, kc, vc, pos0, nt, nh, nkv, chunk):
 
 @pytest.mark.parametrize("ctx,nt", [(1100, 1), (4096, 2), (8192, 1), (8192, 4), (16384, 1)])
 def test_piece_records_equal_f32_records(dev, ctx, nt):
-    """Decode and verify calls of it_attn_f16 whose merge is the wave merge (17-256 splits, at most
+    """Decode and verify calls of it_attn_f16 whose merge is the wave merge (9-256 splits, at most
     256 rows) lay their split records out in 64-byte pieces per (row, 16-dim block, split): the
     same f32 values merged in the same order, so the output equals it_attn_partials +
     it_attn_combine (the 260-word records) bit for bit, at the oracle's bar."""
