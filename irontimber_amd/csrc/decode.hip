@@ -685,7 +685,7 @@ __device__ __forceinline__ void combine_wave_row(const float* __restrict__ q, in
     merge_wave_store<SPL>(merge_gate(q, qts, t, h, d0, l), nh, t, h, ns, hv, ov, out, ots, d0, l);
 }
 
-template <int SPL, bool CR = false>
+template <int SPL>
 __global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __restrict__ q, int qts, int pos0,
                                                                 int nh, int nt, const float* __restrict__ part,
                                                                 int chunk, int smax, float* __restrict__ out,
@@ -702,8 +702,22 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(const float* __r
         row = blockIdx.x >> 2;
         quarter = blockIdx.x & 3;
     }
-    combine_wave_row<SPL, CR>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots, row,
+    combine_wave_row<SPL, false>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots, row,
                           16 * (4 * quarter + (threadIdx.x >> 6)), threadIdx.x & 63);
+}
+
+// The same merge with one wave per workgroup, for the piece layout: (row, 16-dim block) units spread
+// over rows x 16 workgroups instead of a quarter as many. With 260-word records it was slower (each
+// wave's loads touched a line per split); with pieces it is faster: ctx-8192 decode layer 8.53 /
+// 8.54 -> 8.26 / 8.28 us, verify nt = 4 12.51 -> 12.47 us, ctx 512 5.81 -> 5.77 us (same box).
+template <int SPL>
+__global__ __launch_bounds__(64) void attn_combine_wave1_kernel(const float* __restrict__ q, int qts, int pos0,
+                                                                int nh, int nt, const float* __restrict__ part,
+                                                                int chunk, int smax, float* __restrict__ out,
+                                                                int ots) {
+    int row, db;
+    idx::wave1_unit((int)blockIdx.x, nt * nh, row, db);
+    combine_wave_row<SPL, true>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots, row, 16 * db, threadIdx.x & 63);
 }
 
 // One wave merges mailbox unit (row th, dim block db): lane l polls its pieces of splits l + 64j
@@ -936,13 +950,13 @@ hipError_t launch_attn_combine(const float* q, int qts, const float* part, int p
                                float* out, int ots, hipStream_t st, bool pieces) {
     const int smax = idx::split_count((long)pos0 + nt, chunk);
     if (pieces) {   // piece_records() holds: 8 < smax <= 256, at most 256 rows
-        const unsigned wgs = (unsigned)(((long)nt * nh * 16 + 3) / 4);
+        const unsigned wgs = (unsigned)((long)nt * nh * 16);   // one wave each
         if (smax <= 64)
-            attn_combine_wave_kernel<1, true><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+            attn_combine_wave1_kernel<1><<<wgs, 64, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
         else if (smax <= 128)
-            attn_combine_wave_kernel<2, true><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+            attn_combine_wave1_kernel<2><<<wgs, 64, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
         else
-            attn_combine_wave_kernel<4, true><<<wgs, 256, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
+            attn_combine_wave1_kernel<4><<<wgs, 64, 0, st>>>(q, qts, pos0, nh, nt, part, chunk, smax, out, ots);
         return hipGetLastError();
     }
     const unsigned wgs = (unsigned)(((long)nt * nh * 16 + 3) / 4);   // 4 waves each

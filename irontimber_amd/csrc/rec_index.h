@@ -57,6 +57,20 @@ IT_IDX int mb_piece(int th, int db, int s, int smax) { return MB_HEAD + ((th * 1
 // j; slots with l + 64 j >= ns reload the row's last split and are masked.
 IT_IDX int wave_split(int l, int j, int ns) { return imin(l + 64 * j, ns - 1); }
 
+// Wave merge with one wave per workgroup: workgroup id -> (row th, 16-dim block db) of rows x 16
+// units. With rows a multiple of 8, the 16 workgroups of a row get ids 8 apart (one XCD under the
+// round-robin dispatch), so the row's header run is fetched into one L2.
+IT_IDX void wave1_unit(int id, int rows, int& th, int& db) {
+    if (rows % 8 == 0) {
+        const int xcd = id & 7, slot = id >> 3;
+        th = ((slot >> 4) << 3) | xcd;
+        db = slot & 15;
+    } else {
+        th = id >> 4;
+        db = id & 15;
+    }
+}
+
 // Row merge (one wave per row): slot j loads split row_split(j, ns), masked past ns.
 IT_IDX int row_split(int j, int ns) { return imin(j, ns - 1); }
 

@@ -128,6 +128,18 @@ static int check_geometry(int pos0, int nt, int nh, int chunk) {
     return 0;
 }
 
+// one-wave merge: workgroup ids 0 .. rows*16-1 map one-to-one onto (row, 16-dim block)
+static int check_wave1(int rows) {
+    std::vector<uint8_t> hit((size_t)rows * 16, 0);
+    for (int id = 0; id < rows * 16; ++id) {
+        int th = -1, db = -1;
+        wave1_unit(id, rows, th, db);
+        REQUIRE(th >= 0 && th < rows && db >= 0 && db < 16 && !hit[(size_t)th * 16 + db], "wave1 id %d rows %d", id, rows);
+        hit[(size_t)th * 16 + db] = 1;
+    }
+    return 0;
+}
+
 // mailbox (64-key splits): pieces of every (row, block, visible split) disjoint, inside the buffer
 // of it_attn_mailbox_bytes (MB_HEAD + rows * 16 * smax * MB_PIECE floats)
 static int check_mailbox(int ctx, int nt, int nh) {
@@ -162,6 +174,8 @@ int main() {
                     if (check_geometry(pos0, nt, nh, chunk)) return 1;
     for (int ns = 1; ns <= 300; ++ns)   // every split count of the merges at one token
         if (check_geometry(ns * 64 - 1, 1, 16, 64)) return 1;
+    for (int rows = 1; rows <= 256; ++rows)
+        if (check_wave1(rows)) return 1;
     for (int ctx : {1, 63, 64, 65, 1000, 2048, 8192, 16384})
         for (int nt : {1, 2, 4, 8})
             for (int nh : {4, 16, 32})
