@@ -154,6 +154,28 @@ def test_record_layout_entries_reject_bad_arguments_before_device_work():
         assert f(1, chunk=96) != 0 and "multiple of 64" in _lib.last_error()
 
 
+def test_short_context_split_policy():
+    """Split-K plans below 2048 keys: 32-key splits for 1-2 tokens (more workgroups), except where
+    the one-launch mailbox form could launch (at most 8 query rows per KV head and at most 4 merge
+    units per workgroup with 64-key splits), which must stay bit-equal to it_attn_f16; 4-token calls
+    and contexts from 2048 keys keep 64-key splits."""
+    lib = _lib.lib()
+
+    def plan(pos0, nt, nh=16, nkv=2):
+        k, c, b = ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+        assert lib.it_attn_plan(pos0, nt, 256, nh, nkv, ctypes.c_size_t(1 << 40), ctypes.byref(k), ctypes.byref(c),
+                                ctypes.byref(b)) == 0
+        return k.value, c.value
+    assert plan(511, 1) == (1, 32) and plan(1983, 1) == (1, 32) and plan(62, 2) == (1, 32)
+    assert plan(2046, 2) == (1, 64) and plan(8191, 1) == (1, 64)
+    assert plan(1020, 4) == (1, 64)
+    # 2000 keys: 32 splits x 2 KV heads of 64 keys give 64 workgroups for 256 merge units, so the
+    # mailbox could launch: 64 keys (also with 32 heads over 4 KV heads)
+    assert plan(1999, 1) == (1, 64) and plan(1999, 1, 32, 4) == (1, 64)
+    # explicit splits: multiples of 32 for the split-K kernel
+    assert lib.it_attn_scratch_bytes_ex(511, 1, 256, 16, 2, 1, 32) == 16 * 16 * 260 * 4
+
+
 def test_scratch_bytes_policy():
     lib = _lib.lib()
     # decode: split-K, C = 64 -> 128 splits of 260 words per head
