@@ -399,53 +399,42 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     const int cg = tid & 3, rp = tid >> 2;
     const int kh = h % nk, qk = nk * S, cd = (2 * nk + nv) * S;
     const int j0 = cb * 16 + 4 * cg, i0 = 2 * rp;
-    const int cq = kh * S + i0, ck = qk + kh * S + i0, cv = 2 * qk + h * S + j0;   // channel bases
+    const int cq = kh * S + i0, ck = qk + kh * S + i0;   // q and k channel bases of row i0
     float* sb = state + (size_t)h * S * S;
     // every load up front: tokens, weights, the conv window, the gates, then the state. The
     // vector-memory counter retires in order, so the conv inputs issued first can be used (the
     // conv, SiLU and norm sums run) while the state slice is still landing.
-    f2 xq[TM], xk[TM];
-    f4 xv[TM];
+    // Each lane convolves one q/k channel (by its place cg in the row pair's lane quad: q row i0,
+    // q row i0 + 1, k row i0, k row i0 + 1) and one of the workgroup's 16 v channels (lane & 15);
+    // the quad's four values reach its lanes by DPP broadcasts and each lane's four v channels by
+    // lane shuffles. Loading and convolving all 8 of its channels in every thread (the four lanes of
+    // a row pair alike, and all 64 row pairs the same 16 v channels) moved ~64 KB a workgroup
+    // through the CU's load path against its 8 KB state slice.
+    const int cqk = (cg < 2 ? cq : ck) + (cg & 1);
+    const int cvl = 2 * qk + h * S + cb * 16 + (l & 15);
+    float xa[TM], xb[TM];
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-        const float* xr = x + (size_t)t * xts;
-        xq[t] = *(const f2*)(xr + cq);
-        xk[t] = *(const f2*)(xr + ck);
-        xv[t] = ld_f4(xr + cv);
+        xa[t] = x[(size_t)t * xts + cqk];
+        xb[t] = x[(size_t)t * xts + cvl];
     }
-    float wq[2][K], wk[2][K], wv[4][K];
-    if constexpr (K == 4) {   // a channel's taps are one aligned f4 (channel bases are even)
+    float wa[K], wb[K];
+    if constexpr (K == 4) {   // a channel's taps are one aligned f4
+        const f4 a4 = ld_f4(cw + (size_t)cqk * 4), b4 = ld_f4(cw + (size_t)cvl * 4);
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const f4 a4 = ld_f4(cw + (size_t)(cq + e) * 4), b4 = ld_f4(cw + (size_t)(ck + e) * 4);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { wq[e][i] = a4[i]; wk[e][i] = b4[i]; }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const f4 c4 = ld_f4(cw + (size_t)(cv + e) * 4);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) wv[e][i] = c4[i];
-        }
+        for (int i = 0; i < 4; ++i) { wa[i] = a4[i]; wb[i] = b4[i]; }
     } else {
 #pragma unroll
         for (int i = 0; i < K; ++i) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                wq[e][i] = cw[(size_t)(cq + e) * K + i];
-                wk[e][i] = cw[(size_t)(ck + e) * K + i];
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) wv[e][i] = cw[(size_t)(cv + e) * K + i];
+            wa[i] = cw[(size_t)cqk * K + i];
+            wb[i] = cw[(size_t)cvl * K + i];
         }
     }
-    f2 wnq[K - 1], wnk[K - 1];
-    f4 wnv[K - 1];
+    float wna[K - 1], wnb[K - 1];
 #pragma unroll
     for (int i = 0; i < K - 1; ++i) {
-        wnq[i] = *(const f2*)(cst_in + (size_t)i * cd + cq);
-        wnk[i] = *(const f2*)(cst_in + (size_t)i * cd + ck);
-        wnv[i] = ld_f4(cst_in + (size_t)i * cd + cv);
+        wna[i] = cst_in[(size_t)i * cd + cqk];
+        wnb[i] = cst_in[(size_t)i * cd + cvl];
     }
     // the gate inputs too: loaded inside the loop they would wait behind the norm barrier
     float brt[TM], art[TM];
@@ -460,32 +449,26 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     f4 olast = {0.f, 0.f, 0.f, 0.f};   // the last token's output row (threads tid < 4)
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-        // ---- conv + SiLU of this thread's channels
+        // ---- conv + SiLU of this lane's two channels, then the exchanges
+        float ca = 0.f, cv_ = 0.f;
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i) { ca += wna[i] * wa[i]; cv_ += wnb[i] * wb[i]; }
+        ca += xa[t] * wa[K - 1];
+        cv_ += xb[t] * wb[K - 1];
+        ca = silu_hw(ca);
+        cv_ = silu_hw(cv_);
+#pragma unroll
+        for (int i = 0; i + 1 < K - 1; ++i) { wna[i] = wna[i + 1]; wnb[i] = wnb[i + 1]; }
+        wna[K - 2] = xa[t];
+        wnb[K - 2] = xb[t];
         float q[2], k[2];
+        q[0] = dppc<0x00>(ca);   // quad_perm [0,0,0,0]: q row i0
+        q[1] = dppc<0x55>(ca);   // quad_perm [1,1,1,1]: q row i0 + 1
+        k[0] = dppc<0xAA>(ca);   // quad_perm [2,2,2,2]: k row i0
+        k[1] = dppc<0xFF>(ca);   // quad_perm [3,3,3,3]: k row i0 + 1
         f4 v;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            float a = 0.f, b = 0.f;
-#pragma unroll
-            for (int i = 0; i < K - 1; ++i) { a += wnq[i][e] * wq[e][i]; b += wnk[i][e] * wk[e][i]; }
-            a += xq[t][e] * wq[e][K - 1];
-            b += xk[t][e] * wk[e][K - 1];
-            q[e] = silu_hw(a);
-            k[e] = silu_hw(b);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float a = 0.f;
-#pragma unroll
-            for (int i = 0; i < K - 1; ++i) a += wnv[i][e] * wv[e][i];
-            a += xv[t][e] * wv[e][K - 1];
-            v[e] = silu_hw(a);
-        }
-#pragma unroll
-        for (int i = 0; i + 1 < K - 1; ++i) { wnq[i] = wnq[i + 1]; wnk[i] = wnk[i + 1]; wnv[i] = wnv[i + 1]; }
-        wnq[K - 2] = xq[t];
-        wnk[K - 2] = xk[t];
-        wnv[K - 2] = xv[t];
+        for (int e = 0; e < 4; ++e) v[e] = __shfl(cv_, 4 * cg + e);   // column j0 + e = cb*16 + 4cg + e
         // ---- recurrence (gdn_step_kernel) with the q/k L2 norms folded in. The head norms are
         // scalars fq, fk, so with raw q, k: S^T k-hat = fk S^T k, and with S' = S + k-hat delta^T
         // (S already decayed), S'^T q-hat = fq S^T q + fq fk (k.q) delta. The two column sums, the
@@ -528,16 +511,13 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
                 *(f4*)(cb_ + (size_t)(i0 + 1) * S + j0) = s1;
             }
             if (ck_conv) {
-                if (cb == 0 && h == kh && cg == 0) {
+                if (cb == 0 && h == kh) {   // every q/k channel of the head, one per thread
 #pragma unroll
-                    for (int i = 0; i < K - 1; ++i) {
-                        *(f2*)(ck_conv + (size_t)i * cd + cq) = wnq[i];
-                        *(f2*)(ck_conv + (size_t)i * cd + ck) = wnk[i];
-                    }
+                    for (int i = 0; i < K - 1; ++i) ck_conv[(size_t)i * cd + cqk] = wna[i];
                 }
-                if (rp == 0) {
+                if (tid < 16) {             // the workgroup's 16 v channels
 #pragma unroll
-                    for (int i = 0; i < K - 1; ++i) *(f4*)(ck_conv + (size_t)i * cd + cv) = wnv[i];
+                    for (int i = 0; i < K - 1; ++i) ck_conv[(size_t)i * cd + cvl] = wnb[i];
                 }
             }
         }
@@ -547,16 +527,13 @@ __global__ __launch_bounds__(256) void gdn_decode_fused_kernel(
     *(f4*)(sb + (size_t)i0 * S + j0) = s0;
     *(f4*)(sb + (size_t)(i0 + 1) * S + j0) = s1;
     if (tid < 4) *(f4*)(out + (size_t)(TM - 1) * ots + (size_t)h * S + j0) = olast;
-    if (cb == 0 && h == kh && cg == 0) {
+    if (cb == 0 && h == kh) {   // every q/k channel of the head, one per thread
 #pragma unroll
-        for (int i = 0; i < K - 1; ++i) {
-            *(f2*)(cst_out + (size_t)i * cd + cq) = wnq[i];
-            *(f2*)(cst_out + (size_t)i * cd + ck) = wnk[i];
-        }
+        for (int i = 0; i < K - 1; ++i) cst_out[(size_t)i * cd + cqk] = wna[i];
     }
-    if (rp == 0) {
+    if (tid < 16) {             // the workgroup's 16 v channels
 #pragma unroll
-        for (int i = 0; i < K - 1; ++i) *(f4*)(cst_out + (size_t)i * cd + cv) = wnv[i];
+        for (int i = 0; i < K - 1; ++i) cst_out[(size_t)i * cd + cvl] = wnb[i];
     }
 }
 
