@@ -102,8 +102,9 @@ int it_attn_f16(const float* q, int q_tok_stride, const uint16_t* kc, const uint
 /* it_attn_f16 with the kernel choice exposed (the reference's BONSAI_PREFILL_ATTN / chunk policy,
  * src/vk/mod.rs:714-717 and 192-204):
  *   kernel 0 = automatic (what it_attn_f16 does), 1 = split-K partials + combine,
- *          2 = flash prefill (needs nt >= 16): one pass with no scratch, or, when one pass would
- *          leave most of the GPU idle (a short chunk after a long context), key splits whose
+ *          2 = flash prefill (any nt; the automatic choice from nt = 16): one pass with no scratch,
+ *          or, when one pass would leave most of the GPU idle (a short chunk after a long context),
+ *          key splits whose
  *          partial records (132 words: {m, l, k, 0} and O as int16 in units of k) are merged like
  *          kernel 1's,
  *          3 = kernel 2 with lossless key-split records: the split-K kernel's 260-word f32 form

@@ -392,8 +392,6 @@ static int attn_f16_impl(const float* q, int qts, const uint16_t* q16, int q16ts
     if (validate_attn(q, qts, kc, vc, kvd, pos0, hd, nh, nkv, nt, out, ots)) return -1;
     if (kernel != KERNEL_AUTO && kernel != KERNEL_SPLITK && kernel != KERNEL_FLASH && kernel != KERNEL_FLASH_F32)
         return fail("it_attn_f16: unknown kernel %d", kernel);
-    if ((kernel == KERNEL_FLASH || kernel == KERNEL_FLASH_F32) && nt < 16)
-        return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
     if (chunk == 0) {
         // automatic split: fit the caller's scratch (the reference's arena rule), never refuse a
         // geometry for which a smaller record set exists
@@ -409,7 +407,6 @@ static int attn_f16_impl(const float* q, int qts, const uint16_t* q16, int q16ts
     hipStream_t st = (hipStream_t)stream;
     if (kernel == KERNEL_FLASH || kernel == KERNEL_FLASH_F32) {
         const bool f32 = kernel == KERNEL_FLASH_F32;
-        if (nt < 16) return fail("it_attn_f16: the flash prefill kernel needs nt >= 16 (got %d)", nt);
         if (chunk < 0 || chunk % 64 != 0) return fail("it_attn_f16: flash chunk %d must be a multiple of 64", chunk);
         // (chunk is never 0 here: the automatic plan above has replaced it)
         const int c = flash_chunk(pos0, nt, nh, nkv, chunk);

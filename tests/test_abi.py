@@ -81,8 +81,8 @@ def test_attn_rejects_bad_geometry_before_device_work():
     assert rc != 0 and "n_head" in _lib.last_error()
     rc = lib.it_attn_f16_ex(fake, 8192, fake, fake, 512, 0, 256, 16, 2, 1, 0.1, fake, 4096, None, 0, 1, 64, None)
     assert rc != 0 and "scratch" in _lib.last_error()
-    rc = lib.it_attn_f16_ex(fake, 8192, fake, fake, 512, 0, 256, 16, 2, 4, 0.1, fake, 4096, fake, 1 << 30, 2, 0, None)
-    assert rc != 0 and "nt >= 16" in _lib.last_error()
+    rc = lib.it_attn_f16_ex(fake, 8192, fake, fake, 512, 0, 256, 16, 2, 4, 0.1, fake, 4096, fake, 1 << 30, 2, 96, None)
+    assert rc != 0 and "multiple of 64" in _lib.last_error()
     rc = lib.it_gdn_step(fake, 8192, fake, fake, 32, fake, fake, fake, fake, 4096, 1, 32, 16, 64, None)
     assert rc != 0 and "state size" in _lib.last_error()
     rc = lib.it_gdn_conv(fake, 8192, fake, fake, fake, 8192, 8192, 1, 5, None)
